@@ -1,0 +1,127 @@
+/*
+ * xtern — MI355X (gfx950) ternary linear-layer library, C ABI.
+ *
+ * This header is the drop-in boundary for xor-net's bit1_58 ternary linear
+ * path.  Every entry point is plain C: plain pointers and sizes, no exceptions
+ * cross it, every call returns an int status (XT_OK = 0, negative = error) and
+ * leaves a thread-local message readable with xt_last_error().
+ *
+ * Device pointers are HIP device pointers on the current device; `stream` is a
+ * hipStream_t passed as void* (NULL = the default stream).  All compute calls
+ * are asynchronous on `stream`; the library only synchronises inside
+ * xt_weights_create / xt_weights_destroy and when a workspace has to grow.
+ * Calls are thread-safe; calls on different streams may run concurrently.
+ *
+ * Reference paths below are relative to the xor-net source tree.
+ */
+#ifndef XTERN_H
+#define XTERN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum {
+    XT_OK = 0,
+    XT_ERR_INVALID = -1,     /* bad argument / shape (reference: anyhow::bail!) */
+    XT_ERR_HIP = -2,         /* a HIP runtime call failed */
+    XT_ERR_NOMEM = -3,       /* device or host allocation failed */
+    XT_ERR_UNSUPPORTED = -4  /* valid request this build does not handle */
+};
+
+/* Weight storage formats.  Values match the on-disk/host byte layouts the
+ * reference keeps:
+ *   XT_PACK4     TernaryPackType::Pack4, [out_dim][ceil(in_dim/4)] bytes,
+ *                2-bit codes 00=-1 01=0 10=+1 (11 reads as 0)
+ *                (src/bit1_58/quantization.rs:7-46)
+ *   XT_PACK5     TernaryPackType::Pack5, [out_dim][ceil(in_dim/5)] bytes,
+ *                base-3 digits 0=-1 1=0 2=+1, first weight least significant
+ *                (src/bit1_58/quantization.rs:48-91)
+ *   XT_XORSPARSE the XorSparse row blob: per row u32 num_blocks, then per
+ *                64-block u64 mask + ceil(popcount/8) set-order sign bytes
+ *                (src/bit1_58/sparse.rs:9-17, :61-86)                        */
+enum { XT_PACK4 = 0, XT_PACK5 = 1, XT_XORSPARSE = 2 };
+
+/* Activation rounding: which of the reference's two quantiser paths to
+ * reproduce bit for bit (src/bit1_58/quantization.rs:170-195).
+ *   XT_QUANT_AVX512  the path taken on AVX-512F hosts (:95-145): clamp then
+ *                    round half to even for the first floor(K/16)*16 lanes,
+ *                    round half away from zero for the tail.
+ *   XT_QUANT_SCALAR  the portable path (:179-194): round half away, clamp. */
+enum { XT_QUANT_AVX512 = 0, XT_QUANT_SCALAR = 1 };
+
+/* Opaque device-resident weights: the packed ternary matrix in the GPU tile
+ * layout plus the per-output-row f32 scales.  Owns its device memory.
+ * Replaces TernaryLinear { rep, in_dim, out_dim, pack_type, w_scales }
+ * (src/bit1_58/layers.rs:34-41, TernaryRep :23-27). */
+typedef struct xt_weights xt_weights;
+
+/* Library version string. */
+const char* xt_version(void);
+
+/* Message for the last failed call on this host thread ("" if none). */
+const char* xt_last_error(void);
+
+/* Upload packed weights.  `host_bytes`/`nbytes` hold the matrix in `fmt`'s
+ * host layout (see the enum above); `w_scales` holds out_dim floats (one per
+ * output row, as TernaryLinear::w_scales).  The bytes are repacked once into
+ * the device tile layout on the calling thread and copied to the current
+ * device.  Replaces DynamicLinear::new_ternary_direct
+ * (src/nn/dynamic_linear.rs:670-680), TernaryLinear::new_sparse_from_packed
+ * (src/bit1_58/layers.rs:183-210) and, for XT_XORSPARSE,
+ * SparseTernary::from_blob (src/bit1_58/sparse.rs:135-194). */
+int xt_weights_create(int fmt, int64_t in_dim, int64_t out_dim, const void* host_bytes,
+                      size_t nbytes, const float* w_scales, xt_weights** out);
+
+/* Free a handle (NULL is a no-op).  Waits for the device first. */
+int xt_weights_destroy(xt_weights* w);
+
+/* Shape / format / device-footprint queries. */
+int xt_weights_info(const xt_weights* w, int* fmt, int64_t* in_dim, int64_t* out_dim,
+                    size_t* device_bytes);
+
+/* Host-side repack into the device tile layout, exposed so the layout can be
+ * checked (or precomputed) without a GPU.  Writes xt_tile_bytes() bytes. */
+size_t xt_tile_bytes(int fmt, int64_t in_dim, int64_t out_dim);
+int xt_repack_host(int fmt, int64_t in_dim, int64_t out_dim, const void* host_bytes,
+                   size_t nbytes, void* tiles_out);
+
+/* Per-row absmax quantisation of x [M][K] f32 (device) into q [M][K] i8 and
+ * inv_scale [M] f32 (device).  Bit-exact with quantize_f32_to_i8
+ * (src/bit1_58/quantization.rs:170-195) in the selected rounding mode. */
+int xt_quantize_i8(const float* x, int64_t M, int64_t K, int8_t* q, float* inv_scale,
+                   int mode, void* stream);
+
+/* y[M][out_dim] = (f32)dot_i32(q[m], row o) * inv_scale[m] * w_scales[o]
+ * given already-quantised activations q [M][in_dim] i8 and inv_scale [M].
+ * `acc` (nullable, [M][out_dim] i32) receives the exact i32 dot products.
+ * Replaces TernaryLinear::forward_with_quantized (src/bit1_58/layers.rs:315-345)
+ * — which the reference only defines for one row — for any M. */
+int xt_ternary_linear_q(const xt_weights* w, const int8_t* q, const float* inv_scale,
+                        int64_t M, float* y, int32_t* acc, void* stream);
+
+/* Full forward: quantise x [M][in_dim] f32 per row (mode as above), then the
+ * ternary product, y [M][out_dim] f32.  Replaces TernaryLinear::forward
+ * (src/bit1_58/layers.rs:262-313) and DynamicLinear::forward's Ternary arm
+ * (src/nn/dynamic_linear.rs:625-633).  Uses a per-stream device workspace
+ * owned by the library. */
+int xt_ternary_linear_f32(const xt_weights* w, const float* x, int64_t M, float* y,
+                          int mode, void* stream);
+
+/* Several projections that share one input (same in_dim and format) in one
+ * launch: ys[p] [M][out_dim(p)] for p < n (n <= 4).  The input is quantised
+ * once.  Replaces TernaryLinear::fused_forward_qkv (src/bit1_58/layers.rs:347-424)
+ * and fused_forward_mlp (:426-486).  q/inv_scale variant: */
+int xt_ternary_linear_multi_q(const xt_weights* const* ws, int n, const int8_t* q,
+                              const float* inv_scale, int64_t M, float* const* ys,
+                              void* stream);
+int xt_ternary_linear_multi_f32(const xt_weights* const* ws, int n, const float* x,
+                                int64_t M, float* const* ys, int mode, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* XTERN_H */

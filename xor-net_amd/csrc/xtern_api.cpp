@@ -1,0 +1,309 @@
+// xtern C ABI (include/xtern.h): weight handles, per-stream workspaces,
+// argument checking and kernel dispatch.
+//
+// Error behaviour follows the reference layer (src/bit1_58/layers.rs:266-272,
+// :318-325): a shape mismatch is reported, never computed through; here it
+// is a negative status plus xt_last_error() instead of anyhow::bail!.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <map>
+#include <mutex>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "../../include/xtern.h"
+#include "xtern_internal.h"
+#include "xtern_layout.h"
+
+struct xt_weights {
+    int fmt;
+    int64_t K, N;
+    int64_t nch;        // tile chunks along K
+    uint8_t* tiles;     // device, tile_bytes()
+    float* ws;          // device, N floats
+    size_t tile_bytes;
+    int device;
+};
+
+namespace {
+
+thread_local std::string g_err;
+
+int fail(int code, const std::string& msg) {
+    g_err = msg;
+    return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+    return fail(XT_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+#define XT_HIP(call)                                    \
+    do {                                                \
+        hipError_t e_ = (call);                         \
+        if (e_ != hipSuccess) return hip_fail(e_, #call); \
+    } while (0)
+
+// Device workspace for the f32 entry points and for padded copies of
+// caller-provided activations, one per (device, stream).  Work on one stream
+// is ordered, so reusing its buffer across calls is race-free; growing it
+// waits for the stream first.
+struct Workspace {
+    void* ptr = nullptr;
+    size_t cap = 0;
+};
+std::mutex g_ws_mu;
+std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+
+int workspace(hipStream_t s, size_t bytes, void** out) {
+    int dev = 0;
+    XT_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(g_ws_mu);
+    Workspace& w = g_ws[std::make_pair(dev, s)];
+    if (w.cap < bytes) {
+        if (w.ptr) {
+            XT_HIP(hipStreamSynchronize(s));
+            XT_HIP(hipFree(w.ptr));
+            w.ptr = nullptr;
+            w.cap = 0;
+        }
+        size_t cap = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+        hipError_t e = hipMalloc(&w.ptr, cap);
+        if (e != hipSuccess) return fail(XT_ERR_NOMEM, std::string("workspace hipMalloc: ") + hipGetErrorString(e));
+        w.cap = cap;
+    }
+    *out = w.ptr;
+    return XT_OK;
+}
+
+inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+int check_weights(const xt_weights* w) {
+    if (!w) return fail(XT_ERR_INVALID, "weights handle is NULL");
+    return XT_OK;
+}
+
+// Shared tail of every product entry point: quantised activations (ldq with
+// zero padding up to nch*CH, 16-byte aligned) are ready; launch the product.
+int run_product(const xt_weights* const* ws, int n, const int8_t* q, int ldq, const float* inv,
+                const int32_t* rowsum, int64_t M, float* const* ys, int32_t* acc,
+                hipStream_t s) {
+    const int fmt = ws[0]->fmt;
+    int64_t ng_total = 0;
+    for (int p = 0; p < n; ++p) ng_total += (ws[p]->N + 15) / 16;
+    const xt::MMConfig cfg =
+        xt::choose_config(fmt, (int)M, ng_total * 16, (int)ws[0]->nch, rowsum != nullptr);
+    xt::MMArgs a;
+    memset(&a, 0, sizeof a);
+    int tiles = 0;
+    for (int p = 0; p < n; ++p) {
+        a.proj[p].tiles = ws[p]->tiles;
+        a.proj[p].ws = ws[p]->ws;
+        a.proj[p].y = ys[p];
+        a.proj[p].acc = (n == 1) ? acc : nullptr;
+        a.proj[p].N = (int)ws[p]->N;
+        a.proj[p].tile0 = tiles;
+        const int ng = (int)((ws[p]->N + 15) / 16);
+        tiles += (ng + cfg.nb - 1) / cfg.nb;
+    }
+    a.nproj = n;
+    a.q = q;
+    a.inv = inv;
+    a.rowsum = rowsum;
+    a.M = (int)M;
+    a.ldq = ldq;
+    a.nch = (int)ws[0]->nch;
+    if ((int64_t)(M + 16 * cfg.mb - 1) / (16 * cfg.mb) > 65535)
+        return fail(XT_ERR_UNSUPPORTED, "M too large for one launch");
+    hipError_t e = xt::launch_mm(fmt, cfg, a, tiles, s);
+    if (e != hipSuccess) return hip_fail(e, "ternary product launch");
+    return XT_OK;
+}
+
+int check_group(const xt_weights* const* ws, int n, const void* in, int64_t M, float* const* ys) {
+    if (!ws || n < 1 || n > 4) return fail(XT_ERR_INVALID, "need 1..4 weight handles");
+    for (int p = 0; p < n; ++p) {
+        if (check_weights(ws[p])) return XT_ERR_INVALID;
+        if (ws[p]->K != ws[0]->K || ws[p]->fmt != ws[0]->fmt)
+            return fail(XT_ERR_INVALID, "fused projections must share in_dim and format");
+        if (!ys || !ys[p]) return fail(XT_ERR_INVALID, "output pointer is NULL");
+    }
+    if (M < 0) return fail(XT_ERR_INVALID, "M must be >= 0");
+    if (M > 0 && !in) return fail(XT_ERR_INVALID, "input pointer is NULL");
+    if (M > (int64_t)1 << 24) return fail(XT_ERR_UNSUPPORTED, "M above 2^24 is not supported");
+    return XT_OK;
+}
+
+int linear_q(const xt_weights* const* ws, int n, const int8_t* q, const float* inv, int64_t M,
+             float* const* ys, int32_t* acc, hipStream_t s) {
+    if (int rc = check_group(ws, n, q, M, ys)) return rc;
+    if (M > 0 && !inv) return fail(XT_ERR_INVALID, "inv_scale pointer is NULL");
+    if (M == 0) return XT_OK;
+    const int64_t K = ws[0]->K;
+    const int64_t kpad = ws[0]->nch * xt::chunk_cols(ws[0]->fmt);
+    const xt::MMConfig probe = xt::choose_config(ws[0]->fmt, (int)M, 0, 0, true);
+    const bool need_rowsum = probe.mb > 1;
+    const bool direct = (kpad == K) && ((((uintptr_t)q) & 15) == 0);
+    if (direct && !need_rowsum)
+        return run_product(ws, n, q, (int)K, inv, nullptr, M, ys, acc, s);
+    // Padded copy and/or row sums in the workspace.
+    const size_t qbytes = direct ? 0 : align_up((size_t)M * kpad, 256);
+    void* wsp = nullptr;
+    if (int rc = workspace(s, qbytes + align_up((size_t)M * 4, 256), &wsp)) return rc;
+    int8_t* qpad = direct ? nullptr : static_cast<int8_t*>(wsp);
+    int32_t* rowsum = reinterpret_cast<int32_t*>(static_cast<char*>(wsp) + qbytes);
+    hipError_t e = xt::launch_rowsum(q, K, (int)M, (int)K, qpad, (int)kpad, rowsum, s);
+    if (e != hipSuccess) return hip_fail(e, "row-sum launch");
+    return run_product(ws, n, direct ? q : qpad, (int)(direct ? K : kpad), inv, rowsum, M, ys, acc,
+                       s);
+}
+
+int linear_f32(const xt_weights* const* ws, int n, const float* x, int64_t M, float* const* ys,
+               int mode, hipStream_t s) {
+    if (int rc = check_group(ws, n, x, M, ys)) return rc;
+    if (mode != XT_QUANT_AVX512 && mode != XT_QUANT_SCALAR)
+        return fail(XT_ERR_INVALID, "unknown quantisation mode");
+    if (M == 0) return XT_OK;
+    const int64_t K = ws[0]->K;
+    const int64_t kpad = ws[0]->nch * xt::chunk_cols(ws[0]->fmt);
+    const size_t qbytes = align_up((size_t)M * kpad, 256);
+    const size_t fbytes = align_up((size_t)M * 4, 256);
+    void* wsp = nullptr;
+    if (int rc = workspace(s, qbytes + 2 * fbytes, &wsp)) return rc;
+    int8_t* q = static_cast<int8_t*>(wsp);
+    float* inv = reinterpret_cast<float*>(static_cast<char*>(wsp) + qbytes);
+    int32_t* rowsum = reinterpret_cast<int32_t*>(static_cast<char*>(wsp) + qbytes + fbytes);
+    hipError_t e = xt::launch_quantize(x, K, (int)M, (int)K, q, (int)kpad, inv, rowsum, mode, s);
+    if (e != hipSuccess) return hip_fail(e, "quantize launch");
+    return run_product(ws, n, q, (int)kpad, inv, rowsum, M, ys, nullptr, s);
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* xt_version(void) { return "xtern 0.1 gfx950"; }
+
+const char* xt_last_error(void) { return g_err.c_str(); }
+
+size_t xt_tile_bytes(int fmt, int64_t in_dim, int64_t out_dim) {
+    if (in_dim <= 0 || out_dim <= 0 || fmt < 0 || fmt > 2) return 0;
+    return xt::tile_bytes(fmt, in_dim, out_dim);
+}
+
+int xt_repack_host(int fmt, int64_t in_dim, int64_t out_dim, const void* host_bytes,
+                   size_t nbytes, void* tiles_out) {
+    if (!host_bytes || !tiles_out) return fail(XT_ERR_INVALID, "NULL buffer");
+    std::string err;
+    if (xt::repack(fmt, in_dim, out_dim, host_bytes, nbytes, tiles_out, &err))
+        return fail(XT_ERR_INVALID, err);
+    return XT_OK;
+}
+
+int xt_weights_create(int fmt, int64_t in_dim, int64_t out_dim, const void* host_bytes,
+                      size_t nbytes, const float* w_scales, xt_weights** out) {
+    if (!out) return fail(XT_ERR_INVALID, "out is NULL");
+    *out = nullptr;
+    if (!host_bytes || !w_scales) return fail(XT_ERR_INVALID, "NULL weight bytes or w_scales");
+    if (fmt < 0 || fmt > 2) return fail(XT_ERR_INVALID, "unknown weight format");
+    if (in_dim <= 0 || out_dim <= 0) return fail(XT_ERR_INVALID, "in_dim and out_dim must be positive");
+    const size_t tb = xt::tile_bytes(fmt, in_dim, out_dim);
+    std::vector<uint8_t> host;
+    try {
+        host.resize(tb);
+    } catch (...) {
+        return fail(XT_ERR_NOMEM, "host repack buffer");
+    }
+    std::string err;
+    if (xt::repack(fmt, in_dim, out_dim, host_bytes, nbytes, host.data(), &err))
+        return fail(XT_ERR_INVALID, err);
+    xt_weights* w = new (std::nothrow) xt_weights();
+    if (!w) return fail(XT_ERR_NOMEM, "handle");
+    w->fmt = fmt;
+    w->K = in_dim;
+    w->N = out_dim;
+    w->nch = (in_dim + xt::chunk_cols(fmt) - 1) / xt::chunk_cols(fmt);
+    w->tile_bytes = tb;
+    hipError_t e = hipGetDevice(&w->device);
+    if (e == hipSuccess) e = hipMalloc(&w->tiles, tb);
+    if (e == hipSuccess) e = hipMalloc(&w->ws, (size_t)out_dim * sizeof(float));
+    if (e == hipSuccess) e = hipMemcpy(w->tiles, host.data(), tb, hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = hipMemcpy(w->ws, w_scales, (size_t)out_dim * sizeof(float), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        if (w->tiles) (void)hipFree(w->tiles);
+        if (w->ws) (void)hipFree(w->ws);
+        delete w;
+        return hip_fail(e, "weight upload");
+    }
+    *out = w;
+    return XT_OK;
+}
+
+int xt_weights_destroy(xt_weights* w) {
+    if (!w) return XT_OK;
+    int prev = 0;
+    hipError_t e = hipGetDevice(&prev);
+    if (e == hipSuccess && prev != w->device) e = hipSetDevice(w->device);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    hipError_t e1 = hipFree(w->tiles), e2 = hipFree(w->ws);
+    if (prev != w->device) (void)hipSetDevice(prev);
+    delete w;
+    if (e != hipSuccess) return hip_fail(e, "weights destroy");
+    if (e1 != hipSuccess) return hip_fail(e1, "weights destroy");
+    if (e2 != hipSuccess) return hip_fail(e2, "weights destroy");
+    return XT_OK;
+}
+
+int xt_weights_info(const xt_weights* w, int* fmt, int64_t* in_dim, int64_t* out_dim,
+                    size_t* device_bytes) {
+    if (check_weights(w)) return XT_ERR_INVALID;
+    if (fmt) *fmt = w->fmt;
+    if (in_dim) *in_dim = w->K;
+    if (out_dim) *out_dim = w->N;
+    if (device_bytes) *device_bytes = w->tile_bytes + (size_t)w->N * sizeof(float);
+    return XT_OK;
+}
+
+int xt_quantize_i8(const float* x, int64_t M, int64_t K, int8_t* q, float* inv_scale, int mode,
+                   void* stream) {
+    if (M < 0 || K <= 0) return fail(XT_ERR_INVALID, "need M >= 0 and K > 0");
+    if (K > (int64_t)1 << 30 || M > (int64_t)1 << 31) return fail(XT_ERR_UNSUPPORTED, "size too large");
+    if (mode != XT_QUANT_AVX512 && mode != XT_QUANT_SCALAR)
+        return fail(XT_ERR_INVALID, "unknown quantisation mode");
+    if (M == 0) return XT_OK;
+    if (!x || !q || !inv_scale) return fail(XT_ERR_INVALID, "NULL pointer");
+    hipError_t e = xt::launch_quantize(x, K, (int)M, (int)K, q, (int)K, inv_scale, nullptr, mode,
+                                       static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "quantize launch");
+    return XT_OK;
+}
+
+int xt_ternary_linear_q(const xt_weights* w, const int8_t* q, const float* inv_scale, int64_t M,
+                        float* y, int32_t* acc, void* stream) {
+    const xt_weights* ws[1] = {w};
+    float* ys[1] = {y};
+    return linear_q(ws, 1, q, inv_scale, M, ys, acc, static_cast<hipStream_t>(stream));
+}
+
+int xt_ternary_linear_f32(const xt_weights* w, const float* x, int64_t M, float* y, int mode,
+                          void* stream) {
+    const xt_weights* ws[1] = {w};
+    float* ys[1] = {y};
+    return linear_f32(ws, 1, x, M, ys, mode, static_cast<hipStream_t>(stream));
+}
+
+int xt_ternary_linear_multi_q(const xt_weights* const* ws, int n, const int8_t* q,
+                              const float* inv_scale, int64_t M, float* const* ys, void* stream) {
+    return linear_q(ws, n, q, inv_scale, M, ys, nullptr, static_cast<hipStream_t>(stream));
+}
+
+int xt_ternary_linear_multi_f32(const xt_weights* const* ws, int n, const float* x, int64_t M,
+                                float* const* ys, int mode, void* stream) {
+    return linear_f32(ws, n, x, M, ys, mode, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,61 @@
+// Internal declarations shared by the xtern host API and the HIP kernels.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace xt {
+
+// Device tile geometry.  A tile holds 16 output rows x CH input columns of
+// one matrix, 1024 bytes: 64 lanes x 16 bytes, one global_load_dwordx4 per
+// lane.  Lane l = 16*g + j serves output row j of the tile and, inside every
+// 64-wide MFMA k-step s, the 16 columns s*64 + g*16 .. +15.
+//   Pack4 tiles (also used for XorSparse): CH = 256, 4 k-steps, dword s of a
+//     lane holds the 16 codes of step s with the code of column 4*jj + d at
+//     bit 8*d + 2*jj, so (dword >> 2*jj) & 0x03030303 yields the codes of
+//     columns 4*jj .. 4*jj+3 in byte order.
+//   Pack5 tiles: CH = 320, 5 k-steps, byte b of a lane holds the trits of
+//     columns s*64 + g*16 + b for s = 0..4 as the fixed-point base-3 value
+//     e = ceil(v * 256 / 243), v = sum_s t_s * 3^(4-s); trit s is recovered by
+//     five rounds of y = 3*x, t = y >> 8, x = y & 255.
+// Codes are the weight plus one (0 = -1, 1 = 0, 2 = +1); padding holds code
+// 1.  The kernels multiply codes, not weights, and subtract the activation
+// row sum once at the end: sum_k a*(w+1) - sum_k a = sum_k a*w, exactly.
+constexpr int kTileBytes = 1024;
+inline int chunk_cols(int fmt) { return fmt == 1 ? 320 : 256; }
+
+// Up to four projections that share one input, in one launch.
+struct Proj {
+    const uint8_t* tiles;  // [NG][nch][64][16]
+    const float* ws;       // w_scales, [N]
+    float* y;              // [M][N]
+    int32_t* acc;          // optional [M][N] exact i32 dots
+    int N;
+    int tile0;             // first blockIdx.x of this projection
+};
+
+struct MMArgs {
+    Proj proj[4];
+    int nproj;
+    const int8_t* q;        // [M][ldq], zero beyond in_dim up to nch*CH
+    const float* inv;       // [M]
+    const int32_t* rowsum;  // [M] sum of q over the row, or null
+    int M;
+    int ldq;
+    int nch;                // chunks per row
+};
+
+struct MMConfig {
+    int mb, nb, waves;  // tokens per WG = 16*mb, rows per WG = 16*nb
+};
+
+// Kernel launchers (xtern_kernels.hip).  Return the hipError_t of the launch.
+hipError_t launch_quantize(const float* x, int64_t ldx, int M, int K, int8_t* q, int ldq,
+                           float* inv, int32_t* rowsum, int mode, hipStream_t s);
+hipError_t launch_rowsum(const int8_t* qin, int64_t ldin, int M, int K, int8_t* qout,
+                         int ldout, int32_t* rowsum, hipStream_t s);
+hipError_t launch_mm(int fmt, const MMConfig& cfg, const MMArgs& a, int ntiles_total,
+                     hipStream_t s);
+MMConfig choose_config(int fmt, int M, int64_t N_total, int nch, bool have_rowsum);
+
+}  // namespace xt

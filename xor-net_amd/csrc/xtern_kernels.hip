@@ -1,0 +1,375 @@
+// xtern HIP kernels for gfx950 (MI355X): activation quantiser and the
+// ternary x i8 product on MFMA.
+//
+// Reference behaviour these kernels reproduce (paths relative to xor-net):
+//   quantize_f32_to_i8          src/bit1_58/quantization.rs:95-195
+//   ternary_dot_product_pack4   src/bit1_58/simd.rs:256-382
+//   ternary_dot_product_pack5   src/bit1_58/simd.rs:384-414
+//   TernaryLinear::forward      src/bit1_58/layers.rs:262-345 (epilogue :294)
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/xtern.h"
+#include "xtern_internal.h"
+
+namespace xt {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// ---------------------------------------------------------------------------
+// Activation quantiser
+// ---------------------------------------------------------------------------
+
+// One element of quantize_f32_to_i8.  `main_lane` selects, in AVX-512 mode,
+// the vector body (quantization.rs:128-136: min/max clamp in MINPS/MAXPS
+// operand order, then CVTPS2DQ round-half-even, NaN -> 0) versus the scalar
+// tail (:138-142: round half away from zero, clamp, `as i8`).  Scalar mode is
+// :189-192 (round half away; Rust max/min send NaN to -127).
+__device__ __forceinline__ int quant_one(float x, float scale, int mode, bool main_lane) {
+    const float s = __fmul_rn(x, scale);
+    if (mode == XT_QUANT_AVX512) {
+        if (main_lane) {
+            float t = (127.0f < s) ? 127.0f : s;
+            t = (-127.0f > t) ? -127.0f : t;
+            return (t != t) ? 0 : (int)__builtin_rintf(t);
+        }
+        const float r = roundf(s);
+        const float c = (r > 127.0f) ? 127.0f : ((r < -127.0f) ? -127.0f : r);
+        return (c != c) ? 0 : (int)c;
+    }
+    float r = roundf(s);
+    if (r != r) return -127;
+    r = (r < -127.0f) ? -127.0f : r;
+    r = (r > 127.0f) ? 127.0f : r;
+    return (int)r;
+}
+
+template <typename T, typename Op>
+__device__ __forceinline__ T block_reduce(T v, Op op, T* smem) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = op(v, __shfl_xor(v, off, 64));
+    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    if ((threadIdx.x & 63) == 0) smem[wave] = v;
+    __syncthreads();
+    T r = smem[0];
+    for (int w = 1; w < nw; ++w) r = op(r, smem[w]);
+    __syncthreads();
+    return r;
+}
+
+struct MaxOp {
+    __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
+};
+struct AddOp {
+    __device__ int operator()(int a, int b) const { return a + b; }
+};
+
+// One workgroup per row.  Pass 1: absmax (fmaxf ignores NaN; NaN inputs are
+// off-contract).  Pass 2: quantise, write i8 (zero-filling [K, ldq)), and the
+// exact i32 row sum the product kernels subtract.
+__global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__ x, int64_t ldx,
+                                                       int K, int8_t* __restrict__ q, int ldq,
+                                                       float* __restrict__ inv,
+                                                       int32_t* __restrict__ rowsum, int mode) {
+    __shared__ float sm_f[4];
+    __shared__ int sm_i[4];
+    const int m = blockIdx.x;
+    const float* xr = x + (size_t)m * ldx;
+    int8_t* qr = q + (size_t)m * ldq;
+    const bool vec = ((K & 3) == 0) && ((((uintptr_t)xr) & 15) == 0);
+
+    float mx = 0.0f;
+    if (vec) {
+        const float4* x4 = reinterpret_cast<const float4*>(xr);
+        for (int i = threadIdx.x; i < (K >> 2); i += 256) {
+            const float4 v = x4[i];
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))));
+        }
+    } else {
+        for (int k = threadIdx.x; k < K; k += 256) mx = fmaxf(mx, fabsf(xr[k]));
+    }
+    mx = block_reduce(mx, MaxOp(), sm_f);
+    const float scale = (mx > 0.0f) ? __fdiv_rn(127.0f, mx) : 1.0f;
+    const float invs = (mx > 0.0f) ? __fdiv_rn(mx, 127.0f) : 1.0f;
+    const int kmain = (K / 16) * 16;
+
+    int sum = 0;
+    if (vec && (ldq & 3) == 0 && ((((uintptr_t)qr) & 3) == 0)) {
+        const float4* x4 = reinterpret_cast<const float4*>(xr);
+        for (int i = threadIdx.x; i < (ldq >> 2); i += 256) {
+            int b[4] = {0, 0, 0, 0};
+            if (4 * i < K) {
+                const float4 v = x4[i];
+                const float e[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) b[t] = quant_one(e[t], scale, mode, 4 * i + t < kmain);
+            }
+            sum += b[0] + b[1] + b[2] + b[3];
+            const uint32_t packed = (uint32_t)(b[0] & 255) | ((uint32_t)(b[1] & 255) << 8) |
+                                    ((uint32_t)(b[2] & 255) << 16) | ((uint32_t)(b[3] & 255) << 24);
+            reinterpret_cast<uint32_t*>(qr)[i] = packed;
+        }
+    } else {
+        for (int k = threadIdx.x; k < ldq; k += 256) {
+            const int v = (k < K) ? quant_one(xr[k], scale, mode, k < kmain) : 0;
+            qr[k] = (int8_t)v;
+            sum += v;
+        }
+    }
+    sum = block_reduce(sum, AddOp(), sm_i);
+    if (threadIdx.x == 0) {
+        inv[m] = invs;
+        if (rowsum) rowsum[m] = sum;
+    }
+}
+
+// Row sums of caller-provided i8 activations, optionally copying them into a
+// zero-padded buffer with a 16-byte aligned stride.
+__global__ __launch_bounds__(256) void rowsum_kernel(const int8_t* __restrict__ qin, int64_t ldin,
+                                                     int K, int8_t* __restrict__ qout, int ldout,
+                                                     int32_t* __restrict__ rowsum) {
+    __shared__ int sm_i[4];
+    const int m = blockIdx.x;
+    const int8_t* r = qin + (size_t)m * ldin;
+    int sum = 0;
+    const int lim = qout ? ldout : K;
+    for (int k = threadIdx.x; k < lim; k += 256) {
+        const int v = (k < K) ? (int)r[k] : 0;
+        sum += v;
+        if (qout) qout[(size_t)m * ldout + k] = (int8_t)v;
+    }
+    sum = block_reduce(sum, AddOp(), sm_i);
+    if (threadIdx.x == 0) rowsum[m] = sum;
+}
+
+hipError_t launch_quantize(const float* x, int64_t ldx, int M, int K, int8_t* q, int ldq,
+                           float* inv, int32_t* rowsum, int mode, hipStream_t s) {
+    if (M <= 0) return hipSuccess;
+    hipLaunchKernelGGL(quantize_kernel, dim3(M), dim3(256), 0, s, x, ldx, K, q, ldq, inv, rowsum,
+                       mode);
+    return hipGetLastError();
+}
+
+hipError_t launch_rowsum(const int8_t* qin, int64_t ldin, int M, int K, int8_t* qout, int ldout,
+                         int32_t* rowsum, hipStream_t s) {
+    if (M <= 0) return hipSuccess;
+    hipLaunchKernelGGL(rowsum_kernel, dim3(M), dim3(256), 0, s, qin, ldin, K, qout, ldout, rowsum);
+    return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Ternary x i8 product on MFMA
+// ---------------------------------------------------------------------------
+
+__device__ __forceinline__ v4i ld_stream(const uint8_t* p) {
+    return __builtin_nontemporal_load(reinterpret_cast<const v4i*>(p));
+}
+__device__ __forceinline__ v4i ld_cached(const int8_t* p) {
+    return *reinterpret_cast<const v4i*>(p);
+}
+
+// Pack4 tile dword -> four code dwords (columns 4jj..4jj+3 in byte order).
+__device__ __forceinline__ v4i decode4(int x) {
+    v4i b;
+    b[0] = x & 0x03030303;
+    b[1] = (x >> 2) & 0x03030303;
+    b[2] = (x >> 4) & 0x03030303;
+    b[3] = (x >> 6) & 0x03030303;
+    return b;
+}
+
+// One workgroup computes a (16*MB tokens) x (16*NB output rows) tile over the
+// full reduction dimension; its WAVES waves take interleaved chunks (split-K
+// inside the workgroup) and are summed through LDS.  PF chunks per wave are
+// loaded before any is consumed, to keep enough bytes in flight.
+// OWN_ROWSUM: the activation row sums come from an extra MFMA against an
+// all-ones B operand instead of the caller (MB == 1 only).
+template <int FMT, int MB, int NB, int WAVES, int PF, bool OWN_ROWSUM>
+__global__ __launch_bounds__(WAVES * 64) void mm_kernel(const MMArgs a) {
+    constexpr int STEPS = (FMT == XT_PACK5) ? 5 : 4;
+    constexpr int CH = STEPS * 64;
+    constexpr int NACC = MB * NB + (OWN_ROWSUM ? 1 : 0);
+    static_assert(!OWN_ROWSUM || MB == 1, "in-kernel row sums need MB == 1");
+    __shared__ v4i red[WAVES][NACC][64];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int g = lane >> 4;
+    const int j = lane & 15;
+
+    // Which projection this workgroup belongs to (constant-index selects keep
+    // the kernel-argument struct out of scratch memory).
+    const int bx = blockIdx.x;
+    const uint8_t* tiles = a.proj[0].tiles;
+    const float* ws = a.proj[0].ws;
+    float* y = a.proj[0].y;
+    int32_t* accout = a.proj[0].acc;
+    int N = a.proj[0].N;
+    int tile0 = 0;
+#pragma unroll
+    for (int p = 1; p < 4; ++p) {
+        if (p < a.nproj && bx >= a.proj[p].tile0) {
+            tiles = a.proj[p].tiles;
+            ws = a.proj[p].ws;
+            y = a.proj[p].y;
+            accout = a.proj[p].acc;
+            N = a.proj[p].N;
+            tile0 = a.proj[p].tile0;
+        }
+    }
+    const int ntile = bx - tile0;
+    const int NG = (N + 15) >> 4;
+    const int M = a.M;
+    const int mbase = blockIdx.y * (16 * MB);
+    const int nch = a.nch;
+    const int ldq = a.ldq;
+
+    v4i acc[MB][NB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) acc[mb][nb] = v4i{0, 0, 0, 0};
+    v4i accs = v4i{0, 0, 0, 0};
+    const v4i ones = v4i{0x01010101, 0x01010101, 0x01010101, 0x01010101};
+    const v4i zero = v4i{0, 0, 0, 0};
+
+    for (int c0 = wave; c0 < nch; c0 += WAVES * PF) {
+        v4i wv[PF][NB];
+        v4i av[PF][MB][STEPS];
+#pragma unroll
+        for (int pp = 0; pp < PF; ++pp) {
+            const int c = c0 + pp * WAVES;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                const int G = ntile * NB + nb;
+                wv[pp][nb] = (c < nch && G < NG)
+                                 ? ld_stream(tiles + ((size_t)(G * nch + c) * 64 + lane) * 16)
+                                 : zero;
+            }
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb) {
+                const int row = mbase + mb * 16 + j;
+#pragma unroll
+                for (int s = 0; s < STEPS; ++s)
+                    av[pp][mb][s] = (c < nch && row < M)
+                                        ? ld_cached(a.q + (size_t)row * ldq + c * CH + s * 64 + g * 16)
+                                        : zero;
+            }
+        }
+#pragma unroll
+        for (int pp = 0; pp < PF; ++pp) {
+            if (c0 + pp * WAVES >= nch) break;
+#pragma unroll
+            for (int nb = 0; nb < NB; ++nb) {
+                if constexpr (FMT == XT_PACK5) {
+                    int E[4], O[4];
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        E[d] = wv[pp][nb][d] & 0x00ff00ff;
+                        O[d] = ((unsigned)wv[pp][nb][d] >> 8) & 0x00ff00ff;
+                    }
+#pragma unroll
+                    for (int s = 0; s < STEPS; ++s) {
+                        v4i b;
+#pragma unroll
+                        for (int d = 0; d < 4; ++d) {
+                            const int pE = E[d] * 3, pO = O[d] * 3;
+                            b[d] = (int)__builtin_amdgcn_perm((unsigned)pO, (unsigned)pE, 0x07030501u);
+                            E[d] = pE & 0x00ff00ff;
+                            O[d] = pO & 0x00ff00ff;
+                        }
+#pragma unroll
+                        for (int mb = 0; mb < MB; ++mb)
+                            acc[mb][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[pp][mb][s], b,
+                                                                                 acc[mb][nb], 0, 0, 0);
+                        if constexpr (OWN_ROWSUM)
+                            if (nb == 0)
+                                accs = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[pp][0][s], ones,
+                                                                             accs, 0, 0, 0);
+                    }
+                } else {
+#pragma unroll
+                    for (int s = 0; s < STEPS; ++s) {
+                        const v4i b = decode4(wv[pp][nb][s]);
+#pragma unroll
+                        for (int mb = 0; mb < MB; ++mb)
+                            acc[mb][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[pp][mb][s], b,
+                                                                                 acc[mb][nb], 0, 0, 0);
+                        if constexpr (OWN_ROWSUM)
+                            if (nb == 0)
+                                accs = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[pp][0][s], ones,
+                                                                             accs, 0, 0, 0);
+                    }
+                }
+            }
+        }
+    }
+
+    // Split-K reduction through LDS: every wave parks all its accumulators,
+    // then wave w finishes blocks w, w + WAVES, ...
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NB; ++nb) red[wave][mb * NB + nb][lane] = acc[mb][nb];
+    if constexpr (OWN_ROWSUM) red[wave][NACC - 1][lane] = accs;
+    __syncthreads();
+
+    v4i rs = zero;
+    if constexpr (OWN_ROWSUM) {
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) rs += red[w][NACC - 1][lane];
+    }
+    for (int blk = wave; blk < MB * NB; blk += WAVES) {
+        const int mb = blk / NB, nb = blk % NB;
+        v4i sum = zero;
+#pragma unroll
+        for (int w = 0; w < WAVES; ++w) sum += red[w][blk][lane];
+        const int o = (ntile * NB + nb) * 16 + j;
+        if (o >= N) continue;
+        const float wscale = ws[o];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int i = mbase + mb * 16 + 4 * g + r;
+            if (i >= M) continue;
+            const int rsum = OWN_ROWSUM ? rs[r] : a.rowsum[i];
+            const int d = sum[r] - rsum;
+            // layers.rs:294 — (dot as f32 * inv_scale) * w_scale, two roundings.
+            y[(size_t)i * N + o] = __fmul_rn(__fmul_rn((float)d, a.inv[i]), wscale);
+            if (accout) accout[(size_t)i * N + o] = d;
+        }
+    }
+}
+
+template <int FMT, int MB, int NB, int W, int PF, bool OWN>
+static hipError_t launch_t(const MMArgs& a, int ntiles, hipStream_t s) {
+    dim3 grid(ntiles, (a.M + 16 * MB - 1) / (16 * MB));
+    hipLaunchKernelGGL((mm_kernel<FMT, MB, NB, W, PF, OWN>), grid, dim3(W * 64), 0, s, a);
+    return hipGetLastError();
+}
+
+MMConfig choose_config(int fmt, int M, int64_t N_total, int nch, bool have_rowsum) {
+    (void)fmt;
+    (void)N_total;
+    (void)nch;
+    if (M <= 16 || !have_rowsum) return MMConfig{1, 1, 4};
+    return MMConfig{4, 2, 4};
+}
+
+hipError_t launch_mm(int fmt, const MMConfig& cfg, const MMArgs& a, int ntiles_total,
+                     hipStream_t s) {
+    const bool own = (a.rowsum == nullptr);
+    if (cfg.mb == 1 && cfg.nb == 1 && cfg.waves == 4) {
+        if (fmt == XT_PACK5)
+            return own ? launch_t<XT_PACK5, 1, 1, 4, 2, true>(a, ntiles_total, s)
+                       : launch_t<XT_PACK5, 1, 1, 4, 2, false>(a, ntiles_total, s);
+        return own ? launch_t<XT_PACK4, 1, 1, 4, 2, true>(a, ntiles_total, s)
+                   : launch_t<XT_PACK4, 1, 1, 4, 2, false>(a, ntiles_total, s);
+    }
+    if (cfg.mb == 4 && cfg.nb == 2 && cfg.waves == 4 && !own) {
+        if (fmt == XT_PACK5) return launch_t<XT_PACK5, 4, 2, 4, 1, false>(a, (ntiles_total), s);
+        return launch_t<XT_PACK4, 4, 2, 4, 1, false>(a, ntiles_total, s);
+    }
+    return hipErrorInvalidValue;
+}
+
+}  // namespace xt

@@ -1,0 +1,180 @@
+// Host-side repack of the reference's weight byte layouts into the xtern
+// device tile layout (geometry documented in xtern_internal.h).
+//
+// Input formats (paths relative to xor-net):
+//   Pack4      src/bit1_58/quantization.rs:7-46   ([N][ceil(K/4)] bytes)
+//   Pack5      src/bit1_58/quantization.rs:48-91  ([N][ceil(K/5)] bytes)
+//   XorSparse  src/bit1_58/sparse.rs:9-17, :135-194 (row blobs)
+#include <string.h>
+
+#include <string>
+#include <vector>
+
+#include "xtern_layout.h"
+
+namespace xt {
+
+size_t tile_bytes(int fmt, int64_t K, int64_t N) {
+    const int64_t ch = chunk_cols(fmt);
+    const int64_t nch = (K + ch - 1) / ch;
+    const int64_t ng = (N + 15) / 16;
+    return (size_t)(ng * nch * kTileBytes);
+}
+
+namespace {
+
+// Place the code of (row o, column k) into a Pack4 tile buffer.
+inline void put4(uint8_t* tiles, int64_t nch, int64_t o, int64_t k, unsigned code) {
+    const int64_t G = o >> 4, j = o & 15;
+    const int64_t c = k >> 8, kk = k & 255;
+    const int64_t s = kk >> 6, g = (kk & 63) >> 4, b = kk & 15;
+    const int64_t jj = b >> 2, d = b & 3;
+    uint8_t* p = tiles + ((G * nch + c) * 64 + g * 16 + j) * 16 + s * 4 + d;
+    const int sh = (int)(2 * jj);
+    *p = (uint8_t)((*p & ~(3u << sh)) | (code << sh));
+}
+
+// Pack4 code of a reference byte field: 00 -> -1, 10 -> +1, 01 and 11 -> 0
+// (quantization.rs:36-41).  Canonical device code = weight + 1.
+inline unsigned canon4(unsigned field) { return field == 0 ? 0u : (field == 2 ? 2u : 1u); }
+
+int repack_pack4(int64_t K, int64_t N, const uint8_t* src, size_t nbytes, uint8_t* tiles,
+                 std::string* err) {
+    const int64_t bpr = (K + 3) / 4;
+    if ((uint64_t)nbytes < (uint64_t)(bpr * N)) {
+        *err = "Pack4 weights: expected " + std::to_string(bpr * N) + " bytes ([out_dim][ceil(in_dim/4)]), got " +
+               std::to_string(nbytes);
+        return -1;
+    }
+    const int64_t nch = (K + 255) / 256;
+    for (int64_t o = 0; o < N; ++o) {
+        const uint8_t* row = src + o * bpr;
+        for (int64_t k = 0; k < K; ++k)
+            put4(tiles, nch, o, k, canon4((row[k >> 2] >> (2 * (k & 3))) & 3u));
+    }
+    return 0;
+}
+
+// XorSparse row blobs -> Pack4 tiles (lossless; same weights as the dense
+// Pack4 encoding of the rows).
+int repack_sparse(int64_t K, int64_t N, const uint8_t* blob, size_t nbytes, uint8_t* tiles,
+                  std::string* err) {
+    const int64_t nch = (K + 255) / 256;
+    const int64_t want_nb = (K + 63) / 64;
+    size_t p = 0;
+    for (int64_t o = 0; o < N; ++o) {
+        if (p + 4 > nbytes) {
+            *err = "XorSparse blob truncated at row " + std::to_string(o);
+            return -1;
+        }
+        const uint32_t nb = (uint32_t)blob[p] | ((uint32_t)blob[p + 1] << 8) |
+                            ((uint32_t)blob[p + 2] << 16) | ((uint32_t)blob[p + 3] << 24);
+        p += 4;
+        if ((int64_t)nb != want_nb) {
+            *err = "XorSparse row " + std::to_string(o) + ": num_blocks " + std::to_string(nb) +
+                   " != ceil(in_dim/64) = " + std::to_string(want_nb);
+            return -1;
+        }
+        for (int64_t b = 0; b < want_nb; ++b) {
+            if (p + 8 > nbytes) {
+                *err = "XorSparse blob truncated at row " + std::to_string(o);
+                return -1;
+            }
+            uint64_t mask = 0;
+            for (int t = 0; t < 8; ++t) mask |= (uint64_t)blob[p + t] << (8 * t);
+            p += 8;
+            const int nnz = __builtin_popcountll(mask);
+            const size_t sbytes = (size_t)(nnz + 7) / 8;
+            if (p + sbytes > nbytes) {
+                *err = "XorSparse blob truncated at row " + std::to_string(o);
+                return -1;
+            }
+            if (b * 64 + 64 > K && (mask >> (K - b * 64)) != 0) {
+                *err = "XorSparse row " + std::to_string(o) + ": mask sets lanes beyond in_dim";
+                return -1;
+            }
+            uint64_t sb = 0;
+            for (size_t t = 0; t < sbytes; ++t) sb |= (uint64_t)blob[p + t] << (8 * t);
+            p += sbytes;
+            unsigned si = 0;
+            for (int lane = 0; lane < 64; ++lane) {
+                if (!((mask >> lane) & 1u)) continue;
+                const unsigned neg = (unsigned)((sb >> si) & 1u);
+                ++si;
+                put4(tiles, nch, o, b * 64 + lane, neg ? 0u : 2u);
+            }
+        }
+    }
+    return 0;
+}
+
+int repack_pack5(int64_t K, int64_t N, const uint8_t* src, size_t nbytes, uint8_t* tiles,
+                 std::string* err) {
+    const int64_t bpr = (K + 4) / 5;
+    if ((uint64_t)nbytes < (uint64_t)(bpr * N)) {
+        *err = "Pack5 weights: expected " + std::to_string(bpr * N) + " bytes ([out_dim][ceil(in_dim/5)]), got " +
+               std::to_string(nbytes);
+        return -1;
+    }
+    const int64_t nch = (K + 319) / 320;
+    const int64_t ng = (N + 15) / 16;
+    for (int64_t G = 0; G < ng; ++G) {
+        // trits (weight + 1) of the 16 rows of this group; 1 = padding
+        std::vector<uint8_t> rows((size_t)(16 * K), 1);
+        for (int64_t j = 0; j < 16; ++j) {
+            const int64_t o = G * 16 + j;
+            if (o >= N) break;
+            const uint8_t* row = src + o * bpr;
+            // quantization.rs:72-91 / simd.rs:388-414: repeated %3 and /3.
+            for (int64_t c = 0; c < bpr; ++c) {
+                unsigned b = row[c];
+                for (int t = 0; t < 5 && c * 5 + t < K; ++t) {
+                    rows[(size_t)(j * K + c * 5 + t)] = (uint8_t)(b % 3);
+                    b /= 3;
+                }
+            }
+        }
+        for (int64_t c = 0; c < nch; ++c) {
+            uint8_t* out = tiles + (G * nch + c) * kTileBytes;
+            for (int lane = 0; lane < 64; ++lane) {
+                const int g = lane >> 4, j = lane & 15;
+                for (int b = 0; b < 16; ++b) {
+                    unsigned v = 0;
+                    for (int s = 0; s < 5; ++s) {
+                        const int64_t k = c * 320 + s * 64 + g * 16 + b;
+                        const unsigned t = (k < K) ? rows[(size_t)(j * K + k)] : 1u;
+                        v = v * 3 + t;
+                    }
+                    out[lane * 16 + b] = (uint8_t)((v * 256 + 242) / 243);
+                }
+            }
+        }
+    }
+    return 0;
+}
+
+}  // namespace
+
+int repack(int fmt, int64_t K, int64_t N, const void* src, size_t nbytes, void* dst,
+           std::string* err) {
+    if (K <= 0 || N <= 0) {
+        *err = "in_dim and out_dim must be positive";
+        return -1;
+    }
+    if (K > (int64_t)1 << 30 || N > (int64_t)1 << 30) {
+        *err = "in_dim/out_dim above 2^30 are not supported";
+        return -1;
+    }
+    if (fmt != 0 && fmt != 1 && fmt != 2) {
+        *err = "unknown weight format " + std::to_string(fmt);
+        return -1;
+    }
+    const size_t tb = tile_bytes(fmt, K, N);
+    uint8_t* tiles = static_cast<uint8_t*>(dst);
+    if (fmt == 1) return repack_pack5(K, N, static_cast<const uint8_t*>(src), nbytes, tiles, err);
+    memset(tiles, 0x55, tb);  // code 1 (weight 0) in every 2-bit field
+    if (fmt == 0) return repack_pack4(K, N, static_cast<const uint8_t*>(src), nbytes, tiles, err);
+    return repack_sparse(K, N, static_cast<const uint8_t*>(src), nbytes, tiles, err);
+}
+
+}  // namespace xt

@@ -1,0 +1,347 @@
+"""xtern — Python mirror of xor-net's bit1_58 ternary linear API on MI355X.
+
+The compute path is libxtern.so (hand-written HIP for gfx950) reached through
+its C ABI (include/xtern.h) with ctypes.  PyTorch is only used for device
+memory and streams.  There is no CPU fallback: importing this package raises
+if libxtern.so is missing, and every compute call raises XternError on a
+failed status.
+
+Mirrored reference API (paths relative to xor-net):
+  TernaryPackType                 src/bit1_58/quantization.rs:1-5
+  pack_1_58bit_4pack / 5pack      src/bit1_58/quantization.rs:7-91
+  quantize_f32_to_i8              src/bit1_58/quantization.rs:170-195
+  encode_sparse_row_into /
+  encode_sparse_tensor            src/bit1_58/sparse.rs:61-103
+  TernaryLinear                   src/bit1_58/layers.rs:34-750
+  DynamicLinear (Ternary arm)     src/nn/dynamic_linear.rs:610-680
+"""
+import ctypes
+import enum
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libxtern.so")
+
+if not os.path.exists(LIB_PATH):
+    raise ImportError(
+        f"libxtern.so not found at {LIB_PATH}; build it with "
+        "`python xor-net_amd/build_lib.py` (or __graft_entry__.build())")
+
+_lib = ctypes.CDLL(LIB_PATH)
+
+XT_OK = 0
+XT_ERR_INVALID = -1
+XT_ERR_HIP = -2
+XT_ERR_NOMEM = -3
+XT_ERR_UNSUPPORTED = -4
+
+XT_PACK4, XT_PACK5, XT_XORSPARSE = 0, 1, 2
+XT_QUANT_AVX512, XT_QUANT_SCALAR = 0, 1
+
+_vp = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_sz = ctypes.c_size_t
+
+_lib.xt_version.restype = ctypes.c_char_p
+_lib.xt_last_error.restype = ctypes.c_char_p
+_lib.xt_weights_create.argtypes = [ctypes.c_int, _i64, _i64, _vp, _sz, _vp, ctypes.POINTER(_vp)]
+_lib.xt_weights_destroy.argtypes = [_vp]
+_lib.xt_weights_info.argtypes = [_vp, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(_i64),
+                                 ctypes.POINTER(_i64), ctypes.POINTER(_sz)]
+_lib.xt_tile_bytes.argtypes = [ctypes.c_int, _i64, _i64]
+_lib.xt_tile_bytes.restype = _sz
+_lib.xt_repack_host.argtypes = [ctypes.c_int, _i64, _i64, _vp, _sz, _vp]
+_lib.xt_quantize_i8.argtypes = [_vp, _i64, _i64, _vp, _vp, ctypes.c_int, _vp]
+_lib.xt_ternary_linear_q.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp, _vp]
+_lib.xt_ternary_linear_f32.argtypes = [_vp, _vp, _i64, _vp, ctypes.c_int, _vp]
+_lib.xt_ternary_linear_multi_q.argtypes = [_vp, ctypes.c_int, _vp, _vp, _i64, _vp, _vp]
+_lib.xt_ternary_linear_multi_f32.argtypes = [_vp, ctypes.c_int, _vp, _i64, _vp, ctypes.c_int, _vp]
+
+
+class XternError(RuntimeError):
+    """A libxtern call returned a negative status (message from xt_last_error)."""
+
+    def __init__(self, code, msg):
+        super().__init__(f"xtern error {code}: {msg}")
+        self.code = code
+
+
+def _check(rc):
+    if rc != XT_OK:
+        raise XternError(rc, _lib.xt_last_error().decode())
+
+
+def version():
+    return _lib.xt_version().decode()
+
+
+def lib():
+    """The loaded ctypes library (for tests of the raw ABI)."""
+    return _lib
+
+
+# ---------------------------------------------------------------------------
+# Formats and host-side codecs (load-time work, as in the reference)
+# ---------------------------------------------------------------------------
+
+class TernaryPackType(enum.Enum):
+    """quantization.rs:1-5."""
+    Pack4 = XT_PACK4
+    Pack5 = XT_PACK5
+
+
+def _ternarise(w, w_scale):
+    """Per-weight rule of quantization.rs:12-21: clamp(round_half_away(w/s), -1, 1),
+    then < -0.5 -> -1, > 0.5 -> +1, else 0; s <= 0 gives 0; NaN gives -1."""
+    w = np.asarray(w, dtype=np.float32)
+    if w_scale > 0:
+        scaled = (w / np.float32(w_scale)).astype(np.float32)
+    else:
+        scaled = np.zeros_like(w)
+    # Rust f32::round: half away from zero (trunc, then step on |frac| >= 0.5;
+    # both operations are exact in f32).
+    whole = np.trunc(scaled)
+    r = whole + np.where(np.abs(scaled - whole) >= 0.5, np.sign(scaled), 0).astype(np.float32)
+    q = np.where(np.isnan(scaled), np.float32(-1.0), np.clip(r, -1, 1))
+    return np.where(q < -0.5, -1, np.where(q > 0.5, 1, 0)).astype(np.int8)
+
+
+def pack_ternary4(t):
+    """Ternary values (int8 in {-1,0,1}, one row) -> Pack4 bytes (quantization.rs:7-27)."""
+    t = np.asarray(t, dtype=np.int8).ravel()
+    n = t.size
+    codes = np.where(t < 0, 0, np.where(t > 0, 2, 1)).astype(np.uint8)
+    padded = np.zeros(((n + 3) // 4) * 4, dtype=np.uint8)
+    padded[:n] = codes
+    g = padded.reshape(-1, 4)
+    return (g[:, 0] | (g[:, 1] << 2) | (g[:, 2] << 4) | (g[:, 3] << 6)).astype(np.uint8)
+
+
+def pack_ternary5(t):
+    """Ternary values -> Pack5 bytes (quantization.rs:48-70); a short last group
+    only sums the trits it has."""
+    t = np.asarray(t, dtype=np.int8).ravel()
+    n = t.size
+    digits = np.zeros(((n + 4) // 5) * 5, dtype=np.uint32)
+    digits[:n] = np.where(t < 0, 0, np.where(t > 0, 2, 1))
+    g = digits.reshape(-1, 5)
+    return (g[:, 0] + 3 * g[:, 1] + 9 * g[:, 2] + 27 * g[:, 3] + 81 * g[:, 4]).astype(np.uint8)
+
+
+def pack_1_58bit_4pack(weights, w_scale):
+    """quantization.rs:7-27."""
+    return pack_ternary4(_ternarise(weights, w_scale))
+
+
+def pack_1_58bit_5pack(weights, w_scale):
+    """quantization.rs:48-70."""
+    return pack_ternary5(_ternarise(weights, w_scale))
+
+
+def unpack_1_58bit_4pack(packed, n):
+    """quantization.rs:29-46 (code 11 reads as 0)."""
+    packed = np.asarray(packed, dtype=np.uint8)
+    codes = np.stack([(packed >> (2 * j)) & 3 for j in range(4)], axis=1).ravel()[:n]
+    return np.where(codes == 0, -1.0, np.where(codes == 2, 1.0, 0.0)).astype(np.float32)
+
+
+def unpack_1_58bit_5pack(packed, n):
+    """quantization.rs:72-91."""
+    b = np.asarray(packed, dtype=np.uint32)
+    digits = np.stack([(b // 3 ** j) % 3 for j in range(5)], axis=1).ravel()[:n]
+    return np.where(digits == 0, -1.0, np.where(digits == 2, 1.0, 0.0)).astype(np.float32)
+
+
+def encode_sparse_tensor(vals, in_dim, out_dim):
+    """[out_dim*in_dim] ternary -> (blob, row_offsets) (sparse.rs:61-103).
+
+    Per row: u32 num_blocks; per 64-block: u64 mask (bit i: lane i non-zero)
+    then ceil(nnz/8) bytes of set-order sign bits (bit j: j-th non-zero is -1),
+    all little-endian."""
+    v = np.asarray(vals, dtype=np.int8).reshape(out_dim, in_dim)
+    nb = (in_dim + 63) // 64
+    blk = np.zeros((out_dim, nb * 64), dtype=np.int8)
+    blk[:, :in_dim] = v
+    blk = blk.reshape(out_dim, nb, 64)
+    nz = blk != 0
+    lanes = np.arange(64, dtype=np.uint64)
+    mask = np.bitwise_or.reduce(np.where(nz, np.uint64(1) << lanes, np.uint64(0)), axis=2)
+    rank = (np.cumsum(nz, axis=2) - 1).astype(np.uint64)
+    sgn = np.bitwise_or.reduce(
+        np.where(nz & (blk < 0), np.uint64(1) << np.minimum(rank, np.uint64(63)), np.uint64(0)),
+        axis=2)
+    nsb = (nz.sum(axis=2) + 7) // 8                       # [out_dim, nb]
+    rec = 8 + nsb                                         # bytes per block record
+    row_len = 4 + rec.sum(axis=1)
+    row_off = np.concatenate([[0], np.cumsum(row_len)[:-1]]).astype(np.int64)
+    out = np.zeros(int(row_len.sum()), dtype=np.uint8)
+    hdr = np.frombuffer(np.uint32(nb).tobytes(), dtype=np.uint8)
+    out[row_off[:, None] + np.arange(4)] = hdr
+    blk_off = (row_off[:, None] + 4 +
+               np.concatenate([np.zeros((out_dim, 1), np.int64), np.cumsum(rec, axis=1)[:, :-1]],
+                              axis=1))                    # [out_dim, nb]
+    mbytes = mask.astype("<u8").view(np.uint8).reshape(out_dim, nb, 8)
+    out[blk_off[..., None] + np.arange(8)] = mbytes
+    sbytes = sgn.astype("<u8").view(np.uint8).reshape(out_dim, nb, 8)
+    keep = np.arange(8)[None, None, :] < nsb[..., None]
+    idx = blk_off[..., None] + 8 + np.arange(8)
+    out[idx[keep]] = sbytes[keep]
+    return out.tobytes(), [int(o) for o in row_off]
+
+
+def encode_sparse_row(vals, in_dim):
+    """One ternary row -> XorSparse row bytes (sparse.rs:61-86)."""
+    return encode_sparse_tensor(np.asarray(vals, dtype=np.int8)[:in_dim], in_dim, 1)[0]
+
+
+# ---------------------------------------------------------------------------
+# Device weights and raw entry points
+# ---------------------------------------------------------------------------
+
+def _torch():
+    import torch
+    return torch
+
+
+def _stream_ptr(stream=None):
+    torch = _torch()
+    s = stream if stream is not None else torch.cuda.current_stream()
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def _dev_ptr(t, dtype, what):
+    torch = _torch()
+    if not isinstance(t, torch.Tensor) or not t.is_cuda:
+        raise XternError(XT_ERR_INVALID, f"{what} must be a CUDA (HIP) tensor")
+    if t.dtype != dtype:
+        raise XternError(XT_ERR_INVALID, f"{what} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise XternError(XT_ERR_INVALID, f"{what} must be contiguous")
+    return ctypes.c_void_p(t.data_ptr())
+
+
+class DeviceWeights:
+    """Owns an xt_weights handle (device tiles + w_scales)."""
+
+    def __init__(self, fmt, in_dim, out_dim, host_bytes, w_scales):
+        buf = np.ascontiguousarray(np.frombuffer(bytes(host_bytes), dtype=np.uint8)
+                                   if isinstance(host_bytes, (bytes, bytearray))
+                                   else np.asarray(host_bytes, dtype=np.uint8))
+        ws = np.ascontiguousarray(np.asarray(w_scales, dtype=np.float32))
+        if ws.size != out_dim:
+            raise XternError(XT_ERR_INVALID, f"w_scales needs {out_dim} values, got {ws.size}")
+        h = ctypes.c_void_p()
+        _check(_lib.xt_weights_create(fmt, in_dim, out_dim, buf.ctypes.data_as(_vp), buf.size,
+                                      ws.ctypes.data_as(_vp), ctypes.byref(h)))
+        self.handle = h
+        self.fmt, self.in_dim, self.out_dim = fmt, in_dim, out_dim
+
+    def device_bytes(self):
+        nb = _sz()
+        _check(_lib.xt_weights_info(self.handle, None, None, None, ctypes.byref(nb)))
+        return nb.value
+
+    def close(self):
+        if self.handle:
+            _check(_lib.xt_weights_destroy(self.handle))
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def tile_bytes(fmt, in_dim, out_dim):
+    return _lib.xt_tile_bytes(fmt, in_dim, out_dim)
+
+
+def repack_host(fmt, in_dim, out_dim, host_bytes):
+    """Host repack into the device tile layout (no GPU needed)."""
+    src = np.ascontiguousarray(np.frombuffer(bytes(host_bytes), dtype=np.uint8))
+    out = np.zeros(tile_bytes(fmt, in_dim, out_dim), dtype=np.uint8)
+    _check(_lib.xt_repack_host(fmt, in_dim, out_dim, src.ctypes.data_as(_vp), src.size,
+                               out.ctypes.data_as(_vp)))
+    return out
+
+
+def quantize_i8(x, mode=XT_QUANT_AVX512, stream=None):
+    """Device quantize_f32_to_i8 over the rows of x [M, K] (or [K]).
+    Returns (q int8 [M, K], inv_scale f32 [M])."""
+    torch = _torch()
+    x2 = x.reshape(-1, x.shape[-1])
+    M, K = x2.shape
+    q = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    inv = torch.empty((M,), dtype=torch.float32, device=x.device)
+    _check(_lib.xt_quantize_i8(_dev_ptr(x2, torch.float32, "x"), M, K,
+                               _dev_ptr(q, torch.int8, "q"), _dev_ptr(inv, torch.float32, "inv"),
+                               mode, _stream_ptr(stream)))
+    return q, inv
+
+
+def linear_q(w, q, inv, acc=False, out=None, stream=None):
+    """y = dot(q, W) * inv * w_scales for q [M, K] int8, inv [M] f32."""
+    torch = _torch()
+    q2 = q.reshape(-1, q.shape[-1])
+    M = q2.shape[0]
+    if q2.shape[1] != w.in_dim:
+        raise XternError(XT_ERR_INVALID,
+                         f"Input dimension mismatch: expected {w.in_dim}, got {q2.shape[1]}")
+    y = out if out is not None else torch.empty((M, w.out_dim), dtype=torch.float32, device=q.device)
+    a = torch.empty((M, w.out_dim), dtype=torch.int32, device=q.device) if acc else None
+    _check(_lib.xt_ternary_linear_q(w.handle, _dev_ptr(q2, torch.int8, "q"),
+                                    _dev_ptr(inv, torch.float32, "inv_scale"), M,
+                                    _dev_ptr(y, torch.float32, "y"),
+                                    _dev_ptr(a, torch.int32, "acc") if acc else None,
+                                    _stream_ptr(stream)))
+    return (y, a) if acc else y
+
+
+def linear_f32(w, x, mode=XT_QUANT_AVX512, out=None, stream=None):
+    """Quantise rows of x [M, K] f32 and apply the ternary product."""
+    torch = _torch()
+    x2 = x.reshape(-1, x.shape[-1])
+    M = x2.shape[0]
+    if x2.shape[1] != w.in_dim:
+        raise XternError(XT_ERR_INVALID,
+                         f"Input dimension mismatch: expected {w.in_dim}, got {x2.shape[1]}")
+    y = out if out is not None else torch.empty((M, w.out_dim), dtype=torch.float32, device=x.device)
+    _check(_lib.xt_ternary_linear_f32(w.handle, _dev_ptr(x2, torch.float32, "x"), M,
+                                      _dev_ptr(y, torch.float32, "y"), mode, _stream_ptr(stream)))
+    return y
+
+
+def _multi(ws, ys):
+    n = len(ws)
+    harr = (_vp * n)(*[w.handle for w in ws])
+    yarr = (_vp * n)(*[ctypes.c_void_p(y.data_ptr()) for y in ys])
+    return harr, yarr
+
+
+def linear_multi_f32(ws, x, mode=XT_QUANT_AVX512, stream=None):
+    torch = _torch()
+    x2 = x.reshape(-1, x.shape[-1])
+    M = x2.shape[0]
+    ys = [torch.empty((M, w.out_dim), dtype=torch.float32, device=x.device) for w in ws]
+    harr, yarr = _multi(ws, ys)
+    _check(_lib.xt_ternary_linear_multi_f32(harr, len(ws), _dev_ptr(x2, torch.float32, "x"), M,
+                                            yarr, mode, _stream_ptr(stream)))
+    return ys
+
+
+def linear_multi_q(ws, q, inv, stream=None):
+    torch = _torch()
+    q2 = q.reshape(-1, q.shape[-1])
+    M = q2.shape[0]
+    ys = [torch.empty((M, w.out_dim), dtype=torch.float32, device=q.device) for w in ws]
+    harr, yarr = _multi(ws, ys)
+    _check(_lib.xt_ternary_linear_multi_q(harr, len(ws), _dev_ptr(q2, torch.int8, "q"),
+                                          _dev_ptr(inv, torch.float32, "inv_scale"), M, yarr,
+                                          _stream_ptr(stream)))
+    return ys
+
+
+from .layers import TernaryLinear, DynamicLinear, TernaryRep  # noqa: E402,F401
