@@ -1,0 +1,294 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X ternary linear path (libxtern) on one GPU.
+
+Default workload: Pack4 ternary GEMM at prefill size,
+M = 128 tokens, up projection (K=2560 -> N=6912) and down projection
+(K=6912 -> N=2560).  One step = TernaryLinear::forward of both matrices
+(f32 activations in HBM -> per-token absmax i8 quantisation -> ternary i8
+MFMA product -> f32 outputs).  Weights rotate over distinct device copies
+totalling more than 2x the 256 MB MALL, so every step streams its weights
+from HBM.  `value` is whole-job int8 TOPS (2*M*N*K per matrix / step time).
+
+Also reported, from the same process:
+  roofline     the product kernel (mm_kernel) alone: algorithmic ops per
+               launch / average launch duration from HIP events on the
+               launch stream, against the 5.0 POP/s dense int8 MFMA peak
+  gemv_m1      BASELINE configs[0] (Pack4 GEMV, M=1, K=2560, N=6912): GB/s of
+               algorithmic bytes against the 8 TB/s HBM peak
+  cpu_baseline the oracle's restatement of the reference CPU path (AVX-512
+               VNNI dot, min(nproc, 8) threads, per-token tasks) on a bounded
+               sample of the same workload
+
+    python bench.py [--steps K] [--warmup W] [--workload c1|c0|c2|c3|c4]
+                    [--no-cpu] [--copy-calibration]
+"""
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "xor-net_amd"))
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+MALL_BYTES = 256 << 20
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def tern_bytes(np, rng, N, K, fmt, p0=0.35):
+    import xtern
+    p = (1 - p0) / 2
+    t = rng.choice(np.array([-1, 0, 1], np.int8), size=(N, K), p=[p, p0, p])
+    if fmt == xtern.XT_PACK4:
+        codes = np.where(t < 0, 0, np.where(t > 0, 2, 1)).astype(np.uint8)
+        pad = (-K) % 4
+        if pad:
+            codes = np.concatenate([codes, np.ones((N, pad), np.uint8)], axis=1)
+        g = codes.reshape(N, -1, 4)
+        return (g[..., 0] | (g[..., 1] << 2) | (g[..., 2] << 4) | (g[..., 3] << 6)).astype(np.uint8).ravel(), t
+    if fmt == xtern.XT_PACK5:
+        return np.concatenate([xtern.pack_ternary5(r) for r in t]), t
+    return np.frombuffer(xtern.encode_sparse_tensor(t, K, N)[0], np.uint8), t
+
+
+def make_copies(np, xtern, fmt, K, N, wb, ws, min_total):
+    """Distinct device copies of one matrix, >= min_total bytes together."""
+    one = xtern.tile_bytes(fmt, K, N)
+    n = max(1, -(-min_total // one))
+    return [xtern.DeviceWeights(fmt, K, N, wb, ws) for _ in range(n)]
+
+
+def workload_c1(np, torch, xtern, rng):
+    M = 128
+    mats = [("up", 2560, 6912), ("down", 6912, 2560)]
+    per = max(2 * MALL_BYTES // len(mats), 1)
+    sets = []
+    for name, K, N in mats:
+        wb, _ = tern_bytes(np, rng, N, K, xtern.XT_PACK4)
+        ws = np.full(N, 0.8, np.float32)
+        copies = make_copies(np, xtern, xtern.XT_PACK4, K, N, wb, ws, per)
+        x = rng.standard_normal((M, K)).astype(np.float32)
+        x[rng.random((M, K)) < 0.01] *= 20          # 1% outliers x20
+        xd = torch.from_numpy(x).cuda()
+        y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+        sets.append(dict(name=name, K=K, N=N, copies=copies, x=xd, y=y, xh=x, wb=wb, ws=ws))
+    ops_per_step = sum(2 * M * s["N"] * s["K"] for s in sets)
+    return dict(M=M, sets=sets, ops=ops_per_step, fmt=xtern.XT_PACK4,
+                config={"workload": "c1_pack4_gemm_m128", "M": M,
+                        "matrices": [[s["K"], s["N"]] for s in sets],
+                        "weight_copies": [len(s["copies"]) for s in sets]})
+
+
+def run_steps(xtern, wl, steps, start_idx=0):
+    for i in range(steps):
+        for s in wl["sets"]:
+            w = s["copies"][(start_idx + i) % len(s["copies"])]
+            xtern.linear_f32(w, s["x"], out=s["y"])
+
+
+class Graph:
+    """A HIP graph of `fn(i)` for i in range(n), captured on its own stream
+    after one eager warm-up pass on that stream (workspaces are allocated
+    outside capture).  Replays launch the recorded kernels back to back."""
+
+    def __init__(self, torch, fn, n):
+        self.torch = torch
+        self.stream = torch.cuda.Stream()
+        with torch.cuda.stream(self.stream):
+            for i in range(n):
+                fn(i)
+        self.stream.synchronize()
+        self.g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.g, stream=self.stream):
+            for i in range(n):
+                fn(i)
+        self.n = n
+
+    def time_ms(self, replays):
+        """Average ms per captured call over `replays` replays (HIP events on
+        the replay stream)."""
+        torch = self.torch
+        with torch.cuda.stream(self.stream):
+            self.g.replay()
+            a = torch.cuda.Event(enable_timing=True)
+            b = torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(replays):
+                self.g.replay()
+            b.record()
+        b.synchronize()
+        return a.elapsed_time(b) / (replays * self.n)
+
+
+def product_only(np, torch, xtern, wl, reps):
+    """Average duration of one product launch (mm_kernel) per matrix: a HIP
+    graph of back-to-back linear_q_rowsum launches over the rotating copies,
+    timed with events on the graph's stream."""
+    out = []
+    for s in wl["sets"]:
+        q, inv, rs = xtern.quantize_i8_rowsum(s["x"])
+        torch.cuda.synchronize()
+        n = len(s["copies"])
+        g = Graph(torch, lambda i, s=s, q=q, inv=inv, rs=rs:
+                  xtern.linear_q_rowsum(s["copies"][i], q, inv, rs, out=s["y"]), n)
+        out.append(g.time_ms(max(1, reps // n)))
+    return out
+
+
+def gemv_m1(np, torch, xtern, rng, reps=400):
+    """Pack4 GEMV M=1 (K=2560, N=6912), rotating copies
+    in a HIP graph; bytes = packed weights + M*K i8 + 4*M inv + 4*N w_scales
+    + 4*M*N f32 out (the product launch given q, as the metric's GEMV)."""
+    K, N, M = 2560, 6912, 1
+    wb, _ = tern_bytes(np, rng, N, K, xtern.XT_PACK4)
+    ws = np.full(N, 0.8, np.float32)
+    copies = make_copies(np, xtern, xtern.XT_PACK4, K, N, wb, ws, 2 * MALL_BYTES)
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).cuda()
+    q, inv = xtern.quantize_i8(x)
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    y2 = torch.empty_like(y)
+    torch.cuda.synchronize()
+    n = len(copies)
+    g = Graph(torch, lambda i: xtern.linear_q(copies[i], q, inv, out=y), n)
+    ms = g.time_ms(max(1, reps // n))
+    gf = Graph(torch, lambda i: xtern.linear_f32(copies[i], x, out=y2), n)
+    fwd_ms = gf.time_ms(max(1, reps // n))
+    wbytes = N * ((K + 3) // 4)
+    alg = wbytes + M * K + 4 * M + 4 * N + 4 * M * N
+    gbs = alg / (ms * 1e-3) / 1e9
+    fwd_alg = wbytes + 4 * M * K + 4 * N + 4 * M * N
+    return {"workload": "c0_pack4_gemv_m1", "K": K, "N": N, "M": M,
+            "us_per_call_product": round(ms * 1e3, 3),
+            "us_per_call_forward_f32": round(fwd_ms * 1e3, 3),
+            "forward_f32_GBs": round(fwd_alg / (fwd_ms * 1e-3) / 1e9, 1),
+            "alg_bytes_per_call": alg,
+            "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+            "weight_copies": len(copies)}
+
+
+def cpu_baseline(np, wl, budget_s=12.0):
+    """The oracle's restatement of the reference CPU path (TernaryLinear::forward
+    with the VNNI dot when the host has it) on the first `rows` tokens of each
+    matrix of the step, repeated until ~budget_s of CPU time."""
+    sys.path.insert(0, os.path.join(ROOT, "oracle"))
+    import oracle
+    threads = min(os.cpu_count() or 1, 8)
+    kernel = 1 if oracle.has_vnni() else 0
+    rows = 16  # tokens per sample: one per-token task each, as layers.rs:298-310
+    ops = 0
+    t_total = 0.0
+    reps = 0
+    while t_total < budget_s:
+        for s in wl["sets"]:
+            x = s["xh"][:rows]
+            t0 = time.perf_counter()
+            oracle.linear_forward(0, s["K"], s["N"], x, s["ws"], wbytes=s["wb"],
+                                  threads=threads, kernel=kernel)
+            t_total += time.perf_counter() - t0
+            ops += 2 * rows * s["N"] * s["K"]
+        reps += 1
+    tops = ops / t_total / 1e12
+    return {"value": round(tops, 5), "unit": "TOPS (int8)", "cores": threads,
+            "kind": "port",
+            "sample": f"{reps} passes x {rows} tokens of each c1 matrix "
+                      f"({t_total:.1f} s), isa={'avx512-vnni' if kernel else 'scalar'}"}
+
+
+def copy_calibration(torch):
+    """A plain device copy of known size, for scaling rocprof FETCH/WRITE_SIZE."""
+    n = 256 << 20
+    a = torch.empty(n, dtype=torch.uint8, device="cuda").fill_(1)
+    b = torch.empty_like(a)
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes": n, "launches": 3}))
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=600)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="c1")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-extra", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
+              f"got --gpus {args.gpus}", file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+    import xtern
+
+    if args.copy_calibration:
+        copy_calibration(torch)
+        return
+    rng = np.random.default_rng(1234)
+    if args.workload != "c1":
+        raise SystemExit("only the c1 workload is wired as the headline step")
+    log("setting up c1 weights (rotating copies) ...")
+    wl = workload_c1(np, torch, xtern, rng)
+
+    # eager reference outputs, then the step graph (one step per weight copy)
+    run_steps(xtern, wl, 1)
+    torch.cuda.synchronize()
+    eager = [s["y"].clone() for s in wl["sets"]]
+    ncopy = len(wl["sets"][0]["copies"])
+    step_graph = Graph(torch, lambda i: run_steps(xtern, wl, 1, start_idx=i), ncopy)
+    replays = max(1, -(-args.steps // ncopy))
+    warm = max(1, -(-args.warmup // ncopy))
+    for _ in range(warm):
+        step_graph.g.replay()
+    step_graph.stream.synchronize()
+    # the last captured step used copy ncopy-1; recompute it eagerly to compare
+    run_steps(xtern, wl, 1, start_idx=ncopy - 1)
+    torch.cuda.synchronize()
+    check = [s["y"].clone() for s in wl["sets"]]
+    step_graph.g.replay()
+    step_graph.stream.synchronize()
+    for s, c in zip(wl["sets"], check):
+        if not torch.equal(s["y"], c):
+            raise SystemExit("graph replay output differs from eager output")
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    ms_step = step_graph.time_ms(replays)
+    wall = time.perf_counter() - t0
+    steps_timed = replays * ncopy
+    tops = wl["ops"] / (ms_step * 1e-3) / 1e12
+    log(f"step {ms_step * 1e3:.2f} us over {steps_timed} steps (wall {wall:.3f} s)")
+
+    prod_ms = product_only(np, torch, xtern, wl, reps=max(args.steps, 50))
+    prod_ops = [2 * wl["M"] * s["N"] * s["K"] for s in wl["sets"]]
+    ach = sum(prod_ops) / (sum(prod_ms) * 1e-3) / 1e12
+    roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": INT8_PEAK_TOPS,
+            "unit": "TFLOP/s", "frac": round(ach / INT8_PEAK_TOPS, 4), "traffic": None,
+            "kernel": "mm_kernel (ternary x i8 MFMA product)",
+            "us_per_launch": {s["name"]: round(m * 1e3, 3) for s, m in zip(wl["sets"], prod_ms)}}
+
+    out = {"metric": "ternary GEMM int8 TOPS at M=128 (Pack4, BitNet-2B up+down)",
+           "value": round(tops, 3), "unit": "TOPS", "n_gpus": 1, "steps": steps_timed,
+           "warmup": args.warmup, "ms_per_step": round(ms_step, 6), "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "i8 x ternary -> i32, f32 io",
+           "data": "synthetic (seeded ternary weights P(0)=0.35, N(0,1) activations, 1% x20)",
+           "config": wl["config"], "roofline": roof}
+    if not args.no_extra:
+        log("c0 gemv ...")
+        out["gemv_m1"] = gemv_m1(np, torch, xtern, rng)
+    if not args.no_cpu:
+        log("cpu baseline ...")
+        out["cpu_baseline"] = cpu_baseline(np, wl)
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -95,6 +95,12 @@ int xt_repack_host(int fmt, int64_t in_dim, int64_t out_dim, const void* host_by
 int xt_quantize_i8(const float* x, int64_t M, int64_t K, int8_t* q, float* inv_scale,
                    int mode, void* stream);
 
+/* xt_quantize_i8 that also writes rowsum [M] i32 = sum_k q[m][k] (nullable).
+ * No reference counterpart: the row sums let xt_ternary_linear_q_rowsum skip
+ * its own summing pass when one quantised input feeds several products. */
+int xt_quantize_i8_rowsum(const float* x, int64_t M, int64_t K, int8_t* q, float* inv_scale,
+                          int32_t* rowsum, int mode, void* stream);
+
 /* y[M][out_dim] = (f32)dot_i32(q[m], row o) * inv_scale[m] * w_scales[o]
  * given already-quantised activations q [M][in_dim] i8 and inv_scale [M].
  * `acc` (nullable, [M][out_dim] i32) receives the exact i32 dot products.
@@ -102,6 +108,13 @@ int xt_quantize_i8(const float* x, int64_t M, int64_t K, int8_t* q, float* inv_s
  * — which the reference only defines for one row — for any M. */
 int xt_ternary_linear_q(const xt_weights* w, const int8_t* q, const float* inv_scale,
                         int64_t M, float* y, int32_t* acc, void* stream);
+
+/* xt_ternary_linear_q with caller-provided exact row sums of q (from
+ * xt_quantize_i8_rowsum).  No reference counterpart; a wrong rowsum gives
+ * wrong outputs (it is subtracted from the code-domain dot product). */
+int xt_ternary_linear_q_rowsum(const xt_weights* w, const int8_t* q, const float* inv_scale,
+                               const int32_t* rowsum, int64_t M, float* y, int32_t* acc,
+                               void* stream);
 
 /* Full forward: quantise x [M][in_dim] f32 per row (mode as above), then the
  * ternary product, y [M][out_dim] f32.  Replaces TernaryLinear::forward

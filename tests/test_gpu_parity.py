@@ -348,3 +348,60 @@ def test_forward_with_quantized_and_fused():
     assert torch.equal(a, qkv[0]) and torch.equal(b, qkv[1])
     dl = xtern.DynamicLinear(lins[0])
     assert torch.equal(dl.forward(x), qkv[0])
+
+
+# ------------------------------------------------------------ HIP graphs ---
+
+@pytest.mark.parametrize("M", [1, 8, 128])
+def test_graph_replay_matches_eager(M):
+    """Captured linear_f32 launches (including split-K shapes, whose workspace
+    the kernels clear themselves) replay to the eager result every time, with
+    eager work on another stream between replays."""
+    log(f"graph replay M={M}")
+    rng = np.random.default_rng(20 + M)
+    mats = [(2560, 640), (6912, 2560), (2560, 6912)]
+    ws = [xtern.DeviceWeights(xtern.XT_PACK4, K, N,
+                              make_bytes(tern(rng, N, K), xtern.XT_PACK4),
+                              np.full(N, 0.7, np.float32)) for K, N in mats]
+    xs = [torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).to(DEV)
+          for K, _ in mats]
+    ys = [torch.empty((M, N), device=DEV) for _, N in mats]
+    eager = [xtern.linear_f32(w, x) for w, x in zip(ws, xs)]
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        for w, x, y in zip(ws, xs, ys):
+            xtern.linear_f32(w, x, out=y)
+    s.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        for w, x, y in zip(ws, xs, ys):
+            xtern.linear_f32(w, x, out=y)
+    for rep in range(4):
+        for y in ys:
+            y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        for y, e in zip(ys, eager):
+            assert torch.equal(y, e), f"replay {rep} differs"
+        # eager work in between, on the default stream
+        assert torch.equal(xtern.linear_f32(ws[1], xs[1]), eager[1])
+
+
+def test_splitk_workspace_alternating_shapes():
+    """Split-K shapes of different sizes on one stream, interleaved, stay exact
+    (each launch must leave the shared zeroed workspace clean)."""
+    rng = np.random.default_rng(30)
+    cases = [(2560, 640, 1), (6912, 2560, 128), (2560, 640, 16), (6912, 2560, 33), (4096, 160, 3)]
+    prepared = []
+    for K, N, M in cases:
+        t = tern(rng, N, K)
+        w = xtern.DeviceWeights(xtern.XT_PACK4, K, N, make_bytes(t, xtern.XT_PACK4),
+                                np.ones(N, np.float32))
+        q = rng.integers(-127, 128, (M, K)).astype(np.int8)
+        prepared.append((w, torch.from_numpy(q).to(DEV), exact_acc(t, q)))
+    for rnd in range(3):
+        for (K, N, M), (w, q, ref) in zip(cases, prepared):
+            log(f"alternating round={rnd} K={K} N={N} M={M}")
+            _, acc = xtern.linear_q(w, q, torch.ones(M, device=DEV), acc=True)
+            assert np.array_equal(acc.cpu().numpy(), ref)

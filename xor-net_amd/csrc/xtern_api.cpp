@@ -11,6 +11,7 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <tuple>
 #include <utility>
 #include <vector>
 
@@ -47,22 +48,26 @@ int hip_fail(hipError_t e, const char* what) {
         if (e_ != hipSuccess) return hip_fail(e_, #call); \
     } while (0)
 
-// Device workspace for the f32 entry points and for padded copies of
-// caller-provided activations, one per (device, stream).  Work on one stream
-// is ordered, so reusing its buffer across calls is race-free; growing it
+// Device workspaces, one per (device, stream, kind).  Work on one stream is
+// ordered, so reusing a buffer across calls on it is race-free; growing one
 // waits for the stream first.
+//   kind 0: quantised activations, inv scales and row sums of the f32 entry
+//           points, padded copies of caller activations;
+//   kind 1: split-K partial sums and arrival counters.  Zeroed when
+//           allocated; every product launch leaves it zero again (the last
+//           workgroup of a tile clears what it read).
 struct Workspace {
     void* ptr = nullptr;
     size_t cap = 0;
 };
 std::mutex g_ws_mu;
-std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+std::map<std::tuple<int, hipStream_t, int>, Workspace> g_ws;
 
-int workspace(hipStream_t s, size_t bytes, void** out) {
+int workspace(hipStream_t s, size_t bytes, void** out, int kind = 0) {
     int dev = 0;
     XT_HIP(hipGetDevice(&dev));
     std::lock_guard<std::mutex> lk(g_ws_mu);
-    Workspace& w = g_ws[std::make_pair(dev, s)];
+    Workspace& w = g_ws[std::make_tuple(dev, s, kind)];
     if (w.cap < bytes) {
         if (w.ptr) {
             XT_HIP(hipStreamSynchronize(s));
@@ -74,6 +79,10 @@ int workspace(hipStream_t s, size_t bytes, void** out) {
         hipError_t e = hipMalloc(&w.ptr, cap);
         if (e != hipSuccess) return fail(XT_ERR_NOMEM, std::string("workspace hipMalloc: ") + hipGetErrorString(e));
         w.cap = cap;
+        if (kind == 1) {
+            e = hipMemsetAsync(w.ptr, 0, cap, s);
+            if (e != hipSuccess) return hip_fail(e, "workspace clear");
+        }
     }
     *out = w.ptr;
     return XT_OK;
@@ -92,22 +101,24 @@ int run_product(const xt_weights* const* ws, int n, const int8_t* q, int ldq, co
                 const int32_t* rowsum, int64_t M, float* const* ys, int32_t* acc,
                 hipStream_t s) {
     const int fmt = ws[0]->fmt;
-    int64_t ng_total = 0;
-    for (int p = 0; p < n; ++p) ng_total += (ws[p]->N + 15) / 16;
+    int ng_total = 0;
+    for (int p = 0; p < n; ++p) ng_total += (int)((ws[p]->N + 15) / 16);
     const xt::MMConfig cfg =
-        xt::choose_config(fmt, (int)M, ng_total * 16, (int)ws[0]->nch, rowsum != nullptr);
+        xt::choose_config(fmt, (int)M, ng_total, (int)ws[0]->nch, rowsum != nullptr);
     xt::MMArgs a;
     memset(&a, 0, sizeof a);
-    int tiles = 0;
+    int tiles = 0, cols = 0;
     for (int p = 0; p < n; ++p) {
+        const int ng = (int)((ws[p]->N + 15) / 16);
         a.proj[p].tiles = ws[p]->tiles;
         a.proj[p].ws = ws[p]->ws;
         a.proj[p].y = ys[p];
         a.proj[p].acc = (n == 1) ? acc : nullptr;
         a.proj[p].N = (int)ws[p]->N;
         a.proj[p].tile0 = tiles;
-        const int ng = (int)((ws[p]->N + 15) / 16);
+        a.proj[p].col0 = cols;
         tiles += (ng + cfg.nb - 1) / cfg.nb;
+        cols += ng * 16;
     }
     a.nproj = n;
     a.q = q;
@@ -116,8 +127,18 @@ int run_product(const xt_weights* const* ws, int n, const int8_t* q, int ldq, co
     a.M = (int)M;
     a.ldq = ldq;
     a.nch = (int)ws[0]->nch;
-    if ((int64_t)(M + 16 * cfg.mb - 1) / (16 * cfg.mb) > 65535)
-        return fail(XT_ERR_UNSUPPORTED, "M too large for one launch");
+    a.cps = (a.nch + cfg.splitk - 1) / cfg.splitk;
+    const int64_t gy = (M + 16 * cfg.mb - 1) / (16 * cfg.mb);
+    if (gy > 65535) return fail(XT_ERR_UNSUPPORTED, "M too large for one launch");
+    if (cfg.splitk > 1) {
+        const size_t pbytes = align_up((size_t)M * cols * sizeof(int32_t), 256);
+        const size_t cbytes = align_up((size_t)tiles * gy * sizeof(unsigned), 256);
+        void* wsp = nullptr;
+        if (int rc = workspace(s, pbytes + cbytes, &wsp, 1)) return rc;
+        a.part = static_cast<int32_t*>(wsp);
+        a.ldp = cols;
+        a.cnt = reinterpret_cast<unsigned*>(static_cast<char*>(wsp) + pbytes);
+    }
     hipError_t e = xt::launch_mm(fmt, cfg, a, tiles, s);
     if (e != hipSuccess) return hip_fail(e, "ternary product launch");
     return XT_OK;
@@ -129,7 +150,7 @@ int check_group(const xt_weights* const* ws, int n, const void* in, int64_t M, f
         if (check_weights(ws[p])) return XT_ERR_INVALID;
         if (ws[p]->K != ws[0]->K || ws[p]->fmt != ws[0]->fmt)
             return fail(XT_ERR_INVALID, "fused projections must share in_dim and format");
-        if (!ys || !ys[p]) return fail(XT_ERR_INVALID, "output pointer is NULL");
+        if (M > 0 && (!ys || !ys[p])) return fail(XT_ERR_INVALID, "output pointer is NULL");
     }
     if (M < 0) return fail(XT_ERR_INVALID, "M must be >= 0");
     if (M > 0 && !in) return fail(XT_ERR_INVALID, "input pointer is NULL");
@@ -137,8 +158,9 @@ int check_group(const xt_weights* const* ws, int n, const void* in, int64_t M, f
     return XT_OK;
 }
 
-int linear_q(const xt_weights* const* ws, int n, const int8_t* q, const float* inv, int64_t M,
-             float* const* ys, int32_t* acc, hipStream_t s) {
+int linear_q(const xt_weights* const* ws, int n, const int8_t* q, const float* inv,
+             const int32_t* user_rowsum, int64_t M, float* const* ys, int32_t* acc,
+             hipStream_t s) {
     if (int rc = check_group(ws, n, q, M, ys)) return rc;
     if (M > 0 && !inv) return fail(XT_ERR_INVALID, "inv_scale pointer is NULL");
     if (M == 0) return XT_OK;
@@ -147,6 +169,8 @@ int linear_q(const xt_weights* const* ws, int n, const int8_t* q, const float* i
     const xt::MMConfig probe = xt::choose_config(ws[0]->fmt, (int)M, 0, 0, true);
     const bool need_rowsum = probe.mb > 1;
     const bool direct = (kpad == K) && ((((uintptr_t)q) & 15) == 0);
+    if (direct && user_rowsum)
+        return run_product(ws, n, q, (int)K, inv, user_rowsum, M, ys, acc, s);
     if (direct && !need_rowsum)
         return run_product(ws, n, q, (int)K, inv, nullptr, M, ys, acc, s);
     // Padded copy and/or row sums in the workspace.
@@ -270,13 +294,18 @@ int xt_weights_info(const xt_weights* w, int* fmt, int64_t* in_dim, int64_t* out
 
 int xt_quantize_i8(const float* x, int64_t M, int64_t K, int8_t* q, float* inv_scale, int mode,
                    void* stream) {
+    return xt_quantize_i8_rowsum(x, M, K, q, inv_scale, nullptr, mode, stream);
+}
+
+int xt_quantize_i8_rowsum(const float* x, int64_t M, int64_t K, int8_t* q, float* inv_scale,
+                          int32_t* rowsum, int mode, void* stream) {
     if (M < 0 || K <= 0) return fail(XT_ERR_INVALID, "need M >= 0 and K > 0");
     if (K > (int64_t)1 << 30 || M > (int64_t)1 << 31) return fail(XT_ERR_UNSUPPORTED, "size too large");
     if (mode != XT_QUANT_AVX512 && mode != XT_QUANT_SCALAR)
         return fail(XT_ERR_INVALID, "unknown quantisation mode");
     if (M == 0) return XT_OK;
     if (!x || !q || !inv_scale) return fail(XT_ERR_INVALID, "NULL pointer");
-    hipError_t e = xt::launch_quantize(x, K, (int)M, (int)K, q, (int)K, inv_scale, nullptr, mode,
+    hipError_t e = xt::launch_quantize(x, K, (int)M, (int)K, q, (int)K, inv_scale, rowsum, mode,
                                        static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "quantize launch");
     return XT_OK;
@@ -286,7 +315,16 @@ int xt_ternary_linear_q(const xt_weights* w, const int8_t* q, const float* inv_s
                         float* y, int32_t* acc, void* stream) {
     const xt_weights* ws[1] = {w};
     float* ys[1] = {y};
-    return linear_q(ws, 1, q, inv_scale, M, ys, acc, static_cast<hipStream_t>(stream));
+    return linear_q(ws, 1, q, inv_scale, nullptr, M, ys, acc, static_cast<hipStream_t>(stream));
+}
+
+int xt_ternary_linear_q_rowsum(const xt_weights* w, const int8_t* q, const float* inv_scale,
+                               const int32_t* rowsum, int64_t M, float* y, int32_t* acc,
+                               void* stream) {
+    if (M > 0 && !rowsum) return fail(XT_ERR_INVALID, "rowsum pointer is NULL");
+    const xt_weights* ws[1] = {w};
+    float* ys[1] = {y};
+    return linear_q(ws, 1, q, inv_scale, rowsum, M, ys, acc, static_cast<hipStream_t>(stream));
 }
 
 int xt_ternary_linear_f32(const xt_weights* w, const float* x, int64_t M, float* y, int mode,
@@ -298,7 +336,7 @@ int xt_ternary_linear_f32(const xt_weights* w, const float* x, int64_t M, float*
 
 int xt_ternary_linear_multi_q(const xt_weights* const* ws, int n, const int8_t* q,
                               const float* inv_scale, int64_t M, float* const* ys, void* stream) {
-    return linear_q(ws, n, q, inv_scale, M, ys, nullptr, static_cast<hipStream_t>(stream));
+    return linear_q(ws, n, q, inv_scale, nullptr, M, ys, nullptr, static_cast<hipStream_t>(stream));
 }
 
 int xt_ternary_linear_multi_f32(const xt_weights* const* ws, int n, const float* x, int64_t M,

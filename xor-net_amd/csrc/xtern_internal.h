@@ -32,6 +32,7 @@ struct Proj {
     int32_t* acc;          // optional [M][N] exact i32 dots
     int N;
     int tile0;             // first blockIdx.x of this projection
+    int col0;              // first column of this projection in the split-K workspace
 };
 
 struct MMArgs {
@@ -43,10 +44,15 @@ struct MMArgs {
     int M;
     int ldq;
     int nch;                // chunks per row
+    int cps;                // chunks per split-K slice (blockIdx.z)
+    int32_t* part;          // split-K partial sums [M][ldp], all zero between calls
+    int ldp;
+    unsigned* cnt;          // split-K arrival counters, one per (x, y) tile, zero between calls
 };
 
 struct MMConfig {
-    int mb, nb, waves;  // tokens per WG = 16*mb, rows per WG = 16*nb
+    int mb, nb, waves, pf;  // tokens per WG = 16*mb, rows per WG = 16*nb
+    int splitk;             // workgroups along K (blockIdx.z)
 };
 
 // Kernel launchers (xtern_kernels.hip).  Return the hipError_t of the launch.
@@ -56,6 +62,6 @@ hipError_t launch_rowsum(const int8_t* qin, int64_t ldin, int M, int K, int8_t* 
                          int ldout, int32_t* rowsum, hipStream_t s);
 hipError_t launch_mm(int fmt, const MMConfig& cfg, const MMArgs& a, int ntiles_total,
                      hipStream_t s);
-MMConfig choose_config(int fmt, int M, int64_t N_total, int nch, bool have_rowsum);
+MMConfig choose_config(int fmt, int M, int ntiles_nb1, int nch, bool have_rowsum);
 
 }  // namespace xt

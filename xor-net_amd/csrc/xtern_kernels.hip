@@ -178,19 +178,29 @@ __device__ __forceinline__ v4i decode4(int x) {
     return b;
 }
 
-// One workgroup computes a (16*MB tokens) x (16*NB output rows) tile over the
-// full reduction dimension; its WAVES waves take interleaved chunks (split-K
-// inside the workgroup) and are summed through LDS.  PF chunks per wave are
-// loaded before any is consumed, to keep enough bytes in flight.
-// OWN_ROWSUM: the activation row sums come from an extra MFMA against an
-// all-ones B operand instead of the caller (MB == 1 only).
+__device__ __forceinline__ v4i mfma(v4i a, v4i b, v4i c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, c, 0, 0, 0);
+}
+
+// Workgroup (blockIdx.x, blockIdx.y, blockIdx.z) computes a (16*MB tokens) x
+// (16*NB output rows) tile over chunk slice z of the reduction dimension.  Its
+// WAVES waves take interleaved chunks of the slice and are summed through
+// LDS.  Each wave loads PF chunks (weights and activations) before consuming
+// any, so one HBM round trip covers PF chunks.  With gridDim.z > 1 the slices
+// are combined with device-scope i32 atomics in a zeroed workspace; the last
+// workgroup to arrive at a tile runs the epilogue and re-zeroes the workspace
+// and its counter for the next call.
+// OWN_ROWSUM (MB == 1): the activation row sums come from one extra MFMA per
+// k-step against an all-ones B operand instead of the caller.
 template <int FMT, int MB, int NB, int WAVES, int PF, bool OWN_ROWSUM>
 __global__ __launch_bounds__(WAVES * 64) void mm_kernel(const MMArgs a) {
     constexpr int STEPS = (FMT == XT_PACK5) ? 5 : 4;
     constexpr int CH = STEPS * 64;
-    constexpr int NACC = MB * NB + (OWN_ROWSUM ? 1 : 0);
+    constexpr int NBLK = MB * NB;
+    constexpr int NACC = NBLK + (OWN_ROWSUM ? 1 : 0);
     static_assert(!OWN_ROWSUM || MB == 1, "in-kernel row sums need MB == 1");
     __shared__ v4i red[WAVES][NACC][64];
+    __shared__ int last_flag;
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -206,6 +216,7 @@ __global__ __launch_bounds__(WAVES * 64) void mm_kernel(const MMArgs a) {
     int32_t* accout = a.proj[0].acc;
     int N = a.proj[0].N;
     int tile0 = 0;
+    int col0 = a.proj[0].col0;
 #pragma unroll
     for (int p = 1; p < 4; ++p) {
         if (p < a.nproj && bx >= a.proj[p].tile0) {
@@ -215,6 +226,7 @@ __global__ __launch_bounds__(WAVES * 64) void mm_kernel(const MMArgs a) {
             accout = a.proj[p].acc;
             N = a.proj[p].N;
             tile0 = a.proj[p].tile0;
+            col0 = a.proj[p].col0;
         }
     }
     const int ntile = bx - tile0;
@@ -223,6 +235,8 @@ __global__ __launch_bounds__(WAVES * 64) void mm_kernel(const MMArgs a) {
     const int mbase = blockIdx.y * (16 * MB);
     const int nch = a.nch;
     const int ldq = a.ldq;
+    const int cbeg = blockIdx.z * a.cps;
+    const int cend = min(nch, cbeg + a.cps);
 
     v4i acc[MB][NB];
 #pragma unroll
@@ -233,7 +247,7 @@ __global__ __launch_bounds__(WAVES * 64) void mm_kernel(const MMArgs a) {
     const v4i ones = v4i{0x01010101, 0x01010101, 0x01010101, 0x01010101};
     const v4i zero = v4i{0, 0, 0, 0};
 
-    for (int c0 = wave; c0 < nch; c0 += WAVES * PF) {
+    for (int c0 = cbeg + wave; c0 < cend; c0 += WAVES * PF) {
         v4i wv[PF][NB];
         v4i av[PF][MB][STEPS];
 #pragma unroll
@@ -242,7 +256,7 @@ __global__ __launch_bounds__(WAVES * 64) void mm_kernel(const MMArgs a) {
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
                 const int G = ntile * NB + nb;
-                wv[pp][nb] = (c < nch && G < NG)
+                wv[pp][nb] = (c < cend && G < NG)
                                  ? ld_stream(tiles + ((size_t)(G * nch + c) * 64 + lane) * 16)
                                  : zero;
             }
@@ -251,14 +265,14 @@ __global__ __launch_bounds__(WAVES * 64) void mm_kernel(const MMArgs a) {
                 const int row = mbase + mb * 16 + j;
 #pragma unroll
                 for (int s = 0; s < STEPS; ++s)
-                    av[pp][mb][s] = (c < nch && row < M)
+                    av[pp][mb][s] = (c < cend && row < M)
                                         ? ld_cached(a.q + (size_t)row * ldq + c * CH + s * 64 + g * 16)
                                         : zero;
             }
         }
 #pragma unroll
         for (int pp = 0; pp < PF; ++pp) {
-            if (c0 + pp * WAVES >= nch) break;
+            if (c0 + pp * WAVES >= cend) break;
 #pragma unroll
             for (int nb = 0; nb < NB; ++nb) {
                 if constexpr (FMT == XT_PACK5) {
@@ -279,34 +293,26 @@ __global__ __launch_bounds__(WAVES * 64) void mm_kernel(const MMArgs a) {
                             O[d] = pO & 0x00ff00ff;
                         }
 #pragma unroll
-                        for (int mb = 0; mb < MB; ++mb)
-                            acc[mb][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[pp][mb][s], b,
-                                                                                 acc[mb][nb], 0, 0, 0);
+                        for (int mb = 0; mb < MB; ++mb) acc[mb][nb] = mfma(av[pp][mb][s], b, acc[mb][nb]);
                         if constexpr (OWN_ROWSUM)
-                            if (nb == 0)
-                                accs = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[pp][0][s], ones,
-                                                                             accs, 0, 0, 0);
+                            if (nb == 0) accs = mfma(av[pp][0][s], ones, accs);
                     }
                 } else {
 #pragma unroll
                     for (int s = 0; s < STEPS; ++s) {
                         const v4i b = decode4(wv[pp][nb][s]);
 #pragma unroll
-                        for (int mb = 0; mb < MB; ++mb)
-                            acc[mb][nb] = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[pp][mb][s], b,
-                                                                                 acc[mb][nb], 0, 0, 0);
+                        for (int mb = 0; mb < MB; ++mb) acc[mb][nb] = mfma(av[pp][mb][s], b, acc[mb][nb]);
                         if constexpr (OWN_ROWSUM)
-                            if (nb == 0)
-                                accs = __builtin_amdgcn_mfma_i32_16x16x64_i8(av[pp][0][s], ones,
-                                                                             accs, 0, 0, 0);
+                            if (nb == 0) accs = mfma(av[pp][0][s], ones, accs);
                     }
                 }
             }
         }
     }
 
-    // Split-K reduction through LDS: every wave parks all its accumulators,
-    // then wave w finishes blocks w, w + WAVES, ...
+    // Reduction over the waves through LDS: every wave parks all its
+    // accumulators, then wave w finishes blocks w, w + WAVES, ...
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
@@ -314,16 +320,56 @@ __global__ __launch_bounds__(WAVES * 64) void mm_kernel(const MMArgs a) {
     if constexpr (OWN_ROWSUM) red[wave][NACC - 1][lane] = accs;
     __syncthreads();
 
+    // OWN_ROWSUM: row sums of this slice's activations, laid out like the
+    // accumulators (lane (g, j) register r belongs to token 4g + r).
     v4i rs = zero;
     if constexpr (OWN_ROWSUM) {
 #pragma unroll
         for (int w = 0; w < WAVES; ++w) rs += red[w][NACC - 1][lane];
     }
-    for (int blk = wave; blk < MB * NB; blk += WAVES) {
+    const bool split = gridDim.z > 1;
+
+    if (split) {
+        // Add this slice's partial sums (code domain, row sums not yet
+        // subtracted) into the workspace.
+        for (int blk = wave; blk < NBLK; blk += WAVES) {
+            const int mb = blk / NB, nb = blk % NB;
+            v4i sum = zero;
+#pragma unroll
+            for (int w = 0; w < WAVES; ++w) sum += red[w][blk][lane];
+            const int o = (ntile * NB + nb) * 16 + j;
+            if (o >= N) continue;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int i = mbase + mb * 16 + 4 * g + r;
+                if (i >= M) continue;
+                int ownr = 0;
+                if constexpr (OWN_ROWSUM) ownr = rs[r];
+                // OWN_ROWSUM slices carry their own share of the row sum.
+                __hip_atomic_fetch_add(a.part + (size_t)i * a.ldp + col0 + o, sum[r] - ownr,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            }
+        }
+        __threadfence();
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            unsigned* c = a.cnt + (size_t)blockIdx.y * gridDim.x + blockIdx.x;
+            const unsigned old = __hip_atomic_fetch_add(c, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+            last_flag = (old == gridDim.z - 1);
+            if (last_flag) __hip_atomic_store(c, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        __syncthreads();
+        if (!last_flag) return;
+        __threadfence();
+    }
+
+    for (int blk = wave; blk < NBLK; blk += WAVES) {
         const int mb = blk / NB, nb = blk % NB;
         v4i sum = zero;
+        if (!split) {
 #pragma unroll
-        for (int w = 0; w < WAVES; ++w) sum += red[w][blk][lane];
+            for (int w = 0; w < WAVES; ++w) sum += red[w][blk][lane];
+        }
         const int o = (ntile * NB + nb) * 16 + j;
         if (o >= N) continue;
         const float wscale = ws[o];
@@ -331,8 +377,14 @@ __global__ __launch_bounds__(WAVES * 64) void mm_kernel(const MMArgs a) {
         for (int r = 0; r < 4; ++r) {
             const int i = mbase + mb * 16 + 4 * g + r;
             if (i >= M) continue;
-            const int rsum = OWN_ROWSUM ? rs[r] : a.rowsum[i];
-            const int d = sum[r] - rsum;
+            int d;
+            if (split) {
+                int32_t* pp = a.part + (size_t)i * a.ldp + col0 + o;
+                const int tot = __hip_atomic_exchange(pp, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                d = OWN_ROWSUM ? tot : tot - a.rowsum[i];
+            } else {
+                d = sum[r] - (OWN_ROWSUM ? rs[r] : a.rowsum[i]);
+            }
             // layers.rs:294 — (dot as f32 * inv_scale) * w_scale, two roundings.
             y[(size_t)i * N + o] = __fmul_rn(__fmul_rn((float)d, a.inv[i]), wscale);
             if (accout) accout[(size_t)i * N + o] = d;
@@ -341,33 +393,58 @@ __global__ __launch_bounds__(WAVES * 64) void mm_kernel(const MMArgs a) {
 }
 
 template <int FMT, int MB, int NB, int W, int PF, bool OWN>
-static hipError_t launch_t(const MMArgs& a, int ntiles, hipStream_t s) {
-    dim3 grid(ntiles, (a.M + 16 * MB - 1) / (16 * MB));
+static hipError_t launch_t(const MMArgs& a, int ntiles, int splitk, hipStream_t s) {
+    dim3 grid(ntiles, (a.M + 16 * MB - 1) / (16 * MB), splitk);
     hipLaunchKernelGGL((mm_kernel<FMT, MB, NB, W, PF, OWN>), grid, dim3(W * 64), 0, s, a);
     return hipGetLastError();
 }
 
-MMConfig choose_config(int fmt, int M, int64_t N_total, int nch, bool have_rowsum) {
+// Tile shapes (see the roofline notes in the design document of the repo):
+//   M <= 16  one 16-token block per workgroup, 16 output rows, 4 waves
+//            splitting K, up to 4 chunks per wave per HBM round trip;
+//   M > 16   32 tokens x 128 output rows per workgroup (wave tile 32 x 128,
+//            16 MFMAs per k-step per decode of 8 weight blocks).
+// Split-K across workgroups when the (x, y) grid alone cannot fill 256 CUs.
+MMConfig choose_config(int fmt, int M, int ntiles_nb1, int nch, bool have_rowsum) {
     (void)fmt;
-    (void)N_total;
-    (void)nch;
-    if (M <= 16 || !have_rowsum) return MMConfig{1, 1, 4};
-    return MMConfig{4, 2, 4};
+    MMConfig c;
+    if (M <= 16 || !have_rowsum) {
+        c = MMConfig{1, 1, 4, 4, 1};
+        const int mt = (M + 15) / 16;
+        const int base = ntiles_nb1 * mt;
+        if (base > 0 && base < 256 && nch >= 8) {
+            int s = (512 + base - 1) / base;
+            s = s < nch / 4 ? s : nch / 4;
+            c.splitk = s < 1 ? 1 : s;
+        }
+        return c;
+    }
+    c = MMConfig{2, 8, 4, 2, 1};
+    const int mt = (M + 31) / 32;
+    const int nt = (ntiles_nb1 + 7) / 8;
+    const int base = nt * mt;
+    if (base < 256 && nch >= 4) {
+        int s = (400 + base - 1) / base;
+        s = s < nch / 2 ? s : nch / 2;
+        c.splitk = s < 1 ? 1 : s;
+    }
+    return c;
 }
 
 hipError_t launch_mm(int fmt, const MMConfig& cfg, const MMArgs& a, int ntiles_total,
                      hipStream_t s) {
     const bool own = (a.rowsum == nullptr);
-    if (cfg.mb == 1 && cfg.nb == 1 && cfg.waves == 4) {
+    const int sk = cfg.splitk;
+    if (cfg.mb == 1 && cfg.nb == 1 && cfg.waves == 4 && cfg.pf == 4) {
         if (fmt == XT_PACK5)
-            return own ? launch_t<XT_PACK5, 1, 1, 4, 2, true>(a, ntiles_total, s)
-                       : launch_t<XT_PACK5, 1, 1, 4, 2, false>(a, ntiles_total, s);
-        return own ? launch_t<XT_PACK4, 1, 1, 4, 2, true>(a, ntiles_total, s)
-                   : launch_t<XT_PACK4, 1, 1, 4, 2, false>(a, ntiles_total, s);
+            return own ? launch_t<XT_PACK5, 1, 1, 4, 4, true>(a, ntiles_total, sk, s)
+                       : launch_t<XT_PACK5, 1, 1, 4, 4, false>(a, ntiles_total, sk, s);
+        return own ? launch_t<XT_PACK4, 1, 1, 4, 4, true>(a, ntiles_total, sk, s)
+                   : launch_t<XT_PACK4, 1, 1, 4, 4, false>(a, ntiles_total, sk, s);
     }
-    if (cfg.mb == 4 && cfg.nb == 2 && cfg.waves == 4 && !own) {
-        if (fmt == XT_PACK5) return launch_t<XT_PACK5, 4, 2, 4, 1, false>(a, (ntiles_total), s);
-        return launch_t<XT_PACK4, 4, 2, 4, 1, false>(a, ntiles_total, s);
+    if (cfg.mb == 2 && cfg.nb == 8 && cfg.waves == 4 && cfg.pf == 2 && !own) {
+        if (fmt == XT_PACK5) return launch_t<XT_PACK5, 2, 8, 4, 2, false>(a, ntiles_total, sk, s);
+        return launch_t<XT_PACK4, 2, 8, 4, 2, false>(a, ntiles_total, sk, s);
     }
     return hipErrorInvalidValue;
 }

@@ -54,7 +54,9 @@ _lib.xt_tile_bytes.argtypes = [ctypes.c_int, _i64, _i64]
 _lib.xt_tile_bytes.restype = _sz
 _lib.xt_repack_host.argtypes = [ctypes.c_int, _i64, _i64, _vp, _sz, _vp]
 _lib.xt_quantize_i8.argtypes = [_vp, _i64, _i64, _vp, _vp, ctypes.c_int, _vp]
+_lib.xt_quantize_i8_rowsum.argtypes = [_vp, _i64, _i64, _vp, _vp, _vp, ctypes.c_int, _vp]
 _lib.xt_ternary_linear_q.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp, _vp]
+_lib.xt_ternary_linear_q_rowsum.argtypes = [_vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp]
 _lib.xt_ternary_linear_f32.argtypes = [_vp, _vp, _i64, _vp, ctypes.c_int, _vp]
 _lib.xt_ternary_linear_multi_q.argtypes = [_vp, ctypes.c_int, _vp, _vp, _i64, _vp, _vp]
 _lib.xt_ternary_linear_multi_f32.argtypes = [_vp, ctypes.c_int, _vp, _i64, _vp, ctypes.c_int, _vp]
@@ -280,6 +282,36 @@ def quantize_i8(x, mode=XT_QUANT_AVX512, stream=None):
                                _dev_ptr(q, torch.int8, "q"), _dev_ptr(inv, torch.float32, "inv"),
                                mode, _stream_ptr(stream)))
     return q, inv
+
+
+def quantize_i8_rowsum(x, mode=XT_QUANT_AVX512, stream=None):
+    """quantize_i8 plus the exact i32 row sums of q (an xtern extension)."""
+    torch = _torch()
+    x2 = x.reshape(-1, x.shape[-1])
+    M, K = x2.shape
+    q = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    inv = torch.empty((M,), dtype=torch.float32, device=x.device)
+    rs = torch.empty((M,), dtype=torch.int32, device=x.device)
+    _check(_lib.xt_quantize_i8_rowsum(_dev_ptr(x2, torch.float32, "x"), M, K,
+                                      _dev_ptr(q, torch.int8, "q"),
+                                      _dev_ptr(inv, torch.float32, "inv"),
+                                      _dev_ptr(rs, torch.int32, "rowsum"), mode,
+                                      _stream_ptr(stream)))
+    return q, inv, rs
+
+
+def linear_q_rowsum(w, q, inv, rowsum, out=None, stream=None):
+    """linear_q with caller-provided row sums of q (an xtern extension)."""
+    torch = _torch()
+    q2 = q.reshape(-1, q.shape[-1])
+    M = q2.shape[0]
+    y = out if out is not None else torch.empty((M, w.out_dim), dtype=torch.float32, device=q.device)
+    _check(_lib.xt_ternary_linear_q_rowsum(w.handle, _dev_ptr(q2, torch.int8, "q"),
+                                           _dev_ptr(inv, torch.float32, "inv_scale"),
+                                           _dev_ptr(rowsum, torch.int32, "rowsum"), M,
+                                           _dev_ptr(y, torch.float32, "y"), None,
+                                           _stream_ptr(stream)))
+    return y
 
 
 def linear_q(w, q, inv, acc=False, out=None, stream=None):
