@@ -407,3 +407,20 @@ def test_splitk_workspace_alternating_shapes():
             log(f"alternating round={rnd} K={K} N={N} M={M}")
             _, acc = xtern.linear_q(w, q, torch.ones(M, device=DEV), acc=True)
             assert np.array_equal(acc.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("cfg", ["1,1,4,4,3", "1,4,4,2,2", "2,8,4,2,4"])
+def test_forced_splitk_configs(cfg, monkeypatch):
+    """Split-K across workgroups (only taken when forced) stays exact, across
+    shape changes that move the partial-sum planes."""
+    monkeypatch.setenv("XTERN_CONFIG", cfg)
+    rng = np.random.default_rng(40)
+    for K, N, M in ((2560, 640, 1), (6912, 2560, 128), (2560, 6912, 40), (1024, 96, 16)):
+        log(f"forced {cfg} K={K} N={N} M={M}")
+        t = tern(rng, N, K)
+        w = xtern.DeviceWeights(xtern.XT_PACK4, K, N, make_bytes(t, xtern.XT_PACK4),
+                                np.ones(N, np.float32))
+        q = rng.integers(-127, 128, (M, K)).astype(np.int8)
+        _, acc = xtern.linear_q(w, torch.from_numpy(q).to(DEV), torch.ones(M, device=DEV),
+                                acc=True)
+        assert np.array_equal(acc.cpu().numpy(), exact_acc(t, q))

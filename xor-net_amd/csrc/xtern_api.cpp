@@ -53,9 +53,9 @@ int hip_fail(hipError_t e, const char* what) {
 // waits for the stream first.
 //   kind 0: quantised activations, inv scales and row sums of the f32 entry
 //           points, padded copies of caller activations;
-//   kind 1: split-K partial sums and arrival counters.  Zeroed when
-//           allocated; every product launch leaves it zero again (the last
-//           workgroup of a tile clears what it read).
+//   kind 1: split-K partial-sum planes and arrival counters.  Zeroed when
+//           allocated; every product launch leaves the counters zero again
+//           (the last workgroup of a tile resets its counter).
 struct Workspace {
     void* ptr = nullptr;
     size_t cap = 0;
@@ -89,6 +89,23 @@ int workspace(hipStream_t s, size_t bytes, void** out, int kind = 0) {
 }
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
+
+// Split-K workspace of a stream: [counters: g_cnt_region bytes][planes].  The
+// counter region only grows by reallocating the whole buffer (zeroed).
+size_t g_cnt_region = 1 << 16;
+
+int splitk_workspace(hipStream_t s, size_t cbytes, size_t pbytes, void** out, size_t* region) {
+    {
+        std::lock_guard<std::mutex> lk(g_ws_mu);
+        if (cbytes > g_cnt_region) {
+            g_cnt_region = cbytes;
+            for (auto& kv : g_ws)
+                if (std::get<2>(kv.first) == 1) kv.second.cap = 0;  // force regrowth
+        }
+        *region = g_cnt_region;
+    }
+    return workspace(s, *region + pbytes, out, 1);
+}
 
 int check_weights(const xt_weights* w) {
     if (!w) return fail(XT_ERR_INVALID, "weights handle is NULL");
@@ -131,13 +148,17 @@ int run_product(const xt_weights* const* ws, int n, const int8_t* q, int ldq, co
     const int64_t gy = (M + 16 * cfg.mb - 1) / (16 * cfg.mb);
     if (gy > 65535) return fail(XT_ERR_UNSUPPORTED, "M too large for one launch");
     if (cfg.splitk > 1) {
-        const size_t pbytes = align_up((size_t)M * cols * sizeof(int32_t), 256);
-        const size_t cbytes = align_up((size_t)tiles * gy * sizeof(unsigned), 256);
+        // Counters first, at a fixed offset, so every call finds them zero
+        // (launches reset the counters they use; the planes after them are
+        // fully overwritten before they are read).
+        const size_t cbytes = align_up((size_t)tiles * gy * sizeof(unsigned), 4096);
+        const size_t pbytes = align_up((size_t)cfg.splitk * M * cols * sizeof(int32_t), 256);
         void* wsp = nullptr;
-        if (int rc = workspace(s, pbytes + cbytes, &wsp, 1)) return rc;
-        a.part = static_cast<int32_t*>(wsp);
+        size_t region = 0;
+        if (int rc = splitk_workspace(s, cbytes, pbytes, &wsp, &region)) return rc;
+        a.cnt = static_cast<unsigned*>(wsp);
+        a.part = reinterpret_cast<int32_t*>(static_cast<char*>(wsp) + region);
         a.ldp = cols;
-        a.cnt = reinterpret_cast<unsigned*>(static_cast<char*>(wsp) + pbytes);
     }
     hipError_t e = xt::launch_mm(fmt, cfg, a, tiles, s);
     if (e != hipSuccess) return hip_fail(e, "ternary product launch");

@@ -8,6 +8,8 @@
 //   TernaryLinear::forward      src/bit1_58/layers.rs:262-345 (epilogue :294)
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdio.h>
+#include <stdlib.h>
 
 #include "../../include/xtern.h"
 #include "xtern_internal.h"
@@ -187,9 +189,9 @@ __device__ __forceinline__ v4i mfma(v4i a, v4i b, v4i c) {
 // WAVES waves take interleaved chunks of the slice and are summed through
 // LDS.  Each wave loads PF chunks (weights and activations) before consuming
 // any, so one HBM round trip covers PF chunks.  With gridDim.z > 1 the slices
-// are combined with device-scope i32 atomics in a zeroed workspace; the last
-// workgroup to arrive at a tile runs the epilogue and re-zeroes the workspace
-// and its counter for the next call.
+// write their partial sums to planes of a workspace; the last workgroup to
+// arrive at a tile (device-scope counter, release/acquire fences) adds the
+// planes, runs the epilogue and clears the counter for the next call.
 // OWN_ROWSUM (MB == 1): the activation row sums come from one extra MFMA per
 // k-step against an all-ones B operand instead of the caller.
 template <int FMT, int MB, int NB, int WAVES, int PF, bool OWN_ROWSUM>
@@ -330,8 +332,10 @@ __global__ __launch_bounds__(WAVES * 64) void mm_kernel(const MMArgs a) {
     const bool split = gridDim.z > 1;
 
     if (split) {
-        // Add this slice's partial sums (code domain, row sums not yet
-        // subtracted) into the workspace.
+        // Publish this slice's partial sums (code domain; an OWN_ROWSUM slice
+        // has already subtracted its own share of the row sums) to plane z of
+        // the workspace, then count arrivals at this tile.
+        int32_t* plane = a.part + (size_t)blockIdx.z * a.M * a.ldp;
         for (int blk = wave; blk < NBLK; blk += WAVES) {
             const int mb = blk / NB, nb = blk % NB;
             v4i sum = zero;
@@ -345,12 +349,10 @@ __global__ __launch_bounds__(WAVES * 64) void mm_kernel(const MMArgs a) {
                 if (i >= M) continue;
                 int ownr = 0;
                 if constexpr (OWN_ROWSUM) ownr = rs[r];
-                // OWN_ROWSUM slices carry their own share of the row sum.
-                __hip_atomic_fetch_add(a.part + (size_t)i * a.ldp + col0 + o, sum[r] - ownr,
-                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                plane[(size_t)i * a.ldp + col0 + o] = sum[r] - ownr;
             }
         }
-        __threadfence();
+        __threadfence();  // release: the planes are visible device-wide
         __syncthreads();
         if (threadIdx.x == 0) {
             unsigned* c = a.cnt + (size_t)blockIdx.y * gridDim.x + blockIdx.x;
@@ -360,7 +362,7 @@ __global__ __launch_bounds__(WAVES * 64) void mm_kernel(const MMArgs a) {
         }
         __syncthreads();
         if (!last_flag) return;
-        __threadfence();
+        __threadfence();  // acquire: see every other slice's plane
     }
 
     for (int blk = wave; blk < NBLK; blk += WAVES) {
@@ -379,8 +381,11 @@ __global__ __launch_bounds__(WAVES * 64) void mm_kernel(const MMArgs a) {
             if (i >= M) continue;
             int d;
             if (split) {
-                int32_t* pp = a.part + (size_t)i * a.ldp + col0 + o;
-                const int tot = __hip_atomic_exchange(pp, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                const size_t off = (size_t)i * a.ldp + col0 + o;
+                const size_t plane_sz = (size_t)a.M * a.ldp;
+                int tot = 0;
+                for (unsigned z = 0; z < gridDim.z; ++z)
+                    tot += __builtin_nontemporal_load(a.part + z * plane_sz + off);
                 d = OWN_ROWSUM ? tot : tot - a.rowsum[i];
             } else {
                 d = sum[r] - (OWN_ROWSUM ? rs[r] : a.rowsum[i]);
@@ -399,53 +404,80 @@ static hipError_t launch_t(const MMArgs& a, int ntiles, int splitk, hipStream_t 
     return hipGetLastError();
 }
 
-// Tile shapes (see the roofline notes in the design document of the repo):
-//   M <= 16  one 16-token block per workgroup, 16 output rows, 4 waves
-//            splitting K, up to 4 chunks per wave per HBM round trip;
-//   M > 16   32 tokens x 128 output rows per workgroup (wave tile 32 x 128,
-//            16 MFMAs per k-step per decode of 8 weight blocks).
-// Split-K across workgroups when the (x, y) grid alone cannot fill 256 CUs.
+// Compiled tile shapes, selectable by MMConfig.
+#define XT_MM_SHAPES(X)  \
+    X(1, 1, 4, 4)        \
+    X(1, 1, 8, 2)        \
+    X(1, 1, 4, 2)        \
+    X(1, 2, 4, 4)        \
+    X(1, 4, 4, 2)        \
+    X(2, 4, 4, 2)        \
+    X(2, 8, 4, 2)        \
+    X(4, 4, 4, 1)        \
+    X(4, 2, 4, 1)
+
+namespace {
+bool shape_known(const MMConfig& c, bool own) {
+#define XT_KNOWN(MB_, NB_, W_, PF_) \
+    if (c.mb == MB_ && c.nb == NB_ && c.waves == W_ && c.pf == PF_) return !own || MB_ == 1;
+    XT_MM_SHAPES(XT_KNOWN)
+#undef XT_KNOWN
+    return false;
+}
+
+// XTERN_CONFIG="mb,nb,waves,pf,splitk" forces one tile shape (for tuning).
+bool env_config(MMConfig* c) {
+    const char* e = getenv("XTERN_CONFIG");
+    MMConfig f;
+    if (e && sscanf(e, "%d,%d,%d,%d,%d", &f.mb, &f.nb, &f.waves, &f.pf, &f.splitk) == 5 &&
+        f.splitk >= 1) {
+        *c = f;
+        return true;
+    }
+    return false;
+}
+}  // namespace
+
+// Default tile shapes (chosen by measurement on MI355X):
+//   M <= 16  one 16-token block x 16 output rows per workgroup, 4 waves
+//            splitting K with 4 chunks in flight each (8 waves x 2 chunks
+//            for rows longer than 16 chunks);
+//   M > 16   16 tokens x 64 output rows per workgroup.
+// Split-K across workgroups (gridDim.z > 1) is only taken when forced: its
+// device-scope release/acquire costs more than it saves at these sizes.
 MMConfig choose_config(int fmt, int M, int ntiles_nb1, int nch, bool have_rowsum) {
     (void)fmt;
     MMConfig c;
-    if (M <= 16 || !have_rowsum) {
-        c = MMConfig{1, 1, 4, 4, 1};
-        const int mt = (M + 15) / 16;
-        const int base = ntiles_nb1 * mt;
-        if (base > 0 && base < 256 && nch >= 8) {
-            int s = (512 + base - 1) / base;
-            s = s < nch / 4 ? s : nch / 4;
-            c.splitk = s < 1 ? 1 : s;
-        }
+    if (env_config(&c) && shape_known(c, !have_rowsum)) {
+        if (c.splitk > nch) c.splitk = nch;
         return c;
     }
-    c = MMConfig{2, 8, 4, 2, 1};
-    const int mt = (M + 31) / 32;
-    const int nt = (ntiles_nb1 + 7) / 8;
-    const int base = nt * mt;
-    if (base < 256 && nch >= 4) {
-        int s = (400 + base - 1) / base;
-        s = s < nch / 2 ? s : nch / 2;
-        c.splitk = s < 1 ? 1 : s;
+    if (M <= 16 || !have_rowsum) {
+        // deeper K split inside the workgroup for long rows
+        return nch > 16 ? MMConfig{1, 1, 8, 2, 1} : MMConfig{1, 1, 4, 4, 1};
     }
-    return c;
+    (void)ntiles_nb1;
+    return MMConfig{1, 4, 4, 2, 1};
 }
 
 hipError_t launch_mm(int fmt, const MMConfig& cfg, const MMArgs& a, int ntiles_total,
                      hipStream_t s) {
     const bool own = (a.rowsum == nullptr);
     const int sk = cfg.splitk;
-    if (cfg.mb == 1 && cfg.nb == 1 && cfg.waves == 4 && cfg.pf == 4) {
-        if (fmt == XT_PACK5)
-            return own ? launch_t<XT_PACK5, 1, 1, 4, 4, true>(a, ntiles_total, sk, s)
-                       : launch_t<XT_PACK5, 1, 1, 4, 4, false>(a, ntiles_total, sk, s);
-        return own ? launch_t<XT_PACK4, 1, 1, 4, 4, true>(a, ntiles_total, sk, s)
-                   : launch_t<XT_PACK4, 1, 1, 4, 4, false>(a, ntiles_total, sk, s);
+#define XT_LAUNCH(MB_, NB_, W_, PF_)                                                          \
+    if (cfg.mb == MB_ && cfg.nb == NB_ && cfg.waves == W_ && cfg.pf == PF_) {                \
+        if constexpr (MB_ == 1) {                                                              \
+            if (own)                                                                           \
+                return fmt == XT_PACK5                                                         \
+                           ? launch_t<XT_PACK5, MB_, NB_, W_, PF_, true>(a, ntiles_total, sk, s) \
+                           : launch_t<XT_PACK4, MB_, NB_, W_, PF_, true>(a, ntiles_total, sk, s); \
+        }                                                                                      \
+        if (own) return hipErrorInvalidValue;                                                  \
+        return fmt == XT_PACK5 ? launch_t<XT_PACK5, MB_, NB_, W_, PF_, false>(a, ntiles_total, sk, s) \
+                               : launch_t<XT_PACK4, MB_, NB_, W_, PF_, false>(a, ntiles_total, sk, s); \
     }
-    if (cfg.mb == 2 && cfg.nb == 8 && cfg.waves == 4 && cfg.pf == 2 && !own) {
-        if (fmt == XT_PACK5) return launch_t<XT_PACK5, 2, 8, 4, 2, false>(a, ntiles_total, sk, s);
-        return launch_t<XT_PACK4, 2, 8, 4, 2, false>(a, ntiles_total, sk, s);
-    }
+    XT_MM_SHAPES(XT_LAUNCH)
+#undef XT_LAUNCH
     return hipErrorInvalidValue;
 }
 
