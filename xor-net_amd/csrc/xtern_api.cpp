@@ -147,6 +147,24 @@ int run_product(const xt_weights* const* ws, int n, const int8_t* q, int ldq, co
     a.cps = (a.nch + cfg.splitk - 1) / cfg.splitk;
     const int64_t gy = (M + 16 * cfg.mb - 1) / (16 * cfg.mb);
     if (gy > 65535) return fail(XT_ERR_UNSUPPORTED, "M too large for one launch");
+    if (cfg.kind == 2) {
+        hipError_t e = xt::launch_gemv(fmt, a, tiles, cfg.waves, s);
+        if (e != hipSuccess) return hip_fail(e, "ternary GEMV launch");
+        return XT_OK;
+    }
+    if (cfg.kind == 1) {
+        if (cfg.splitk > 1) {
+            void* wsp = nullptr;
+            size_t region = 0;
+            const size_t pbytes = align_up((size_t)cfg.splitk * M * cols * sizeof(int32_t), 256);
+            if (int rc = splitk_workspace(s, 0, pbytes, &wsp, &region)) return rc;
+            a.part = reinterpret_cast<int32_t*>(static_cast<char*>(wsp) + region);
+        }
+        a.ldp = cols;
+        hipError_t e = xt::launch_gemm(fmt, a, tiles, cfg.splitk, s);
+        if (e != hipSuccess) return hip_fail(e, "ternary GEMM launch");
+        return XT_OK;
+    }
     if (cfg.splitk > 1) {
         // Counters first, at a fixed offset, so every call finds them zero
         // (launches reset the counters they use; the planes after them are
@@ -188,7 +206,7 @@ int linear_q(const xt_weights* const* ws, int n, const int8_t* q, const float* i
     const int64_t K = ws[0]->K;
     const int64_t kpad = ws[0]->nch * xt::chunk_cols(ws[0]->fmt);
     const xt::MMConfig probe = xt::choose_config(ws[0]->fmt, (int)M, 0, 0, true);
-    const bool need_rowsum = probe.mb > 1;
+    const bool need_rowsum = probe.kind == 1;
     const bool direct = (kpad == K) && ((((uintptr_t)q) & 15) == 0);
     if (direct && user_rowsum)
         return run_product(ws, n, q, (int)K, inv, user_rowsum, M, ys, acc, s);

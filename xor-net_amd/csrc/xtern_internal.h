@@ -53,6 +53,7 @@ struct MMArgs {
 struct MMConfig {
     int mb, nb, waves, pf;  // tokens per WG = 16*mb, rows per WG = 16*nb
     int splitk;             // workgroups along K (blockIdx.z)
+    int kind = 0;           // 0 mm_kernel, 1 prefill GEMM, 2 decode GEMV (waves used)
 };
 
 // Kernel launchers (xtern_kernels.hip).  Return the hipError_t of the launch.
@@ -63,5 +64,11 @@ hipError_t launch_rowsum(const int8_t* qin, int64_t ldin, int M, int K, int8_t* 
 hipError_t launch_mm(int fmt, const MMConfig& cfg, const MMArgs& a, int ntiles_total,
                      hipStream_t s);
 MMConfig choose_config(int fmt, int M, int ntiles_nb1, int nch, bool have_rowsum);
+// Prefill GEMM (M > 16, row sums required): 32 tokens x 128 rows per
+// workgroup, at most gemm_ncmax(fmt) chunks per split-K slice.
+int gemm_ncmax(int fmt);
+hipError_t launch_gemm(int fmt, const MMArgs& a, int ntiles, int splitk, hipStream_t s);
+// Decode GEMV (M <= 16): 16 output rows per workgroup, activations in LDS.
+hipError_t launch_gemv(int fmt, const MMArgs& a, int ntiles, int waves, hipStream_t s);
 
 }  // namespace xt

@@ -14,6 +14,14 @@
 #include "../../include/xtern.h"
 #include "xtern_internal.h"
 
+// XT_ABLATE (0 in the library) lets a timing harness compile the prefill
+// GEMM with parts removed: 1 = no weight loads, 2 = no activation loads,
+// 4 = no MFMA phase, 8 = no output stores, 16 = no LDS staging stores.
+// Outputs are meaningless when it is non-zero.
+#ifndef XT_ABLATE
+#define XT_ABLATE 0
+#endif
+
 namespace xt {
 
 typedef int v4i __attribute__((ext_vector_type(4)));
@@ -168,6 +176,17 @@ __device__ __forceinline__ v4i ld_stream(const uint8_t* p) {
 }
 __device__ __forceinline__ v4i ld_cached(const int8_t* p) {
     return *reinterpret_cast<const v4i*>(p);
+}
+
+// Workgroups are dispatched to the 8 XCDs round-robin in linear order, and
+// each XCD has its own L2.  xcd_remap turns the linear workgroup id into a
+// logical tile id so that every XCD owns a contiguous range of logical tiles
+// (a bijection on [0, total)); callers order logical tiles so that tiles that
+// share weights are adjacent and hence share an L2.
+__device__ __forceinline__ int xcd_remap(int lin, int total) {
+    const int q = total >> 3, r = total & 7;
+    const int xcd = lin & 7, slot = lin >> 3;
+    return xcd < r ? xcd * (q + 1) + slot : r * (q + 1) + (xcd - r) * q + slot;
 }
 
 // Pack4 tile dword -> four code dwords (columns 4jj..4jj+3 in byte order).
@@ -404,9 +423,475 @@ static hipError_t launch_t(const MMArgs& a, int ntiles, int splitk, hipStream_t 
     return hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Decode GEMV (M <= 16): activations staged in LDS, all weights in flight
+// ---------------------------------------------------------------------------
+//
+// Workgroup x owns the 16 output rows of row group x (or of the projection
+// x falls in) over the full reduction dimension.  The M <= 16 activation
+// rows go to LDS once ([chunk][step][g][token][16 B], only real tokens), so
+// each wave keeps nothing but weights in registers: wave w loads chunks
+// w, w + WAVES, ... (at most NCW each) before its first MFMA, one HBM round
+// trip for the whole row group.  The exact row sums are taken while staging
+// (v_dot4 against 1s, LDS atomics); the epilogue's scales are loaded at entry;
+// waves are summed through LDS.
+template <int FMT, int WAVES, int NCW>
+__global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const MMArgs a) {
+    constexpr int STEPS = (FMT == XT_PACK5) ? 5 : 4;
+    constexpr int CH = STEPS * 64;
+    constexpr int SEGS = CH / 16;
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ v4i red[WAVES][64];
+    __shared__ int rsum[16];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int g = lane >> 4;
+    const int j = lane & 15;
+
+    const int bx = blockIdx.x;
+    const uint8_t* tiles = a.proj[0].tiles;
+    const float* ws = a.proj[0].ws;
+    float* y = a.proj[0].y;
+    int32_t* accout = a.proj[0].acc;
+    int N = a.proj[0].N;
+    int tile0 = 0;
+#pragma unroll
+    for (int p = 1; p < 4; ++p) {
+        if (p < a.nproj && bx >= a.proj[p].tile0) {
+            tiles = a.proj[p].tiles;
+            ws = a.proj[p].ws;
+            y = a.proj[p].y;
+            accout = a.proj[p].acc;
+            N = a.proj[p].N;
+            tile0 = a.proj[p].tile0;
+        }
+    }
+    const int G = bx - tile0;
+    const int M = a.M;
+    const int nch = a.nch;
+    if (threadIdx.x < 16) rsum[threadIdx.x] = 0;
+
+    // weights first: they come from HBM and take longest
+    v4i wv[NCW];
+#pragma unroll
+    for (int t = 0; t < NCW; ++t) {
+        const int c = wave + t * WAVES;
+        wv[t] = c < nch ? ld_stream(tiles + ((size_t)(G * nch + c) * 64 + lane) * 16) : v4i{0, 0, 0, 0};
+    }
+    // epilogue operands, so no memory round trip is left after the MFMAs
+    const int o = G * 16 + j;
+    const float wscale = (wave == 0 && o < N) ? ws[o] : 0.0f;
+    float invr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) invr[r] = (wave == 0 && 4 * g + r < M) ? a.inv[4 * g + r] : 0.0f;
+    __syncthreads();  // rsum cleared
+
+    // activations -> LDS, with exact per-token byte sums (v_dot4 by 1s)
+    const int pieces = M * nch * SEGS;
+    for (int p = threadIdx.x; p < pieces; p += WAVES * 64) {
+        const int m = p % M;
+        const int seg = (p / M) % SEGS;
+        const int c = p / (M * SEGS);
+        const v4i v = ld_cached(a.q + (size_t)m * a.ldq + (size_t)c * CH + seg * 16);
+        int part = 0;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) part = __builtin_amdgcn_sdot4(v[d], 0x01010101, part, false);
+        atomicAdd(&rsum[m], part);
+        const int st = seg >> 2, gg = seg & 3;
+        *reinterpret_cast<v4i*>(lds + ((((c * STEPS + st) * 4 + gg) * M + m) << 4)) = v;
+    }
+    __syncthreads();
+
+    // one accumulator per k-step: short dependent MFMA chains
+    v4i acc[STEPS];
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) acc[s] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < NCW; ++t) {
+        const int c = wave + t * WAVES;
+        if (c < nch) {
+            if constexpr (FMT == XT_PACK5) {
+                int E[4], O[4];
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    E[d] = wv[t][d] & 0x00ff00ff;
+                    O[d] = ((unsigned)wv[t][d] >> 8) & 0x00ff00ff;
+                }
+#pragma unroll
+                for (int s = 0; s < STEPS; ++s) {
+                    v4i b;
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        const int pE = E[d] * 3, pO = O[d] * 3;
+                        b[d] = (int)__builtin_amdgcn_perm((unsigned)pO, (unsigned)pE, 0x07030501u);
+                        E[d] = pE & 0x00ff00ff;
+                        O[d] = pO & 0x00ff00ff;
+                    }
+                    v4i av = v4i{0, 0, 0, 0};
+                    if (j < M)
+                        av = *reinterpret_cast<const v4i*>(lds + ((((c * STEPS + s) * 4 + g) * M + j) << 4));
+                    acc[s] = mfma(av, b, acc[s]);
+                }
+            } else {
+#pragma unroll
+                for (int s = 0; s < STEPS; ++s) {
+                    v4i av = v4i{0, 0, 0, 0};
+                    if (j < M)
+                        av = *reinterpret_cast<const v4i*>(lds + ((((c * STEPS + s) * 4 + g) * M + j) << 4));
+                    acc[s] = mfma(av, decode4(wv[t][s]), acc[s]);
+                }
+            }
+        }
+    }
+#pragma unroll
+    for (int s = 1; s < STEPS; ++s) acc[0] += acc[s];
+
+    red[wave][lane] = acc[0];
+    __syncthreads();
+    if (wave != 0) return;
+    v4i sum = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) sum += red[w][lane];
+    if (o >= N) return;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int i = 4 * g + r;
+        if (i >= M) continue;
+        const int d = sum[r] - rsum[i];
+        // layers.rs:294 — (dot as f32 * inv_scale) * w_scale, two roundings.
+        y[(size_t)i * N + o] = __fmul_rn(__fmul_rn((float)d, invr[r]), wscale);
+        if (accout) accout[(size_t)i * N + o] = d;
+    }
+}
+
+// LDS budget for staged activations and the chunk bound per wave.
+constexpr int kGemvLds = 96 * 1024;
+
+// chunks per wave each compiled GEMV width can hold
+int gemv_ncw(int waves) { return waves == 16 ? 4 : waves == 8 ? 8 : 16; }
+
+bool gemv_fits(int fmt, int M, int nch, int waves, int ncw) {
+    const int ch = fmt == XT_PACK5 ? 320 : 256;
+    return M >= 1 && M <= 16 && (size_t)M * nch * ch <= (size_t)kGemvLds &&
+           (nch + waves - 1) / waves <= ncw;
+}
+
+hipError_t launch_gemv(int fmt, const MMArgs& a, int ntiles, int waves, hipStream_t s) {
+    const int ch = fmt == XT_PACK5 ? 320 : 256;
+    const size_t lds = (size_t)a.M * a.nch * ch;
+#define XT_GEMV(W_, NCW_)                                                                        \
+    if (waves == W_) {                                                                           \
+        if (fmt == XT_PACK5)                                                                     \
+            hipLaunchKernelGGL((gemv_kernel<XT_PACK5, W_, NCW_>), dim3(ntiles), dim3(W_ * 64), lds, s, a); \
+        else                                                                                     \
+            hipLaunchKernelGGL((gemv_kernel<XT_PACK4, W_, NCW_>), dim3(ntiles), dim3(W_ * 64), lds, s, a); \
+        return hipGetLastError();                                                                \
+    }
+    XT_GEMV(4, 16)
+    XT_GEMV(8, 8)
+    XT_GEMV(2, 16)
+    XT_GEMV(16, 4)
+#undef XT_GEMV
+    return hipErrorInvalidValue;
+}
+
+// ---------------------------------------------------------------------------
+// Prefill GEMM (M > 16): one load round per workgroup
+// ---------------------------------------------------------------------------
+//
+// Workgroup (x, y, z): 32 tokens (y) x 128 output rows (x) over chunk slice z
+// of at most NCMAX chunks.  Its 8 waves are 4 row groups of 32 rows x 2
+// chunk groups (even / odd chunks of the slice).  At entry every thread
+// issues all of its loads: the activation slice (32 x slice bytes, coalesced
+// 16-byte pieces) goes to LDS in MFMA A-operand order
+// [chunk][step][token block][lane][16 B], and each wave pulls its own weights
+// (32 rows x its chunks) into registers.  After one barrier the waves run
+// 2 x 2 accumulator blocks of 16x16x64 i8 MFMAs, prefetching the next
+// k-step's A operands from LDS before issuing the current step's MFMAs (two
+// waves per SIMD hide the rest).  The two chunk groups are added through LDS.
+// gridDim.z == 1 writes y; otherwise the slice's code-domain partial sums go
+// to plane z of `part` and gemm_reduce_kernel finishes.
+template <int FMT, int NCMAX, int KG>
+__global__ __launch_bounds__(256 * KG) void gemm_kernel(const MMArgs a) {
+    constexpr int STEPS = (FMT == XT_PACK5) ? 5 : 4;
+    constexpr int CH = STEPS * 64;
+    constexpr int SEGS = CH / 16;       // 16-byte pieces per token per chunk
+    constexpr int MB = 2;               // token blocks of 16
+    constexpr int NBW = 2;              // output-row blocks of 16 per wave
+    constexpr int NCW = (NCMAX + KG - 1) / KG;  // chunks per wave
+    constexpr int NT = 256 * KG;                 // threads
+    extern __shared__ __align__(16) uint8_t lds_a[];
+    __shared__ v4i red[KG - 1][4][MB * NBW][64];
+
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int ngrp = wave & 3;          // row group of 32 rows
+    const int kgrp = wave >> 2;         // chunks kgrp, kgrp + KG, ...
+    const int g = lane >> 4;
+    const int j = lane & 15;
+
+    // Logical tile: token blocks (y) fastest, so the token blocks that read the
+    // same weight rows sit on one XCD and share its L2.
+    const int gx = gridDim.x, gy = gridDim.y;
+    const int lin = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+    const int t = xcd_remap(lin, gx * gy * gridDim.z);
+    const int by = t % gy;
+    const int bx = (t / gy) % gx;
+    const int bz = t / (gx * gy);
+    const uint8_t* tiles = a.proj[0].tiles;
+    const float* ws = a.proj[0].ws;
+    float* y = a.proj[0].y;
+    int32_t* accout = a.proj[0].acc;
+    int N = a.proj[0].N;
+    int tile0 = 0;
+    int col0 = a.proj[0].col0;
+#pragma unroll
+    for (int p = 1; p < 4; ++p) {
+        if (p < a.nproj && bx >= a.proj[p].tile0) {
+            tiles = a.proj[p].tiles;
+            ws = a.proj[p].ws;
+            y = a.proj[p].y;
+            accout = a.proj[p].acc;
+            N = a.proj[p].N;
+            tile0 = a.proj[p].tile0;
+            col0 = a.proj[p].col0;
+        }
+    }
+    const int NG = (N + 15) >> 4;
+    const int M = a.M;
+    const int mbase = by * 32;
+    const int nch = a.nch;
+    const int cbeg = bz * a.cps;
+    const int nc = min(nch - cbeg, a.cps);  // chunks in this slice (<= NCMAX)
+    const int gbase = (bx - tile0) * 8 + ngrp * NBW;  // first row group of this wave
+
+    // Weights of this wave: NBW row groups x its chunks, 16 bytes per lane each.
+    v4i wv[NCW][NBW];
+#pragma unroll
+    for (int u = 0; u < NCW; ++u)
+#pragma unroll
+        for (int nb = 0; nb < NBW; ++nb) {
+            const int cc = kgrp + KG * u;
+            const int G = gbase + nb;
+            wv[u][nb] = (!(XT_ABLATE & 1) && cc < nc && G < NG)
+                            ? *reinterpret_cast<const v4i*>(tiles + ((size_t)(G * nch + cbeg + cc) * 64 + lane) * 16)
+                            : v4i{0, 0, 0, 0};
+        }
+
+    // Epilogue operands now, so no memory round trip is left after the MFMAs.
+    const bool split = gridDim.z > 1;
+    float wsc[NBW];
+#pragma unroll
+    for (int nb = 0; nb < NBW; ++nb) {
+        const int o = (gbase + nb) * 16 + j;
+        wsc[nb] = (!split && kgrp == 0 && o < N) ? ws[o] : 0.0f;
+    }
+    float invr[MB][4];
+    int rsr[MB][4];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const int i = mbase + mb * 16 + 4 * g + r;
+            const bool ok = !split && kgrp == 0 && i < M;
+            invr[mb][r] = ok ? a.inv[i] : 0.0f;
+            rsr[mb][r] = ok ? a.rowsum[i] : 0;
+        }
+
+    // Activation slice -> LDS, A-operand order.  Pieces are taken in LDS
+    // order (lane fastest), so the LDS stores are sequential; the global side
+    // reads 64-byte runs of 16 token rows.
+    const int pieces = 32 * nc * SEGS;
+    for (int p = threadIdx.x; p < pieces; p += NT) {
+        const int ln = p & 63;
+        const int blk = p >> 6;                 // (cc * STEPS + st) * MB + mb
+        const int mb = blk % MB;
+        const int cs = blk / MB;                // cc * STEPS + st
+        const int row = mbase + mb * 16 + (ln & 15);
+        v4i v = v4i{0, 0, 0, 0};
+        if (!(XT_ABLATE & 2) && row < M)
+            v = ld_cached(a.q + (size_t)row * a.ldq + (size_t)cbeg * CH + cs * 64 + (ln >> 4) * 16);
+        if (!(XT_ABLATE & 16)) *reinterpret_cast<v4i*>(lds_a + ((size_t)p << 4)) = v;
+    }
+    __syncthreads();
+
+    v4i acc[MB][NBW];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NBW; ++nb) acc[mb][nb] = v4i{0, 0, 0, 0};
+
+    // A operands of k-step (u, s) of this wave; `nxt` is read one step ahead.
+    auto a_addr = [&](int u, int st, int mb) {
+        return lds_a + (((((kgrp + KG * u) * STEPS + st) * MB + mb) * 64 + lane) << 4);
+    };
+    v4i cur[MB], nxt[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+        cur[mb] = (kgrp < nc) ? *reinterpret_cast<const v4i*>(a_addr(0, 0, mb)) : v4i{0, 0, 0, 0};
+
+#pragma unroll
+    for (int u = 0; u < NCW; ++u) {
+        if (!(XT_ABLATE & 4) && kgrp + KG * u < nc) {
+            int E[NBW][4], O[NBW][4];
+            if constexpr (FMT == XT_PACK5) {
+#pragma unroll
+                for (int nb = 0; nb < NBW; ++nb)
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        E[nb][d] = wv[u][nb][d] & 0x00ff00ff;
+                        O[nb][d] = ((unsigned)wv[u][nb][d] >> 8) & 0x00ff00ff;
+                    }
+            }
+#pragma unroll
+            for (int st = 0; st < STEPS; ++st) {
+                // prefetch the next k-step's operands
+                const int nu = (st + 1 < STEPS) ? u : u + 1;
+                const int ns = (st + 1 < STEPS) ? st + 1 : 0;
+                const bool have_next = (nu < NCW) && (kgrp + KG * nu < nc);
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb)
+                    nxt[mb] = have_next ? *reinterpret_cast<const v4i*>(a_addr(nu, ns, mb))
+                                        : v4i{0, 0, 0, 0};
+                v4i b[NBW];
+#pragma unroll
+                for (int nb = 0; nb < NBW; ++nb) {
+                    if constexpr (FMT == XT_PACK5) {
+#pragma unroll
+                        for (int d = 0; d < 4; ++d) {
+                            const int pE = E[nb][d] * 3, pO = O[nb][d] * 3;
+                            b[nb][d] = (int)__builtin_amdgcn_perm((unsigned)pO, (unsigned)pE, 0x07030501u);
+                            E[nb][d] = pE & 0x00ff00ff;
+                            O[nb][d] = pO & 0x00ff00ff;
+                        }
+                    } else {
+                        b[nb] = decode4(wv[u][nb][st]);
+                    }
+                }
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                    for (int nb = 0; nb < NBW; ++nb) acc[mb][nb] = mfma(cur[mb], b[nb], acc[mb][nb]);
+#pragma unroll
+                for (int mb = 0; mb < MB; ++mb) cur[mb] = nxt[mb];
+            }
+        }
+    }
+
+    // Add the odd-chunk waves into the even-chunk waves, stage the 32 x 128
+    // tile in LDS (every wave is past its LDS operand reads at the first
+    // barrier), then all 512 threads write whole rows with 16-byte stores.
+    if (kgrp > 0) {
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+            for (int nb = 0; nb < NBW; ++nb) red[kgrp - 1][ngrp][mb * NBW + nb][lane] = acc[mb][nb];
+    }
+    __syncthreads();
+    float* ytile = reinterpret_cast<float*>(lds_a);            // [32][128]
+    int* dtile = reinterpret_cast<int*>(lds_a + 32 * 128 * 4);  // [32][128]
+    if (kgrp == 0) {
+#pragma unroll
+        for (int nb = 0; nb < NBW; ++nb) {
+            const int col = ngrp * 32 + nb * 16 + j;
+#pragma unroll
+            for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int row = mb * 16 + 4 * g + r;
+                    int v = acc[mb][nb][r];
+#pragma unroll
+                    for (int kk = 0; kk < KG - 1; ++kk) v += red[kk][ngrp][mb * NBW + nb][lane][r];
+                    if (split) {
+                        dtile[row * 128 + col] = v;
+                    } else {
+                        const int d = v - rsr[mb][r];
+                        // layers.rs:294 — (dot as f32 * inv_scale) * w_scale.
+                        ytile[row * 128 + col] = __fmul_rn(__fmul_rn((float)d, invr[mb][r]), wsc[nb]);
+                        dtile[row * 128 + col] = d;
+                    }
+                }
+        }
+    }
+    __syncthreads();
+    if (XT_ABLATE & 8) return;
+    const int obase = (bx - tile0) * 128;
+    int32_t* plane = a.part + (size_t)bz * a.M * a.ldp;
+    const bool vec = (N & 3) == 0;
+    for (int idx = threadIdx.x; idx < 32 * 32; idx += NT) {
+        const int row = idx >> 5, c4 = (idx & 31) * 4;
+        const int i = mbase + row, o = obase + c4;
+        if (i >= M || o >= N) continue;
+        if (split) {
+            // planes have a padded stride (a multiple of 16 columns)
+            *reinterpret_cast<int4*>(plane + (size_t)i * a.ldp + col0 + o) =
+                *reinterpret_cast<const int4*>(dtile + row * 128 + c4);
+            continue;
+        }
+        if (vec && o + 3 < N) {
+            *reinterpret_cast<float4*>(y + (size_t)i * N + o) =
+                *reinterpret_cast<const float4*>(ytile + row * 128 + c4);
+            if (accout)
+                *reinterpret_cast<int4*>(accout + (size_t)i * N + o) =
+                    *reinterpret_cast<const int4*>(dtile + row * 128 + c4);
+        } else {
+            for (int e2 = 0; e2 < 4 && o + e2 < N; ++e2) {
+                y[(size_t)i * N + o + e2] = ytile[row * 128 + c4 + e2];
+                if (accout) accout[(size_t)i * N + o + e2] = dtile[row * 128 + c4 + e2];
+            }
+        }
+    }
+}
+
+// Sum the split-K planes of every projection and apply the epilogue.
+// One thread per (token, workspace column).
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(const MMArgs a, int nsplit) {
+    const int i = blockIdx.y;
+    const int col = blockIdx.x * 256 + threadIdx.x;
+    if (col >= a.ldp || i >= a.M) return;
+    int p = 0;
+#pragma unroll
+    for (int q = 1; q < 4; ++q)
+        if (q < a.nproj && col >= a.proj[q].col0) p = q;
+    const Proj& pr = a.proj[p];
+    const int o = col - pr.col0;
+    if (o >= pr.N) return;
+    const size_t plane_sz = (size_t)a.M * a.ldp;
+    int tot = 0;
+    for (int z = 0; z < nsplit; ++z) tot += a.part[z * plane_sz + (size_t)i * a.ldp + col];
+    const int d = tot - a.rowsum[i];
+    pr.y[(size_t)i * pr.N + o] = __fmul_rn(__fmul_rn((float)d, a.inv[i]), pr.ws[o]);
+    if (pr.acc) pr.acc[(size_t)i * pr.N + o] = d;
+}
+
+int gemm_ncmax(int fmt) { return fmt == XT_PACK5 ? 8 : 10; }
+
+hipError_t launch_gemm(int fmt, const MMArgs& a, int ntiles, int splitk, hipStream_t s) {
+    const dim3 grid(ntiles, (a.M + 31) / 32, splitk);
+    const int ch = fmt == XT_PACK5 ? 320 : 256;
+    size_t lds = (size_t)a.cps * ch * 32;
+    if (lds < 32 * 128 * 8) lds = 32 * 128 * 8;  // the staged output tile
+#ifndef XT_GEMM_KG
+#define XT_GEMM_KG 4
+#endif
+    constexpr int KG = XT_GEMM_KG;
+    if (fmt == XT_PACK5)
+        hipLaunchKernelGGL((gemm_kernel<XT_PACK5, 8, KG>), grid, dim3(256 * KG), lds, s, a);
+    else
+        hipLaunchKernelGGL((gemm_kernel<XT_PACK4, 10, KG>), grid, dim3(256 * KG), lds, s, a);
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess || splitk == 1) return e;
+    const dim3 rgrid((a.ldp + 255) / 256, a.M);
+    hipLaunchKernelGGL(gemm_reduce_kernel, rgrid, dim3(256), 0, s, a, splitk);
+    return hipGetLastError();
+}
+
 // Compiled tile shapes, selectable by MMConfig.
 #define XT_MM_SHAPES(X)  \
     X(1, 1, 4, 4)        \
+    X(1, 1, 2, 8)        \
+    X(1, 1, 2, 4)        \
     X(1, 1, 8, 2)        \
     X(1, 1, 4, 2)        \
     X(1, 2, 4, 4)        \
@@ -429,6 +914,12 @@ bool shape_known(const MMConfig& c, bool own) {
 bool env_config(MMConfig* c) {
     const char* e = getenv("XTERN_CONFIG");
     MMConfig f;
+    if (e && sscanf(e, "gemv,%d", &f.waves) == 1) {
+        f = MMConfig{1, 1, f.waves, 1, 1};
+        f.kind = 2;
+        *c = f;
+        return true;
+    }
     if (e && sscanf(e, "%d,%d,%d,%d,%d", &f.mb, &f.nb, &f.waves, &f.pf, &f.splitk) == 5 &&
         f.splitk >= 1) {
         *c = f;
@@ -439,24 +930,40 @@ bool env_config(MMConfig* c) {
 }  // namespace
 
 // Default tile shapes (chosen by measurement on MI355X):
-//   M <= 16  one 16-token block x 16 output rows per workgroup, 4 waves
-//            splitting K with 4 chunks in flight each (8 waves x 2 chunks
-//            for rows longer than 16 chunks);
-//   M > 16   16 tokens x 64 output rows per workgroup.
+//   M <= 16  the decode GEMV (activations in LDS, 16 waves) when the staged
+//            activations fit, else 16 rows per workgroup, 8 waves x 2 chunks;
+//   M > 16   the prefill GEMM (32 tokens x 128 rows) when K fits one LDS
+//            slice, else 16 tokens x 64 rows with 4 waves splitting K.
 // Split-K across workgroups (gridDim.z > 1) is only taken when forced: its
 // device-scope release/acquire costs more than it saves at these sizes.
 MMConfig choose_config(int fmt, int M, int ntiles_nb1, int nch, bool have_rowsum) {
-    (void)fmt;
     MMConfig c;
-    if (env_config(&c) && shape_known(c, !have_rowsum)) {
-        if (c.splitk > nch) c.splitk = nch;
+    if (env_config(&c)) {
+        if (c.kind == 2 && M <= 16 && gemv_fits(fmt, M, nch, c.waves, gemv_ncw(c.waves)))
+            return c;
+        if (c.kind == 0 && shape_known(c, !have_rowsum)) {
+            if (c.splitk > nch) c.splitk = nch;
+            return c;
+        }
+    }
+    if (M <= 16) {
+        const int w = 16;
+        if (gemv_fits(fmt, M, nch, w, gemv_ncw(w))) {
+            c = MMConfig{1, 1, w, 1, 1};
+            c.kind = 2;
+            return c;
+        }
+        return MMConfig{1, 1, 8, 2, 1};
+    }
+    // Prefill: the LDS GEMM when its activation slice covers K in one
+    // workgroup; otherwise 16 tokens x 64 rows per workgroup with K split
+    // over 4 waves (measured faster than split-K planes plus a reduction).
+    if (have_rowsum && nch <= gemm_ncmax(fmt)) {
+        c = MMConfig{2, 8, 4, 1, 1};
+        c.kind = 1;
+        (void)ntiles_nb1;
         return c;
     }
-    if (M <= 16 || !have_rowsum) {
-        // deeper K split inside the workgroup for long rows
-        return nch > 16 ? MMConfig{1, 1, 8, 2, 1} : MMConfig{1, 1, 4, 4, 1};
-    }
-    (void)ntiles_nb1;
     return MMConfig{1, 4, 4, 2, 1};
 }
 
