@@ -200,6 +200,20 @@ def cpu_baseline(np, wl, budget_s=12.0):
                       f"({t_total:.1f} s), isa={'avx512-vnni' if kernel else 'scalar'}"}
 
 
+def recorded_traffic():
+    """HBM bytes per product launch (FETCH_SIZE + WRITE_SIZE, calibrated)
+    from the committed rocprofv3 summary, or None."""
+    path = os.path.join(ROOT, "profiles", "pmc_traffic_c1.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                kv = dict(t.split("=") for t in line.split(":", 1)[1].split())
+                return {k: int(v) for k, v in kv.items()}
+    except OSError:
+        pass
+    return None
+
+
 def copy_calibration(torch):
     """A plain device copy of known size, for scaling rocprof FETCH/WRITE_SIZE."""
     n = 256 << 20
@@ -270,9 +284,12 @@ def main():
     prod_ms = product_only(np, torch, xtern, wl, reps=max(args.steps, 50))
     prod_ops = [2 * wl["M"] * s["N"] * s["K"] for s in wl["sets"]]
     ach = sum(prod_ops) / (sum(prod_ms) * 1e-3) / 1e12
+    tr = recorded_traffic()
     roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": INT8_PEAK_TOPS,
-            "unit": "TFLOP/s", "frac": round(ach / INT8_PEAK_TOPS, 4), "traffic": None,
-            "kernel": "mm_kernel (ternary x i8 MFMA product)",
+            "unit": "TFLOP/s", "frac": round(ach / INT8_PEAK_TOPS, 4),
+            "traffic": (sum(tr.values()) // len(tr)) if tr else None,
+            "traffic_per_launch": tr,
+            "kernel": "product launches (gemm_kernel up, mm_kernel down)",
             "us_per_launch": {s["name"]: round(m * 1e3, 3) for s, m in zip(wl["sets"], prod_ms)}}
 
     out = {"metric": "ternary GEMM int8 TOPS at M=128 (Pack4, BitNet-2B up+down)",

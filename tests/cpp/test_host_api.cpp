@@ -1,0 +1,179 @@
+// C++ host-API tests, in the shape of xor-net's own Rust tests (file:line of
+// the reference tree in each comment).  `--cpu` runs the codec tests only
+// (no HIP calls); without arguments every test runs and needs the GPU.
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <vector>
+
+#include "../../xor-net_amd/host/xtern.hpp"
+
+using namespace xtern;
+
+static int g_fail = 0;
+#define CHECK(cond, ...)                                               \
+    do {                                                               \
+        if (!(cond)) {                                                 \
+            std::fprintf(stderr, "FAIL %s:%d: %s: ", __FILE__, __LINE__, #cond); \
+            std::fprintf(stderr, __VA_ARGS__);                         \
+            std::fprintf(stderr, "\n");                                \
+            ++g_fail;                                                  \
+        }                                                              \
+    } while (0)
+
+// tests/bit1_58_tests.rs:10-21
+static void test_ternary_pack_unpack_roundtrip() {
+    std::vector<float> w = {1, 0, -1, 1, 0, -1, -1, 0, 1, 1};
+    auto p4 = pack_1_58bit_4pack(w.data(), w.size(), 1.0f);
+    auto p5 = pack_1_58bit_5pack(w.data(), w.size(), 1.0f);
+    CHECK(unpack_1_58bit_4pack(p4.data(), w.size()) == w, "pack4 roundtrip");
+    CHECK(unpack_1_58bit_5pack(p5.data(), w.size()) == w, "pack5 roundtrip");
+}
+
+// tests/quantization_158bit_tests.rs:30-38, :70-77
+static void test_roundtrip_non_aligned_length() {
+    for (size_t n : {1, 2, 3, 5, 6, 7, 9, 11, 13, 15, 17, 21}) {
+        std::vector<float> w(n);
+        for (size_t i = 0; i < n; ++i) w[i] = (float)((int)(i % 3) - 1);
+        auto p4 = pack_1_58bit_4pack(w.data(), n, 1.0f);
+        auto p5 = pack_1_58bit_5pack(w.data(), n, 1.0f);
+        CHECK(unpack_1_58bit_4pack(p4.data(), n) == w, "pack4 len %zu", n);
+        CHECK(unpack_1_58bit_5pack(p5.data(), n) == w, "pack5 len %zu", n);
+    }
+}
+
+// sparse.rs:61-86 layout, hand-computed
+static void test_sparse_row_bytes() {
+    std::vector<int8_t> row(64, 0);
+    row[0] = 1;
+    row[2] = -1;
+    std::vector<uint8_t> buf;
+    encode_sparse_row_into(buf, row.data(), 64);
+    const std::vector<uint8_t> want = {1, 0, 0, 0, 5, 0, 0, 0, 0, 0, 0, 0, 2};
+    CHECK(buf == want, "sparse row bytes");
+}
+
+// tests/bit1_58_tests.rs:25-34
+static void test_absmax_quantization() {
+    FastTensor x(std::vector<float>{0.0f, -2.5f, 5.0f, 1.25f}, {4});
+    auto qi = quantize_f32_to_i8(x);
+    auto q = qi.first.download();
+    auto inv = qi.second.download();
+    CHECK((q == std::vector<int8_t>{0, -64, 127, 32}), "q");
+    CHECK(std::fabs(inv[0] - 5.0f / 127.0f) < 1e-5f, "inv %f", inv[0]);
+    FastTensor z(std::vector<float>{0, 0, 0}, {3});
+    auto zi = quantize_f32_to_i8(z);
+    CHECK(zi.second.download()[0] == 1.0f, "zero inv");
+}
+
+// tests/bit1_58_tests.rs:68-92, with the current scale semantics (w_scale
+// 1.0 for already-ternary weights): dots 191 and -96 times 2/127.
+static void test_ternary_linear_layer() {
+    std::vector<float> w = {1, 0, -1, 1, 0, -1, 1, 0};
+    auto l4 = TernaryLinear::new_(4, 2, w, TernaryPackType::Pack4);
+    auto l5 = TernaryLinear::new_(4, 2, w, TernaryPackType::Pack5);
+    FastTensor x(std::vector<float>{0.5f, 1.0f, -0.5f, 2.0f}, {1, 4});
+    auto o4 = l4.forward(x).data.download();
+    auto o5 = l5.forward(x).data.download();
+    CHECK(o4 == o5, "pack4 == pack5");
+    CHECK(std::fabs(o4[0] - 3.007874f) < 1e-4f && std::fabs(o4[1] + 1.511811f) < 1e-4f,
+          "got %f %f", o4[0], o4[1]);
+}
+
+// tests/linear_layer_tests.rs:66-80 and :82-91
+static void test_linear_parity_and_zero_input() {
+    const size_t K = 20, N = 4;
+    std::vector<float> w(K * N);
+    for (size_t i = 0; i < w.size(); ++i) w[i] = (float)((int)(i % 3) - 1);
+    std::vector<float> xin(K);
+    for (size_t i = 0; i < K; ++i) xin[i] = ((float)i - 10.0f) * 0.1f;
+    FastTensor x(xin, {1, K});
+    auto a = TernaryLinear::new_(K, N, w, TernaryPackType::Pack4).forward(x).data.download();
+    auto b = TernaryLinear::new_(K, N, w, TernaryPackType::Pack5).forward(x).data.download();
+    for (size_t i = 0; i < N; ++i) CHECK(std::fabs(a[i] - b[i]) < 1e-5f, "idx %zu", i);
+    auto z = TernaryLinear::new_(2, 2, {1, -1, 0, 1}, TernaryPackType::Pack4)
+                 .forward(FastTensor(std::vector<float>{0, 0}, {1, 2}))
+                 .data.download();
+    CHECK(z[0] == 0.0f && z[1] == 0.0f, "zero input");
+}
+
+// src/bit1_58/simd.rs:581-625 at layer level: dense Pack4 and XorSparse
+// (built from floats and from the packed bytes) give identical outputs.
+static void test_dense_and_sparse_match() {
+    uint64_t s = 0x123456789abcdef0ull;
+    auto below = [&](uint64_t n) {
+        s = s * 6364136223846793005ull + 1442695040888963407ull;
+        return (s >> 33) % n;
+    };
+    const size_t pairs[][2] = {{2560, 2560}, {6912, 2560}, {2560, 640}, {2560, 6912}};
+    for (auto& kn : pairs) {
+        const size_t K = kn[0], N = kn[1];
+        std::vector<float> w(K * N);
+        for (auto& v : w) v = (float)((int)below(3) - 1);
+        auto dense = TernaryLinear::new_(K, N, w, TernaryPackType::Pack4);
+        auto sparse = TernaryLinear::new_sparse(K, N, w, TernaryPackType::Pack4);
+        auto from_packed = TernaryLinear::new_sparse_from_packed(dense.host_bytes, K, N,
+                                                                 TernaryPackType::Pack4,
+                                                                 dense.w_scales);
+        std::vector<float> xin(2 * K);
+        for (size_t i = 0; i < xin.size(); ++i) xin[i] = (float)((int)below(7) - 3);
+        FastTensor x(xin, {2, K});
+        auto yd = dense.forward(x).data.download();
+        CHECK(sparse.forward(x).data.download() == yd, "sparse K=%zu N=%zu", K, N);
+        CHECK(from_packed.forward(x).data.download() == yd, "from_packed K=%zu N=%zu", K, N);
+    }
+}
+
+// layers.rs:266-272 error texts; layers.rs:347-424 fused QKV
+static void test_errors_and_fused() {
+    std::vector<float> w(256 * 64);
+    for (size_t i = 0; i < w.size(); ++i) w[i] = (float)((int)((i * 7) % 3) - 1);
+    auto l = TernaryLinear::new_(256, 64, w, TernaryPackType::Pack4);
+    bool threw = false;
+    try {
+        l.forward(FastTensor(std::vector<float>(255, 1.0f), {1, 255}));
+    } catch (const Error& e) {
+        threw = std::string(e.what()).find("Input dimension mismatch: expected 256, got 255") != std::string::npos;
+    }
+    CHECK(threw, "dimension mismatch error");
+    threw = false;
+    try {
+        TernaryLinear::new_(256, 65, w, TernaryPackType::Pack4);
+    } catch (const Error& e) {
+        threw = std::string(e.what()) == "Weight length must match in_dim * out_dim";
+    }
+    CHECK(threw, "weight length error");
+
+    std::vector<float> xin(3 * 256);
+    for (size_t i = 0; i < xin.size(); ++i) xin[i] = std::sin(0.37f * (float)i);
+    FastTensor x(xin, {3, 256});
+    auto lk = TernaryLinear::new_(256, 32, std::vector<float>(w.begin(), w.begin() + 256 * 32),
+                                  TernaryPackType::Pack4);
+    auto qi = quantize_f32_to_i8(x);
+    auto fused = TernaryLinear::fused_forward_qkv(x, qi.first.data(), qi.second.data(), l, lk, lk);
+    CHECK(fused.size() == 3 && fused[1].shape == (std::vector<size_t>{3, 32}), "fused shapes");
+    CHECK(fused[0].data.download() == l.forward(x).data.download(), "fused q");
+    CHECK(fused[1].data.download() == lk.forward(x).data.download(), "fused k");
+    CHECK(l.forward_with_quantized(x, qi.first.data(), qi.second.data()).data.download() ==
+              fused[0].data.download(),
+          "forward_with_quantized");
+    DynamicLinear dl(l);
+    CHECK(dl.forward(x).data.download() == fused[0].data.download(), "DynamicLinear");
+}
+
+int main(int argc, char** argv) {
+    const bool cpu_only = argc > 1 && std::strcmp(argv[1], "--cpu") == 0;
+    test_ternary_pack_unpack_roundtrip();
+    test_roundtrip_non_aligned_length();
+    test_sparse_row_bytes();
+    if (!cpu_only) {
+        test_absmax_quantization();
+        test_ternary_linear_layer();
+        test_linear_parity_and_zero_input();
+        test_dense_and_sparse_match();
+        test_errors_and_fused();
+    }
+    std::printf("%s: %d failure(s)\n", cpu_only ? "cpu tests" : "all tests", g_fail);
+    return g_fail ? 1 : 0;
+}

@@ -33,6 +33,24 @@ def hipcc():
     raise RuntimeError("hipcc not found")
 
 
+ROOT = os.path.dirname(HERE)
+CPP_TEST_SRC = os.path.join(ROOT, "tests", "cpp", "test_host_api.cpp")
+CPP_TEST_BIN = os.path.join(ROOT, "tests", "cpp", "test_host_api")
+
+
+def build_cpp_tests(verbose=False):
+    """The C++ host-API test program (links libxtern.so, rpath in-tree)."""
+    cmd = [hipcc(), "-std=c++17", "-O2", "-Wall", CPP_TEST_SRC,
+           "-L" + os.path.dirname(OUT), "-lxtern",
+           "-Wl,-rpath,$ORIGIN/../../xor-net_amd/xtern", "-o", CPP_TEST_BIN]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError("hipcc (C++ tests) failed:\n" + res.stderr)
+    return CPP_TEST_BIN
+
+
 def build(verbose=False):
     cmd = [hipcc()] + HIPCC_FLAGS + [os.path.join(CSRC, s) for s in SOURCES] + ["-o", OUT]
     if verbose:
@@ -49,3 +67,4 @@ def build(verbose=False):
 
 if __name__ == "__main__":
     print(build(verbose="-q" not in sys.argv))
+    print(build_cpp_tests(verbose="-q" not in sys.argv))

@@ -133,6 +133,53 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
     }
 }
 
+// Single-pass variant for K <= 1024 * NV with 16-byte aligned rows: each
+// thread keeps its NV float4 of the row in registers between the absmax
+// reduction and the quantisation, so the row is read from memory once.
+template <int NV>
+__global__ __launch_bounds__(256) void quantize_reg_kernel(const float* __restrict__ x, int64_t ldx,
+                                                           int K, int8_t* __restrict__ q, int ldq,
+                                                           float* __restrict__ inv,
+                                                           int32_t* __restrict__ rowsum, int mode) {
+    __shared__ float sm_f[4];
+    __shared__ int sm_i[4];
+    const int m = blockIdx.x;
+    const float4* x4 = reinterpret_cast<const float4*>(x + (size_t)m * ldx);
+    uint32_t* q4 = reinterpret_cast<uint32_t*>(q + (size_t)m * ldq);
+    const int K4 = K >> 2;
+    float4 v[NV];
+    float mx = 0.0f;
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+        const int i = threadIdx.x + u * 256;
+        v[u] = i < K4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
+    }
+    mx = block_reduce(mx, MaxOp(), sm_f);
+    const float scale = (mx > 0.0f) ? __fdiv_rn(127.0f, mx) : 1.0f;
+    const float invs = (mx > 0.0f) ? __fdiv_rn(mx, 127.0f) : 1.0f;
+    const int kmain = (K / 16) * 16;
+    int sum = 0;
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+        const int i = threadIdx.x + u * 256;
+        if (i >= K4) continue;
+        const float e[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+        int b[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) b[t] = quant_one(e[t], scale, mode, 4 * i + t < kmain);
+        sum += b[0] + b[1] + b[2] + b[3];
+        q4[i] = (uint32_t)(b[0] & 255) | ((uint32_t)(b[1] & 255) << 8) |
+                ((uint32_t)(b[2] & 255) << 16) | ((uint32_t)(b[3] & 255) << 24);
+    }
+    for (int i = K4 + threadIdx.x; i < (ldq >> 2); i += 256) q4[i] = 0u;  // padding
+    sum = block_reduce(sum, AddOp(), sm_i);
+    if (threadIdx.x == 0) {
+        inv[m] = invs;
+        if (rowsum) rowsum[m] = sum;
+    }
+}
+
 // Row sums of caller-provided i8 activations, optionally copying them into a
 // zero-padded buffer with a 16-byte aligned stride.
 __global__ __launch_bounds__(256) void rowsum_kernel(const int8_t* __restrict__ qin, int64_t ldin,
@@ -155,6 +202,22 @@ __global__ __launch_bounds__(256) void rowsum_kernel(const int8_t* __restrict__ 
 hipError_t launch_quantize(const float* x, int64_t ldx, int M, int K, int8_t* q, int ldq,
                            float* inv, int32_t* rowsum, int mode, hipStream_t s) {
     if (M <= 0) return hipSuccess;
+    const bool aligned = (K % 4 == 0) && (ldx % 4 == 0) && (ldq % 4 == 0) &&
+                         ((uintptr_t)x % 16 == 0) && ((uintptr_t)q % 4 == 0);
+    if (aligned && K <= 16384) {
+#define XT_QREG(NV_)                                                                            \
+    if (K <= 1024 * NV_) {                                                                      \
+        hipLaunchKernelGGL(quantize_reg_kernel<NV_>, dim3(M), dim3(256), 0, s, x, ldx, K, q, ldq, \
+                           inv, rowsum, mode);                                                  \
+        return hipGetLastError();                                                               \
+    }
+        XT_QREG(1)
+        XT_QREG(2)
+        XT_QREG(4)
+        XT_QREG(8)
+        XT_QREG(16)
+#undef XT_QREG
+    }
     hipLaunchKernelGGL(quantize_kernel, dim3(M), dim3(256), 0, s, x, ldx, K, q, ldq, inv, rowsum,
                        mode);
     return hipGetLastError();
