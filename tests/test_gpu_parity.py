@@ -92,7 +92,8 @@ def test_quantize_exact(M, K, mode):
 @pytest.mark.parametrize("fmt", FMTS, ids=FMT_ID.get)
 @pytest.mark.parametrize("K,N,M", [(256, 16, 1), (300, 37, 3), (64, 1, 1), (5, 3, 2),
                                    (2560, 96, 16), (1000, 50, 17), (640, 64, 40),
-                                   (1281, 33, 128), (320, 16, 5)])
+                                   (1281, 33, 128), (320, 16, 5), (4000, 48, 20),
+                                   (7168, 80, 33)])
 def test_linear_q_matches_oracle(fmt, K, N, M):
     log(f"linear_q fmt={FMT_ID[fmt]} K={K} N={N} M={M}")
     rng = np.random.default_rng(K + 7 * N + 13 * M + fmt)
