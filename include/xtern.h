@@ -76,6 +76,35 @@ const char* xt_last_error(void);
 int xt_weights_create(int fmt, int64_t in_dim, int64_t out_dim, const void* host_bytes,
                       size_t nbytes, const float* w_scales, xt_weights** out);
 
+/* HF prepacked checkpoints (U8, output-dim striped): `stored` holds the
+ * [out_dim/f][in_dim] bytes of the safetensors tensor, f = 4 (XT_PACK4) or
+ * 5 (XT_PACK5); digit j of byte [p][i] is the weight of output row
+ * j*(out_dim/f) + p at input column i.
+ *
+ * xt_hf_destripe writes the input-dim packed rows, out_dim * ceil(in_dim/f)
+ * bytes, byte-identical to what get_prepacked_ternary returns
+ * (src/loader/mod.rs:301-394, the unpack/transpose/repack of :351-390), so
+ * they can be passed to xt_weights_create or kept on the host.
+ *
+ * xt_weights_create_hf uploads the striped bytes and builds the device tiles
+ * on the GPU (no host transpose); w_scales are out_dim copies of
+ * `weight_scale`, or of 1.0f / weight_scale when is_inverted_scale != 0
+ * (:340-347, :392).  Together with xt_weights_create it replaces the
+ * get_prepacked_ternary -> DynamicLinear::new_ternary_direct chain of
+ * DynamicLinear::load (src/nn/dynamic_linear.rs:729-741).  Both reject a byte
+ * count other than in_dim * out_dim / f, or out_dim not a multiple of f, as
+ * the loader's is_packed check does (:324-331). */
+int xt_hf_destripe(int fmt, int64_t in_dim, int64_t out_dim, const void* stored, size_t nbytes,
+                   void* packed_out);
+int xt_weights_create_hf(int fmt, int64_t in_dim, int64_t out_dim, const void* stored,
+                         size_t nbytes, float weight_scale, int is_inverted_scale,
+                         xt_weights** out);
+
+/* Copy a handle's device tiles (xt_tile_bytes() bytes) to host memory, after
+ * waiting for the device.  No reference counterpart: lets tests compare
+ * tiles built on the device with xt_repack_host's. */
+int xt_weights_read_tiles(const xt_weights* w, void* host_out, size_t nbytes);
+
 /* Free a handle (NULL is a no-op).  Waits for the device first. */
 int xt_weights_destroy(xt_weights* w);
 

@@ -40,6 +40,8 @@ _o.or_linear_forward.argtypes = [ctypes.c_int, _vp, _vp, _vp, _vp, _i64, _i64, _
                                  _vp, _vp, _vp, ctypes.c_int, ctypes.c_int, ctypes.c_int]
 _o.or_linear_forward_q.argtypes = [ctypes.c_int, _vp, _vp, _vp, _vp, _i64, _i64, _vp, _vp, _i64,
                                    _vp, _vp]
+_o.or_hf_destripe.argtypes = [ctypes.c_int, _i64, _i64, _vp, _vp]
+_o.or_hf_destripe.restype = ctypes.c_int
 _o.or_lcg_next.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
 _o.or_lcg_next.restype = ctypes.c_uint64
 _o.or_cpu_has_vnni.restype = ctypes.c_int
@@ -179,6 +181,16 @@ def linear_forward_q(fmt, K, N, q, inv, w_scales, wbytes=None, masks=None, signs
     _o.or_linear_forward_q(fmt, _p(wb), _p(mk), _p(sg), _p(_c(w_scales, np.float32)), K, N,
                            _p(q), _p(inv), M, _p(y), _p(acc))
     return y, acc
+
+
+def hf_destripe(fmt, in_dim, out_dim, stored):
+    """loader/mod.rs:301-394 destripe -> input-dim packed rows."""
+    f = 5 if fmt == 1 else 4
+    st = _c(stored, np.uint8)
+    out = np.zeros(out_dim * ((in_dim + f - 1) // f), np.uint8)
+    if _o.or_hf_destripe(fmt, in_dim, out_dim, _p(st), _p(out)) != 0:
+        raise ValueError("out_dim must be a multiple of the pack factor")
+    return out
 
 
 class Lcg:

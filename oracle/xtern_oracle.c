@@ -13,6 +13,7 @@
 #include <immintrin.h>
 #include <math.h>
 #include <omp.h>
+#include <stdlib.h>
 #include <string.h>
 #include <unistd.h>
 
@@ -434,6 +435,39 @@ void or_linear_forward_q(int fmt, const uint8_t* wbytes, const uint64_t* masks,
             float t = (float)d * inv[m];
             y[m * N + o] = t * w_scales[o];
         }
+}
+
+/* loader/mod.rs:355-389: unpack the whole stored stream linearly
+ * (unpack_1_58bit_{4,5}pack), scatter value k to row j*stored_rows + p,
+ * column i (byte k/f = p*in_dim + i, j = k % f), then pack each row at
+ * scale 1.0. */
+int or_hf_destripe(int fmt, int64_t in_dim, int64_t out_dim, const uint8_t* stored,
+                   uint8_t* out_packed) {
+    const int64_t f = fmt == 1 ? 5 : 4;
+    if (out_dim % f) return -1;
+    const int64_t n = in_dim * out_dim, stored_rows = out_dim / f;
+    float* flat = (float*)malloc((size_t)n * sizeof(float));
+    float* rows = (float*)malloc((size_t)n * sizeof(float));
+    if (!flat || !rows) {
+        free(flat);
+        free(rows);
+        return -1;
+    }
+    if (fmt == 1) or_unpack5(stored, n, flat);
+    else or_unpack4(stored, n, flat);
+    for (int64_t k = 0; k < n; ++k) {
+        const int64_t byte_idx = k / f, j = k % f;
+        const int64_t row_p = byte_idx / in_dim, col = byte_idx % in_dim;
+        rows[(j * stored_rows + row_p) * in_dim + col] = flat[k];
+    }
+    const int64_t bpr = (in_dim + f - 1) / f;
+    for (int64_t o = 0; o < out_dim; ++o) {
+        if (fmt == 1) or_pack5(rows + o * in_dim, in_dim, 1.0f, out_packed + o * bpr);
+        else or_pack4(rows + o * in_dim, in_dim, 1.0f, out_packed + o * bpr);
+    }
+    free(flat);
+    free(rows);
+    return 0;
 }
 
 /* simd.rs:556-565: x = x*6364136223846793005 + 1442695040888963407; x >> 33. */

@@ -79,6 +79,15 @@ void or_linear_forward_q(int fmt, const uint8_t* wbytes, const uint64_t* masks,
                          int64_t N, const int8_t* q, const float* inv, int64_t M,
                          float* y, int32_t* acc);
 
+/* ---- HF prepacked weights: src/loader/mod.rs:301-394 ----
+ * `stored` is the checkpoint's U8 tensor [out_dim/f][in_dim] (f = 4 for Pack4,
+ * 5 for Pack5) whose byte [p][i] holds output rows j*(out_dim/f) + p for
+ * j < f.  Writes the input-dim packed rows get_prepacked_ternary returns
+ * ([out_dim][ceil(in_dim/f)] bytes, packed at scale 1.0).  Returns 0, or -1
+ * when out_dim is not a multiple of f. */
+int or_hf_destripe(int fmt, int64_t in_dim, int64_t out_dim, const uint8_t* stored,
+                   uint8_t* out_packed);
+
 /* ---- the reference's deterministic test RNG: simd.rs:556-565 ---- */
 uint64_t or_lcg_next(uint64_t* state);
 

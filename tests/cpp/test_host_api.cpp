@@ -162,12 +162,59 @@ static void test_errors_and_fused() {
     CHECK(dl.forward(x).data.download() == fused[0].data.download(), "DynamicLinear");
 }
 
+// loader/mod.rs:301-394: striped bytes -> the same layer as its destriped rows.
+// Rows 0..7 of a K=3 matrix striped over R = 2 stored rows (Pack4).
+static void test_hf_prepacked() {
+    const int8_t t[8][3] = {{1, 0, -1}, {0, 1, 1}, {-1, -1, 0}, {1, 1, 1},
+                            {0, 0, 0},  {-1, 1, 0}, {1, -1, 1}, {0, -1, -1}};
+    std::vector<uint8_t> stored(2 * 3, 0);
+    for (int o = 0; o < 8; ++o)
+        for (int i = 0; i < 3; ++i)
+            stored[(o % 2) * 3 + i] |= (uint8_t)((t[o][i] + 1) << (2 * (o / 2)));
+    auto pp = get_prepacked_ternary(stored.data(), stored.size(), 8, 3, TernaryPackType::Pack4,
+                                    0.25f, true);
+    for (int o = 0; o < 8; ++o) {
+        auto row = unpack_1_58bit_4pack(pp.packed.data() + o, 3);
+        for (int i = 0; i < 3; ++i) CHECK(row[i] == (float)t[o][i], "row %d col %d", o, i);
+    }
+    CHECK(pp.w_scales.size() == 8 && pp.w_scales[0] == 4.0f, "inverted scale");
+    bool threw = false;
+    try {
+        get_prepacked_ternary(stored.data(), 5, 8, 3, TernaryPackType::Pack4, 1.0f, false);
+    } catch (const Error& e) {
+        threw = std::string(e.what()).find("pre-packed U8") != std::string::npos;
+    }
+    CHECK(threw, "bad byte count");
+}
+
+static void test_hf_prepacked_layer() {
+    std::vector<uint8_t> stored(160 * 2560);
+    uint64_t s = 0x9e3779b97f4a7c15ull;
+    for (auto& b : stored) {
+        s = s * 6364136223846793005ull + 1442695040888963407ull;
+        b = (uint8_t)(s >> 33);
+    }
+    auto hf = TernaryLinear::from_hf_prepacked(stored.data(), stored.size(), 2560, 640,
+                                               TernaryPackType::Pack4, 0.5f, false);
+    auto pp = get_prepacked_ternary(stored.data(), stored.size(), 640, 2560,
+                                    TernaryPackType::Pack4, 0.5f, false);
+    auto direct = TernaryLinear::new_direct(pp.packed, 2560, 640, TernaryPackType::Pack4,
+                                            pp.w_scales);
+    CHECK(hf.packed_bytes() == direct.packed_bytes(), "packed_bytes");
+    std::vector<float> xin(3 * 2560);
+    for (size_t i = 0; i < xin.size(); ++i) xin[i] = std::cos(0.11f * (float)i);
+    FastTensor x(xin, {3, 2560});
+    CHECK(hf.forward(x).data.download() == direct.forward(x).data.download(), "hf layer");
+}
+
 int main(int argc, char** argv) {
     const bool cpu_only = argc > 1 && std::strcmp(argv[1], "--cpu") == 0;
     test_ternary_pack_unpack_roundtrip();
     test_roundtrip_non_aligned_length();
     test_sparse_row_bytes();
+    test_hf_prepacked();
     if (!cpu_only) {
+        test_hf_prepacked_layer();
         test_absmax_quantization();
         test_ternary_linear_layer();
         test_linear_parity_and_zero_input();

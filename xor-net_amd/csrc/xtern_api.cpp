@@ -266,6 +266,35 @@ int xt_repack_host(int fmt, int64_t in_dim, int64_t out_dim, const void* host_by
     return XT_OK;
 }
 
+namespace {
+
+// A handle with device memory for `fmt`'s tiles and N scales (scales
+// uploaded, tiles left for the caller to fill).
+int weights_alloc(int fmt, int64_t K, int64_t N, const float* w_scales, xt_weights** out) {
+    xt_weights* w = new (std::nothrow) xt_weights();
+    if (!w) return fail(XT_ERR_NOMEM, "handle");
+    w->fmt = fmt;
+    w->K = K;
+    w->N = N;
+    w->nch = (K + xt::chunk_cols(fmt) - 1) / xt::chunk_cols(fmt);
+    w->tile_bytes = xt::tile_bytes(fmt, K, N);
+    hipError_t e = hipGetDevice(&w->device);
+    if (e == hipSuccess) e = hipMalloc(&w->tiles, w->tile_bytes);
+    if (e == hipSuccess) e = hipMalloc(&w->ws, (size_t)N * sizeof(float));
+    if (e == hipSuccess)
+        e = hipMemcpy(w->ws, w_scales, (size_t)N * sizeof(float), hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        if (w->tiles) (void)hipFree(w->tiles);
+        if (w->ws) (void)hipFree(w->ws);
+        delete w;
+        return hip_fail(e, "weight allocation");
+    }
+    *out = w;
+    return XT_OK;
+}
+
+}  // namespace
+
 int xt_weights_create(int fmt, int64_t in_dim, int64_t out_dim, const void* host_bytes,
                       size_t nbytes, const float* w_scales, xt_weights** out) {
     if (!out) return fail(XT_ERR_INVALID, "out is NULL");
@@ -283,26 +312,87 @@ int xt_weights_create(int fmt, int64_t in_dim, int64_t out_dim, const void* host
     std::string err;
     if (xt::repack(fmt, in_dim, out_dim, host_bytes, nbytes, host.data(), &err))
         return fail(XT_ERR_INVALID, err);
-    xt_weights* w = new (std::nothrow) xt_weights();
-    if (!w) return fail(XT_ERR_NOMEM, "handle");
-    w->fmt = fmt;
-    w->K = in_dim;
-    w->N = out_dim;
-    w->nch = (in_dim + xt::chunk_cols(fmt) - 1) / xt::chunk_cols(fmt);
-    w->tile_bytes = tb;
-    hipError_t e = hipGetDevice(&w->device);
-    if (e == hipSuccess) e = hipMalloc(&w->tiles, tb);
-    if (e == hipSuccess) e = hipMalloc(&w->ws, (size_t)out_dim * sizeof(float));
-    if (e == hipSuccess) e = hipMemcpy(w->tiles, host.data(), tb, hipMemcpyHostToDevice);
-    if (e == hipSuccess)
-        e = hipMemcpy(w->ws, w_scales, (size_t)out_dim * sizeof(float), hipMemcpyHostToDevice);
+    xt_weights* w = nullptr;
+    if (int rc = weights_alloc(fmt, in_dim, out_dim, w_scales, &w)) return rc;
+    hipError_t e = hipMemcpy(w->tiles, host.data(), tb, hipMemcpyHostToDevice);
     if (e != hipSuccess) {
-        if (w->tiles) (void)hipFree(w->tiles);
-        if (w->ws) (void)hipFree(w->ws);
-        delete w;
+        (void)xt_weights_destroy(w);
         return hip_fail(e, "weight upload");
     }
     *out = w;
+    return XT_OK;
+}
+
+int xt_hf_destripe(int fmt, int64_t in_dim, int64_t out_dim, const void* stored, size_t nbytes,
+                   void* packed_out) {
+    if (!stored || !packed_out) return fail(XT_ERR_INVALID, "NULL buffer");
+    std::string err;
+    if (xt::hf_destripe(fmt, in_dim, out_dim, static_cast<const uint8_t*>(stored), nbytes,
+                        static_cast<uint8_t*>(packed_out), &err))
+        return fail(XT_ERR_INVALID, err);
+    return XT_OK;
+}
+
+int xt_weights_create_hf(int fmt, int64_t in_dim, int64_t out_dim, const void* stored,
+                         size_t nbytes, float weight_scale, int is_inverted_scale,
+                         xt_weights** out) {
+    if (!out) return fail(XT_ERR_INVALID, "out is NULL");
+    *out = nullptr;
+    if (!stored) return fail(XT_ERR_INVALID, "NULL weight bytes");
+    if (fmt != XT_PACK4 && fmt != XT_PACK5)
+        return fail(XT_ERR_INVALID, "HF prepacked weights are Pack4 or Pack5 only");
+    if (in_dim <= 0 || out_dim <= 0) return fail(XT_ERR_INVALID, "in_dim and out_dim must be positive");
+    if (in_dim > (int64_t)1 << 30 || out_dim > (int64_t)1 << 30)
+        return fail(XT_ERR_UNSUPPORTED, "in_dim/out_dim above 2^30 are not supported");
+    const int64_t f = fmt == XT_PACK5 ? 5 : 4;
+    if (out_dim % f != 0 || (uint64_t)nbytes != (uint64_t)(in_dim * (out_dim / f)))
+        return fail(XT_ERR_INVALID,
+                    "Tensor is not in pre-packed U8 ternary format: expected [" +
+                        std::to_string(out_dim / f) + "][" + std::to_string(in_dim) +
+                        "] bytes for out_dim " + std::to_string(out_dim) + ", got " +
+                        std::to_string(nbytes));
+    // loader/mod.rs:343-347 (f32 division) and :392 (one scale per row).
+    const float ws = is_inverted_scale ? 1.0f / weight_scale : weight_scale;
+    std::vector<float> scales;
+    try {
+        scales.assign((size_t)out_dim, ws);
+    } catch (...) {
+        return fail(XT_ERR_NOMEM, "host scale buffer");
+    }
+    xt_weights* w = nullptr;
+    if (int rc = weights_alloc(fmt, in_dim, out_dim, scales.data(), &w)) return rc;
+    void* dstored = nullptr;
+    hipError_t e = hipMalloc(&dstored, nbytes);
+    if (e == hipSuccess) e = hipMemcpy(dstored, stored, nbytes, hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = xt::launch_hf_tiles(fmt, static_cast<const uint8_t*>(dstored), in_dim, out_dim, w->tiles,
+                                nullptr);
+    if (e == hipSuccess) e = hipStreamSynchronize(nullptr);
+    if (dstored) {
+        hipError_t ef = hipFree(dstored);
+        if (e == hipSuccess) e = ef;
+    }
+    if (e != hipSuccess) {
+        (void)xt_weights_destroy(w);
+        return hip_fail(e, "HF weight upload");
+    }
+    *out = w;
+    return XT_OK;
+}
+
+int xt_weights_read_tiles(const xt_weights* w, void* host_out, size_t nbytes) {
+    if (check_weights(w)) return XT_ERR_INVALID;
+    if (!host_out) return fail(XT_ERR_INVALID, "NULL buffer");
+    if (nbytes < w->tile_bytes)
+        return fail(XT_ERR_INVALID, "buffer holds " + std::to_string(nbytes) + " bytes, tiles need " +
+                                        std::to_string(w->tile_bytes));
+    int prev = 0;
+    XT_HIP(hipGetDevice(&prev));
+    if (prev != w->device) XT_HIP(hipSetDevice(w->device));
+    hipError_t e = hipDeviceSynchronize();
+    if (e == hipSuccess) e = hipMemcpy(host_out, w->tiles, w->tile_bytes, hipMemcpyDeviceToHost);
+    if (prev != w->device) (void)hipSetDevice(prev);
+    if (e != hipSuccess) return hip_fail(e, "read tiles");
     return XT_OK;
 }
 

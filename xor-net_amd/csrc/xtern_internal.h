@@ -70,5 +70,8 @@ int gemm_ncmax(int fmt);
 hipError_t launch_gemm(int fmt, const MMArgs& a, int ntiles, int splitk, hipStream_t s);
 // Decode GEMV (M <= 16): 16 output rows per workgroup, activations in LDS.
 hipError_t launch_gemv(int fmt, const MMArgs& a, int ntiles, int waves, hipStream_t s);
+// HF prepacked striped bytes [N/f][K] (device) -> tiles (device).
+hipError_t launch_hf_tiles(int fmt, const uint8_t* stored, int64_t K, int64_t N, uint8_t* tiles,
+                           hipStream_t s);
 
 }  // namespace xt

@@ -1051,4 +1051,86 @@ hipError_t launch_mm(int fmt, const MMConfig& cfg, const MMArgs& a, int ntiles_t
     return hipErrorInvalidValue;
 }
 
+// ---------------------------------------------------------------------------
+// HF prepacked weights -> device tiles (src/loader/mod.rs:301-394)
+// ---------------------------------------------------------------------------
+
+// The checkpoint stores U8 bytes [R][K], R = N/f, whose digit j (Pack4: bits
+// 2j..2j+1, Pack5: base-3 digit j) of byte [p][i] is the weight of output row
+// j*R + p at input column i.  One thread builds the 16 bytes of one lane of
+// one tile (geometry in xtern_internal.h), reading the digits it needs
+// straight from the striped bytes, so the loader's host-side unpack /
+// transpose / repack is not needed.  Pack4 code 11 reads as weight 0, as
+// unpack_1_58bit_4pack does (quantization.rs:36-41); Pack5 digits are the
+// repeated %3, /3 of unpack_1_58bit_5pack (:72-91).
+template <int FMT>
+__global__ void __launch_bounds__(256)
+hf_tiles_kernel(const uint8_t* __restrict__ stored, int64_t K, int64_t N, int64_t R, int64_t nch,
+                int64_t nlanes, uint8_t* __restrict__ tiles) {
+    const int64_t t = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (t >= nlanes) return;
+    const int lane = (int)(t & 63);
+    const int64_t tile = t >> 6;
+    const int64_t G = tile / nch, c = tile % nch;
+    const int g = lane >> 4, jr = lane & 15;
+    const int64_t o = G * 16 + jr;
+    const bool row_ok = o < N;
+    const int64_t js = row_ok ? o / R : 0, p = row_ok ? o % R : 0;
+    const uint8_t* src = stored + p * K;
+    uint32_t out[4];
+    if constexpr (FMT == XT_PACK5) {
+        const unsigned div = js == 0 ? 1u : js == 1 ? 3u : js == 2 ? 9u : js == 3 ? 27u : 81u;
+        uint8_t bytes[16];
+#pragma unroll
+        for (int b = 0; b < 16; ++b) {
+            unsigned v = 0;
+#pragma unroll
+            for (int st = 0; st < 5; ++st) {
+                const int64_t k = c * 320 + st * 64 + g * 16 + b;
+                const unsigned code = (row_ok && k < K) ? (src[k] / div) % 3u : 1u;
+                v = v * 3u + code;
+            }
+            bytes[b] = (uint8_t)((v * 256u + 242u) / 243u);
+        }
+#pragma unroll
+        for (int w = 0; w < 4; ++w)
+            out[w] = (uint32_t)bytes[4 * w] | ((uint32_t)bytes[4 * w + 1] << 8) |
+                     ((uint32_t)bytes[4 * w + 2] << 16) | ((uint32_t)bytes[4 * w + 3] << 24);
+    } else {
+        const int sh = (int)(2 * js);
+#pragma unroll
+        for (int st = 0; st < 4; ++st) {
+            uint32_t d = 0;
+#pragma unroll
+            for (int b = 0; b < 16; ++b) {
+                const int64_t k = c * 256 + st * 64 + g * 16 + b;
+                unsigned code = 1u;
+                if (row_ok && k < K) {
+                    const unsigned f = (src[k] >> sh) & 3u;
+                    code = f == 0u ? 0u : (f == 2u ? 2u : 1u);
+                }
+                d |= code << (8 * (b & 3) + 2 * (b >> 2));
+            }
+            out[st] = d;
+        }
+    }
+    *reinterpret_cast<uint4*>(tiles + t * 16) = make_uint4(out[0], out[1], out[2], out[3]);
+}
+
+hipError_t launch_hf_tiles(int fmt, const uint8_t* stored, int64_t K, int64_t N, uint8_t* tiles,
+                           hipStream_t s) {
+    const int64_t f = fmt == XT_PACK5 ? 5 : 4;
+    const int64_t nch = (K + chunk_cols(fmt) - 1) / chunk_cols(fmt);
+    const int64_t nlanes = (N + 15) / 16 * nch * 64;
+    const int64_t blocks = (nlanes + 255) / 256;
+    if (blocks > 0x7fffffff) return hipErrorInvalidValue;
+    if (fmt == XT_PACK5)
+        hipLaunchKernelGGL(hf_tiles_kernel<XT_PACK5>, dim3((unsigned)blocks), dim3(256), 0, s,
+                           stored, K, N, N / f, nch, nlanes, tiles);
+    else
+        hipLaunchKernelGGL(hf_tiles_kernel<XT_PACK4>, dim3((unsigned)blocks), dim3(256), 0, s,
+                           stored, K, N, N / f, nch, nlanes, tiles);
+    return hipGetLastError();
+}
+
 }  // namespace xt

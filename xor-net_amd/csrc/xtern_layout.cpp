@@ -155,6 +155,47 @@ int repack_pack5(int64_t K, int64_t N, const uint8_t* src, size_t nbytes, uint8_
 
 }  // namespace
 
+// loader/mod.rs:351-390 without the f32 round trip: the value of (row o,
+// column i) is digit j of stored byte [p][i] with o = j*R + p, R = N/f; it
+// is re-emitted in input-dim order exactly as pack_1_58bit_{4,5}pack at
+// scale 1.0 would (quantization.rs:7-70): Pack4 code 11 becomes 01, unused
+// high fields / digits of a row's last byte stay 0.
+int hf_destripe(int fmt, int64_t K, int64_t N, const uint8_t* stored, size_t nbytes,
+                uint8_t* out, std::string* err) {
+    if (fmt != 0 && fmt != 1) {
+        *err = "HF prepacked weights are Pack4 or Pack5 only";
+        return -1;
+    }
+    const int64_t f = fmt == 1 ? 5 : 4;
+    if (K <= 0 || N <= 0 || N % f != 0 || (uint64_t)nbytes != (uint64_t)(K * (N / f))) {
+        *err = "Tensor is not in pre-packed U8 ternary format: expected [" + std::to_string(N / f) +
+               "][" + std::to_string(K) + "] bytes for out_dim " + std::to_string(N) +
+               " (a multiple of " + std::to_string(f) + "), got " + std::to_string(nbytes);
+        return -1;
+    }
+    const int64_t R = N / f, bpr = (K + f - 1) / f;
+    static const unsigned pow3[5] = {1, 3, 9, 27, 81};
+    for (int64_t o = 0; o < N; ++o) {
+        const int64_t j = o / R, p = o % R;
+        const uint8_t* src = stored + p * K;
+        uint8_t* dst = out + o * bpr;
+        for (int64_t c = 0; c < bpr; ++c) {
+            unsigned b = 0;
+            for (int64_t t = 0; t < f && c * f + t < K; ++t) {
+                const unsigned x = src[c * f + t];
+                if (fmt == 0) {
+                    const unsigned code = canon4((x >> (2 * j)) & 3u);
+                    b |= code << (2 * t);
+                } else {
+                    b += ((x / pow3[j]) % 3u) * pow3[t];
+                }
+            }
+            dst[c] = (uint8_t)b;
+        }
+    }
+    return 0;
+}
+
 int repack(int fmt, int64_t K, int64_t N, const void* src, size_t nbytes, void* dst,
            std::string* err) {
     if (K <= 0 || N <= 0) {

@@ -12,4 +12,8 @@ size_t tile_bytes(int fmt, int64_t K, int64_t N);
 // Returns 0, or -1 with *err set.
 int repack(int fmt, int64_t K, int64_t N, const void* src, size_t nbytes, void* dst,
            std::string* err);
+// HF prepacked (output-dim striped) bytes [N/f][K] -> input-dim packed rows
+// [N][ceil(K/f)], f = 4 (fmt 0) or 5 (fmt 1).  Returns 0, or -1 with *err set.
+int hf_destripe(int fmt, int64_t K, int64_t N, const uint8_t* stored, size_t nbytes,
+                uint8_t* out, std::string* err);
 }  // namespace xt

@@ -205,6 +205,31 @@ inline std::pair<DeviceBuffer<int8_t>, DeviceBuffer<float>> quantize_f32_to_i8(
     return {std::move(q), std::move(inv)};
 }
 
+// ------------------------------------------------------------ HF loader
+
+// VarBuilder::get_prepacked_ternary (loader/mod.rs:301-394) on tensor bytes
+// already read from the checkpoint: `stored` is the U8 [out_dim/f][in_dim]
+// tensor, `weight_scale` the first element of its weight_scale companion.
+struct PrepackedTernary {
+    std::vector<uint8_t> packed;  // input-dim packed rows [out_dim][ceil(in_dim/f)]
+    std::vector<float> w_scales;  // out_dim copies of the (inverted) scale
+    size_t in_dim, out_dim;
+};
+
+inline PrepackedTernary get_prepacked_ternary(const uint8_t* stored, size_t nbytes,
+                                              size_t out_dim, size_t in_dim, TernaryPackType pt,
+                                              float weight_scale, bool is_inverted_scale) {
+    const size_t f = pt == TernaryPackType::Pack4 ? 4 : 5;
+    PrepackedTernary r;
+    r.packed.resize(out_dim * ((in_dim + f - 1) / f));
+    check(xt_hf_destripe((int)pt, (int64_t)in_dim, (int64_t)out_dim, stored, nbytes,
+                         r.packed.data()));
+    r.w_scales.assign(out_dim, is_inverted_scale ? 1.0f / weight_scale : weight_scale);
+    r.in_dim = in_dim;
+    r.out_dim = out_dim;
+    return r;
+}
+
 // ------------------------------------------------------------ layers
 
 enum class TernaryRep { Dense, Sparse };  // layers.rs:23-27
@@ -297,8 +322,27 @@ class TernaryLinear {
                              std::move(packed));
     }
 
-    // layers.rs:234-239
-    size_t packed_bytes() const { return host_bytes.size(); }
+    // DynamicLinear::load's prepacked arm (dynamic_linear.rs:729-741): the
+    // tiles are built on the device from the striped bytes
+    // (xt_weights_create_hf); host_bytes stays empty.
+    static TernaryLinear from_hf_prepacked(const uint8_t* stored, size_t nbytes, size_t in_dim,
+                                           size_t out_dim, TernaryPackType pt,
+                                           float weight_scale, bool is_inverted_scale) {
+        xt_weights* h = nullptr;
+        check(xt_weights_create_hf((int)pt, (int64_t)in_dim, (int64_t)out_dim, stored, nbytes,
+                                   weight_scale, is_inverted_scale ? 1 : 0, &h));
+        std::vector<float> ws(out_dim, is_inverted_scale ? 1.0f / weight_scale : weight_scale);
+        return TernaryLinear(pt, in_dim, out_dim, std::move(ws), h);
+    }
+
+    // layers.rs:234-239 (Dense: out_dim * ceil(in_dim/f); Sparse: blob bytes)
+    size_t packed_bytes() const {
+        if (rep == TernaryRep::Dense && host_bytes.empty()) {
+            const size_t f = pack_type == TernaryPackType::Pack4 ? 4 : 5;
+            return out_dim * ((in_dim + f - 1) / f);
+        }
+        return host_bytes.size();
+    }
 
     // layers.rs:262-313
     FastTensor forward(const FastTensor& xs, bool scalar_rounding = false,
@@ -356,6 +400,12 @@ class TernaryLinear {
         const int fmt = r == TernaryRep::Sparse ? XT_XORSPARSE : (int)pt;
         check(xt_weights_create(fmt, (int64_t)in_dim, (int64_t)out_dim, host_bytes.data(),
                                 host_bytes.size(), w_scales.data(), &h));
+        w_.reset(h, Deleter());
+    }
+
+    TernaryLinear(TernaryPackType pt, size_t in, size_t out, std::vector<float> ws, xt_weights* h)
+        : rep(TernaryRep::Dense), in_dim(in), out_dim(out), pack_type(pt),
+          w_scales(std::move(ws)) {
         w_.reset(h, Deleter());
     }
 

@@ -29,6 +29,16 @@ if not os.path.exists(LIB_PATH):
         f"libxtern.so not found at {LIB_PATH}; build it with "
         "`python xor-net_amd/build_lib.py` (or __graft_entry__.build())")
 
+# torch bundles its own HIP runtime.  Loading libxtern.so first would bring
+# ROCm's copy into the process ahead of torch's and the two then disagree
+# about the device ("No HIP GPUs are available" / "no ROCm-capable device").
+# Importing torch first makes libxtern bind to the runtime torch already
+# loaded, so both share one device context.
+try:
+    import torch as _torch_mod  # noqa: F401
+except ImportError:  # the C ABI itself does not need torch
+    _torch_mod = None
+
 _lib = ctypes.CDLL(LIB_PATH)
 
 XT_OK = 0
@@ -53,6 +63,10 @@ _lib.xt_weights_info.argtypes = [_vp, ctypes.POINTER(ctypes.c_int), ctypes.POINT
 _lib.xt_tile_bytes.argtypes = [ctypes.c_int, _i64, _i64]
 _lib.xt_tile_bytes.restype = _sz
 _lib.xt_repack_host.argtypes = [ctypes.c_int, _i64, _i64, _vp, _sz, _vp]
+_lib.xt_hf_destripe.argtypes = [ctypes.c_int, _i64, _i64, _vp, _sz, _vp]
+_lib.xt_weights_create_hf.argtypes = [ctypes.c_int, _i64, _i64, _vp, _sz, ctypes.c_float,
+                                      ctypes.c_int, ctypes.POINTER(_vp)]
+_lib.xt_weights_read_tiles.argtypes = [_vp, _vp, _sz]
 _lib.xt_quantize_i8.argtypes = [_vp, _i64, _i64, _vp, _vp, ctypes.c_int, _vp]
 _lib.xt_quantize_i8_rowsum.argtypes = [_vp, _i64, _i64, _vp, _vp, _vp, ctypes.c_int, _vp]
 _lib.xt_ternary_linear_q.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp, _vp]
@@ -240,6 +254,26 @@ class DeviceWeights:
         self.handle = h
         self.fmt, self.in_dim, self.out_dim = fmt, in_dim, out_dim
 
+    @classmethod
+    def from_hf(cls, fmt, in_dim, out_dim, stored, weight_scale, is_inverted_scale=False):
+        """xt_weights_create_hf: tiles built on the device from the HF
+        checkpoint's output-dim striped bytes [out_dim/f][in_dim]."""
+        buf = np.ascontiguousarray(np.asarray(stored, dtype=np.uint8).ravel())
+        h = ctypes.c_void_p()
+        _check(_lib.xt_weights_create_hf(fmt, in_dim, out_dim, buf.ctypes.data_as(_vp), buf.size,
+                                         float(weight_scale), int(bool(is_inverted_scale)),
+                                         ctypes.byref(h)))
+        self = cls.__new__(cls)
+        self.handle = h
+        self.fmt, self.in_dim, self.out_dim = fmt, in_dim, out_dim
+        return self
+
+    def read_tiles(self):
+        """The device tiles, copied to a host uint8 array."""
+        out = np.zeros(tile_bytes(self.fmt, self.in_dim, self.out_dim), dtype=np.uint8)
+        _check(_lib.xt_weights_read_tiles(self.handle, out.ctypes.data_as(_vp), out.size))
+        return out
+
     def device_bytes(self):
         nb = _sz()
         _check(_lib.xt_weights_info(self.handle, None, None, None, ctypes.byref(nb)))
@@ -268,6 +302,36 @@ def repack_host(fmt, in_dim, out_dim, host_bytes):
     _check(_lib.xt_repack_host(fmt, in_dim, out_dim, src.ctypes.data_as(_vp), src.size,
                                out.ctypes.data_as(_vp)))
     return out
+
+
+def hf_destripe(fmt, in_dim, out_dim, stored):
+    """xt_hf_destripe: HF output-dim striped bytes [out_dim/f][in_dim] ->
+    input-dim packed rows [out_dim][ceil(in_dim/f)] (loader/mod.rs:351-390)."""
+    src = np.ascontiguousarray(np.asarray(stored, dtype=np.uint8).ravel())
+    f = 5 if fmt == XT_PACK5 else 4
+    out = np.zeros(out_dim * ((in_dim + f - 1) // f), dtype=np.uint8)
+    _check(_lib.xt_hf_destripe(fmt, in_dim, out_dim, src.ctypes.data_as(_vp), src.size,
+                               out.ctypes.data_as(_vp)))
+    return out
+
+
+def get_prepacked_ternary(stored, stored_dtype, expected_shape, pack_type, weight_scale,
+                          is_inverted_scale):
+    """VarBuilder::get_prepacked_ternary (loader/mod.rs:301-394) on an
+    already-read tensor: `stored` is the checkpoint array (its shape is the
+    stored shape), `stored_dtype` its safetensors dtype name, `weight_scale`
+    the first element of the companion weight_scale tensor as f32.  Returns
+    (packed input-dim bytes, w_scales, in_dim, out_dim) like the reference."""
+    out_dim, in_dim = int(expected_shape[0]), int(expected_shape[1])
+    f = 4 if pack_type == TernaryPackType.Pack4 else 5
+    shape = tuple(np.shape(stored))
+    if not (stored_dtype == "U8" and len(shape) == 2 and shape[1] == in_dim
+            and shape[0] * f == out_dim):
+        raise XternError(XT_ERR_INVALID, "Tensor is not in pre-packed U8 ternary format")
+    s = np.float32(weight_scale)
+    ws = np.float32(1.0) / s if is_inverted_scale else s
+    packed = hf_destripe(pack_type.value, in_dim, out_dim, stored)
+    return packed, np.full(out_dim, ws, dtype=np.float32), in_dim, out_dim
 
 
 def quantize_i8(x, mode=XT_QUANT_AVX512, stream=None):

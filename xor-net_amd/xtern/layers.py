@@ -11,6 +11,7 @@ import numpy as np
 
 from . import (XT_ERR_INVALID, XT_PACK4, XT_PACK5, XT_QUANT_AVX512, XT_XORSPARSE,
                DeviceWeights, TernaryPackType, XternError, _ternarise, encode_sparse_tensor,
+               hf_destripe,
                linear_f32, linear_multi_q, linear_q, pack_ternary4, pack_ternary5,
                unpack_1_58bit_4pack, unpack_1_58bit_5pack)
 
@@ -37,7 +38,7 @@ def _pack_rows(tern, pack_type):
 class TernaryLinear:
     """layers.rs:34-41: weights (rep), in_dim, out_dim, pack_type, w_scales."""
 
-    def __init__(self, rep, in_dim, out_dim, pack_type, w_scales, host_bytes):
+    def __init__(self, rep, in_dim, out_dim, pack_type, w_scales, host_bytes, weights=None):
         self.rep = rep
         self.in_dim = int(in_dim)
         self.out_dim = int(out_dim)
@@ -45,7 +46,8 @@ class TernaryLinear:
         self.w_scales = np.asarray(w_scales, dtype=np.float32)
         self.host_bytes = host_bytes
         fmt = XT_XORSPARSE if rep == TernaryRep.Sparse else pack_type.value
-        self.weights = DeviceWeights(fmt, self.in_dim, self.out_dim, host_bytes, self.w_scales)
+        self.weights = weights if weights is not None else DeviceWeights(
+            fmt, self.in_dim, self.out_dim, host_bytes, self.w_scales)
 
     # --- constructors -----------------------------------------------------
 
@@ -115,10 +117,35 @@ class TernaryLinear:
         builds from SparseFile::get_sparse (dynamic_linear.rs:697-715)."""
         return cls(TernaryRep.Sparse, in_dim, out_dim, pack_type, w_scales, blob)
 
+    @classmethod
+    def from_hf_prepacked(cls, stored, in_dim, out_dim, pack_type, weight_scale,
+                          is_inverted_scale, sparse=False):
+        """DynamicLinear::load's prepacked arm (dynamic_linear.rs:729-741) for
+        one tensor: `stored` is the checkpoint's U8 [out_dim/f][in_dim] array.
+        Dense: the tiles are built on the device from the striped bytes
+        (xt_weights_create_hf) and the host keeps no copy.  sparse=True
+        (XORNET_WEIGHT_FMT=sparse): destripe on the host, then
+        new_sparse_from_packed, as the reference does."""
+        f = 4 if pack_type == TernaryPackType.Pack4 else 5
+        if np.shape(stored) != (out_dim // f, in_dim) or out_dim % f:
+            raise XternError(XT_ERR_INVALID, "Tensor is not in pre-packed U8 ternary format")
+        s = np.float32(weight_scale)
+        ws = np.full(out_dim, np.float32(1.0) / s if is_inverted_scale else s, np.float32)
+        if sparse:
+            packed = hf_destripe(pack_type.value, in_dim, out_dim, stored)
+            return cls.new_sparse_from_packed(packed, in_dim, out_dim, pack_type, ws)
+        dev = DeviceWeights.from_hf(pack_type.value, in_dim, out_dim, stored, weight_scale,
+                                    is_inverted_scale)
+        return cls(TernaryRep.Dense, in_dim, out_dim, pack_type, ws, None, weights=dev)
+
     # --- queries ----------------------------------------------------------
 
     def packed_bytes(self):
-        """layers.rs:234-239 — bytes of the weight bytes as uploaded."""
+        """layers.rs:234-239 — bytes of the packed weights (Pack4/Pack5:
+        out_dim * ceil(in_dim/f); XorSparse: the row blob)."""
+        if self.host_bytes is None:
+            f = 4 if self.pack_type == TernaryPackType.Pack4 else 5
+            return self.out_dim * ((self.in_dim + f - 1) // f)
         return len(self.host_bytes)
 
     def device_bytes(self):
