@@ -53,6 +53,25 @@ enum { XT_PACK4 = 0, XT_PACK5 = 1, XT_XORSPARSE = 2 };
  *   XT_QUANT_SCALAR  the portable path (:179-194): round half away, clamp. */
 enum { XT_QUANT_AVX512 = 0, XT_QUANT_SCALAR = 1 };
 
+/* Elementwise activations of the MLP, each reproducing one reference
+ * function bit for bit (out = act(gate) * up):
+ *   XT_ACT_RELU2_MUL            max(g, 0)^2 * u (quantization.rs:215-216,
+ *                               tensor.rs:206-238)
+ *   XT_ACT_SILU_INPLACE_AVX512  silu_inplace on an AVX-512F host
+ *                               (quantization.rs:225-286): exp polynomial for
+ *                               the first floor(n/16)*16 lanes of each row,
+ *                               g * (1 / (1 + expf(-g))) * u for the tail
+ *   XT_ACT_SILU_INPLACE_SCALAR  silu_inplace elsewhere (:208-218)
+ *   XT_ACT_SILU_MUL             FastTensor::silu_mul_inplace
+ *                               (tensor.rs:170-204): (g / (1 + expf(-g))) * u
+ * expf is the C library's (glibc) expf, reproduced exactly. */
+enum {
+    XT_ACT_RELU2_MUL = 0,
+    XT_ACT_SILU_INPLACE_AVX512 = 1,
+    XT_ACT_SILU_INPLACE_SCALAR = 2,
+    XT_ACT_SILU_MUL = 3
+};
+
 /* Opaque device-resident weights: the packed ternary matrix in the GPU tile
  * layout plus the per-output-row f32 scales.  Owns its device memory.
  * Replaces TernaryLinear { rep, in_dim, out_dim, pack_type, w_scales }
@@ -162,6 +181,45 @@ int xt_ternary_linear_multi_q(const xt_weights* const* ws, int n, const int8_t* 
                               void* stream);
 int xt_ternary_linear_multi_f32(const xt_weights* const* ws, int n, const float* x,
                                 int64_t M, float* const* ys, int mode, void* stream);
+
+/* out[m][i] = act(gate[m][i]) * up[m][i] for M rows of n (device, f32),
+ * act one of XT_ACT_*.  Replaces quantization::silu_inplace
+ * (src/bit1_58/quantization.rs:201-286; call once per row, as the reference
+ * applies it to one row) and FastTensor::silu_mul_inplace /
+ * relu2_mul_inplace (src/tensor.rs:170-238).  n <= 16384. */
+int xt_activation_mul(int act, const float* gate, const float* up, int64_t M, int64_t n,
+                      float* out, void* stream);
+
+/* y[m] = rms_norm(x[m]) for M rows of n (device, f32), bit-exact with
+ * rms_norm (src/nn/fast_attention_simd.rs:458-516: the sum of squares is
+ * accumulated in index order in f32; rms = sqrt(sum / n + eps); y = x * (1 /
+ * rms) * weight).  Replaces FastRmsNorm::forward / FastTensor::rmsnorm
+ * (src/tensor.rs:242-265).  n <= 16384. */
+int xt_rms_norm(const float* x, const float* weight, int64_t M, int64_t n, float eps, float* y,
+                void* stream);
+
+/* The ternary MLP block: gate = x Wg, up = x Wu (one quantised input, one
+ * launch), mid = act(gate) * up, optional RMSNorm of mid (norm_weight [I]
+ * device f32, or NULL), requantisation of mid, y = down(mid) [M][out_dim].
+ * gate/up share in_dim and format; down's in_dim is the intermediate size
+ * I <= 16384.  use_silu = 0 selects ReLU^2.
+ *
+ * xt_ternary_mlp_q takes the quantised input (q [M][in_dim] i8, inv_scale
+ * [M]) and applies TernaryLinear::fused_mlp_all (src/bit1_58/layers.rs:
+ * 497-645) to every row: SiLU is silu_inplace's AVX-512 path when mode is
+ * XT_QUANT_AVX512, its portable path otherwise.
+ *
+ * xt_ternary_mlp_f32 is Mlp::forward (src/models/llama/mlp.rs:43-128) for
+ * all-ternary projections: it quantises x; one row (M == 1) takes the fused
+ * path above, several rows take the reference's unfused path (SiLU as
+ * silu_mul_inplace).  Uses a per-stream device workspace of
+ * M * (8 * I + padded I + 8) bytes. */
+int xt_ternary_mlp_q(const xt_weights* gate, const xt_weights* up, const xt_weights* down,
+                     const float* norm_weight, float eps, int use_silu, const int8_t* q,
+                     const float* inv_scale, int64_t M, float* y, int mode, void* stream);
+int xt_ternary_mlp_f32(const xt_weights* gate, const xt_weights* up, const xt_weights* down,
+                       const float* norm_weight, float eps, int use_silu, const float* x,
+                       int64_t M, float* y, int mode, void* stream);
 
 #ifdef __cplusplus
 }

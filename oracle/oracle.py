@@ -42,6 +42,10 @@ _o.or_linear_forward_q.argtypes = [ctypes.c_int, _vp, _vp, _vp, _vp, _i64, _i64,
                                    _vp, _vp]
 _o.or_hf_destripe.argtypes = [ctypes.c_int, _i64, _i64, _vp, _vp]
 _o.or_hf_destripe.restype = ctypes.c_int
+_o.or_silu_inplace.argtypes = [_vp, _vp, _i64, ctypes.c_int, ctypes.c_int]
+_o.or_act_mul_inplace.argtypes = [_vp, _vp, _i64, ctypes.c_int]
+_o.or_rms_norm.argtypes = [_vp, _vp, _i64, ctypes.c_float]
+_o.or_rms_norm.restype = ctypes.c_float
 _o.or_lcg_next.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
 _o.or_lcg_next.restype = ctypes.c_uint64
 _o.or_cpu_has_vnni.restype = ctypes.c_int
@@ -191,6 +195,63 @@ def hf_destripe(fmt, in_dim, out_dim, stored):
     if _o.or_hf_destripe(fmt, in_dim, out_dim, _p(st), _p(out)) != 0:
         raise ValueError("out_dim must be a multiple of the pack factor")
     return out
+
+
+def silu_inplace(gate, up, use_silu, avx512=True):
+    """quantization::silu_inplace on each row of gate/up [..., n]; returns a copy."""
+    g = _c(gate, np.float32).copy()
+    u = _c(up, np.float32)
+    n = g.shape[-1]
+    g2, u2 = g.reshape(-1, n), u.reshape(-1, n)
+    for r in range(g2.shape[0]):
+        _o.or_silu_inplace(_p(g2[r]), _p(u2[r]), n, int(use_silu), int(avx512))
+    return g
+
+
+def act_mul(x, up, use_silu):
+    """FastTensor::silu_mul_inplace / relu2_mul_inplace; returns a copy."""
+    g = _c(x, np.float32).copy()
+    u = _c(up, np.float32)
+    _o.or_act_mul_inplace(_p(g), _p(u), g.size, int(use_silu))
+    return g
+
+
+def rms_norm(x, w, eps):
+    """rms_norm on each row of x [..., n]; returns (normed copy, row sums of squares)."""
+    y = _c(x, np.float32).copy()
+    n = y.shape[-1]
+    y2 = y.reshape(-1, n)
+    wv = _c(w, np.float32)
+    sums = np.array([_o.or_rms_norm(_p(y2[r]), _p(wv), n, eps) for r in range(y2.shape[0])],
+                    np.float32)
+    return y, sums
+
+
+def mlp_forward(x, gate, up, down, norm_w, eps, use_silu, quant_mode=0, fused=None):
+    """Mlp::forward (models/llama/mlp.rs:43-128) for all-ternary projections.
+
+    gate/up/down: (fmt, K, N, w_scales, dict(wbytes=... | masks=..., signs=...)).
+    fused=None follows the reference's dispatch: one token -> fused_mlp_all
+    (layers.rs:497-645: silu_inplace, optional norm, quantise, down); several
+    tokens -> the fallback (silu_mul_inplace / relu2_mul_inplace, norm,
+    c_proj.forward).  Returns (y, mid_q, mid_inv)."""
+    x = _c(x, np.float32)
+    K = gate[1]
+    x2 = x.reshape(-1, K)
+    M = x2.shape[0]
+    if fused is None:
+        fused = (M == 1)
+    g = linear_forward(gate[0], gate[1], gate[2], x2, gate[3], quant_mode=quant_mode, **gate[4])[0]
+    u = linear_forward(up[0], up[1], up[2], x2, up[3], quant_mode=quant_mode, **up[4])[0]
+    if fused:
+        mid = silu_inplace(g, u, use_silu, avx512=(quant_mode == 0))
+    else:
+        mid = act_mul(g, u, use_silu)
+    if norm_w is not None:
+        mid, _ = rms_norm(mid, norm_w, eps)
+    y, q, inv, _ = linear_forward(down[0], down[1], down[2], mid, down[3], quant_mode=quant_mode,
+                                  **down[4])
+    return y.reshape(x.shape[:-1] + (down[2],)), q, inv
 
 
 class Lcg:

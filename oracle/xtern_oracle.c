@@ -470,6 +470,87 @@ int or_hf_destripe(int fmt, int64_t in_dim, int64_t out_dim, const uint8_t* stor
     return 0;
 }
 
+static inline float silu_scalar(float g, float u) {
+    /* quantization.rs:213 / :280: g * (1.0 / (1.0 + (-g).exp())) * u */
+    const float e = expf(-g);
+    const float sig = 1.0f / (1.0f + e);
+    const float a = g * sig;
+    return a * u;
+}
+
+static inline float relu2_mul(float g, float u) {
+    /* :215-216 / :282-283 and tensor.rs:223-224: r = max(g, 0); r * r * u.
+     * MAXPS(g, 0) returns 0 for NaN g, as does Rust's f32::max. */
+    const float r = (g > 0.0f) ? g : 0.0f;
+    const float rr = r * r;
+    return rr * u;
+}
+
+/* One lane of silu_inplace_avx512's vector body (quantization.rs:243-272):
+ * MINPS/MAXPS return their second operand unless the comparison holds
+ * (so NaN clamps to the bound), ROUNDSCALE imm 0 rounds half to even,
+ * the polynomial uses fused multiply-adds, 2^n is built from the bits
+ * ((n + 127) << 23) with 32-bit wrap, and 1 / (1 + e) is an IEEE division. */
+static inline float silu_avx512_lane(float g, float u) {
+    const float inv_ln2 = 1.44269504088896341f, ln2 = 0.693147180559945309f;
+    const float hi = 88.3762626647949f, lo = -88.3762626647949f;
+    float x = 0.0f - g;
+    x = (x < hi) ? x : hi;
+    x = (x > lo) ? x : lo;
+    const float fx = x * inv_ln2;
+    const float n_f = nearbyintf(fx); /* default rounding mode: to nearest even */
+    const float t = x - n_f * ln2;
+    float e = fmaf(1.0f / 24.0f, t, 1.0f / 6.0f);
+    e = fmaf(e, t, 0.5f);
+    e = fmaf(e, t, 1.0f);
+    e = fmaf(e, t, 1.0f);
+    const int32_t ni = (int32_t)n_f; /* n_f is integral and in [-128, 128] */
+    const uint32_t bits = ((uint32_t)ni + 127u) << 23;
+    float pow2n;
+    memcpy(&pow2n, &bits, 4);
+    const float exp_x = e * pow2n;
+    const float sig = 1.0f / (1.0f + exp_x);
+    const float act = g * sig;
+    return act * u;
+}
+
+void or_silu_inplace(float* gate, const float* up, int64_t n, int use_silu, int avx512) {
+    const int64_t nmain = avx512 ? (n / 16) * 16 : 0;
+    for (int64_t i = 0; i < n; ++i) {
+        const float g = gate[i], u = up[i];
+        if (!use_silu) gate[i] = relu2_mul(g, u);
+        else gate[i] = i < nmain ? silu_avx512_lane(g, u) : silu_scalar(g, u);
+    }
+}
+
+void or_act_mul_inplace(float* x, const float* up, int64_t n, int use_silu) {
+    for (int64_t i = 0; i < n; ++i) {
+        const float g = x[i], u = up[i];
+        if (use_silu) {
+            const float d = 1.0f + expf(-g);
+            const float s = g / d;
+            x[i] = s * u;
+        } else {
+            x[i] = relu2_mul(g, u);
+        }
+    }
+}
+
+float or_rms_norm(float* x, const float* w, int64_t n, float eps) {
+    float sum = 0.0f;
+    for (int64_t i = 0; i < n; ++i) {
+        const float sq = x[i] * x[i];
+        sum += sq;
+    }
+    const float rms = sqrtf(sum / (float)n + eps);
+    const float inv = 1.0f / rms;
+    for (int64_t i = 0; i < n; ++i) {
+        const float a = x[i] * inv;
+        x[i] = a * w[i];
+    }
+    return sum;
+}
+
 /* simd.rs:556-565: x = x*6364136223846793005 + 1442695040888963407; x >> 33. */
 uint64_t or_lcg_next(uint64_t* state) {
     *state = *state * 6364136223846793005ull + 1442695040888963407ull;

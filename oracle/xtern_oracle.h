@@ -88,6 +88,24 @@ void or_linear_forward_q(int fmt, const uint8_t* wbytes, const uint64_t* masks,
 int or_hf_destripe(int fmt, int64_t in_dim, int64_t out_dim, const uint8_t* stored,
                    uint8_t* out_packed);
 
+/* ---- MLP activations and RMSNorm ----
+ * or_silu_inplace: quantization::silu_inplace (src/bit1_58/quantization.rs:
+ * 201-286), the activation of the fused MLP (layers.rs:563).  gate[i] becomes
+ * silu(gate)*up or relu(gate)^2*up.  avx512 != 0 restates the AVX-512F path
+ * (:225-286: lanes below floor(n/16)*16 take the vectorised exp polynomial,
+ * the tail takes the scalar formula), avx512 == 0 the portable path
+ * (:208-218).  The scalar formula is g * (1 / (1 + expf(-g))) * u with the C
+ * library's expf, as Rust's f32::exp calls it. */
+void or_silu_inplace(float* gate, const float* up, int64_t n, int use_silu, int avx512);
+/* FastTensor::silu_mul_inplace / relu2_mul_inplace (src/tensor.rs:170-238),
+ * the activation of the unfused MLP (models/llama/mlp.rs:118-121):
+ * (x / (1 + expf(-x))) * u, or relu(x)^2 * u. */
+void or_act_mul_inplace(float* x, const float* up, int64_t n, int use_silu);
+/* rms_norm (src/nn/fast_attention_simd.rs:458-516; every ISA path sums x*x
+ * sequentially in index order): rms = sqrtf(sum / n + eps), inv = 1 / rms,
+ * x[i] = x[i] * inv * w[i].  In place.  Returns sum. */
+float or_rms_norm(float* x, const float* w, int64_t n, float eps);
+
 /* ---- the reference's deterministic test RNG: simd.rs:556-565 ---- */
 uint64_t or_lcg_next(uint64_t* state);
 

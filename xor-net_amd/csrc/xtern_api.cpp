@@ -244,6 +244,77 @@ int linear_f32(const xt_weights* const* ws, int n, const float* x, int64_t M, fl
     return run_product(ws, n, q, (int)kpad, inv, rowsum, M, ys, nullptr, s);
 }
 
+int launch_mid(const xt::MidArgs& a, int64_t M, hipStream_t s) {
+    hipError_t e = xt::launch_mlp_mid(a, (int)M, s);
+    if (e != hipSuccess) return hip_fail(e, "MLP activation / norm launch");
+    return XT_OK;
+}
+
+int check_row_len(int64_t n) {
+    if (n <= 0) return fail(XT_ERR_INVALID, "row length must be positive");
+    if (n > xt::mid_max_cols())
+        return fail(XT_ERR_UNSUPPORTED, "row length " + std::to_string(n) + " above " +
+                                            std::to_string(xt::mid_max_cols()) + " is not supported");
+    return XT_OK;
+}
+
+// gate+up on one quantised input (done by the caller: `first` runs the
+// product into g/u), then activation [+ norm] + requantisation, then down.
+// Shared by xt_ternary_mlp_q and xt_ternary_mlp_f32.
+int mlp_run(const xt_weights* gate, const xt_weights* up, const xt_weights* down,
+            const float* norm_w, float eps, int act, int mode, int64_t M, float* y, hipStream_t s,
+            const void* in, bool in_is_f32, const float* inv_in) {
+    if (check_weights(gate) || check_weights(up) || check_weights(down)) return XT_ERR_INVALID;
+    if (gate->K != up->K || gate->N != up->N || gate->fmt != up->fmt)
+        return fail(XT_ERR_INVALID, "gate and up projections must have the same shape and format");
+    if (down->K != gate->N)
+        return fail(XT_ERR_INVALID, "down in_dim " + std::to_string(down->K) +
+                                        " != intermediate size " + std::to_string(gate->N));
+    if (mode != XT_QUANT_AVX512 && mode != XT_QUANT_SCALAR)
+        return fail(XT_ERR_INVALID, "unknown quantisation mode");
+    if (M < 0) return fail(XT_ERR_INVALID, "M must be >= 0");
+    if (M == 0) return XT_OK;
+    if (!in || !y || (!in_is_f32 && !inv_in)) return fail(XT_ERR_INVALID, "NULL pointer");
+    if (int rc = check_row_len(gate->N)) return rc;
+    const int64_t I = gate->N;
+    const int64_t kpad = down->nch * xt::chunk_cols(down->fmt);
+    const size_t fb = align_up((size_t)M * I * sizeof(float), 256);
+    const size_t qb = align_up((size_t)M * kpad, 256);
+    const size_t sb = align_up((size_t)M * 4, 256);
+    void* wsp = nullptr;
+    if (int rc = workspace(s, 2 * fb + qb + 2 * sb, &wsp, 2)) return rc;
+    char* base = static_cast<char*>(wsp);
+    float* g = reinterpret_cast<float*>(base);
+    float* u = reinterpret_cast<float*>(base + fb);
+    int8_t* qm = reinterpret_cast<int8_t*>(base + 2 * fb);
+    float* invm = reinterpret_cast<float*>(base + 2 * fb + qb);
+    int32_t* rsm = reinterpret_cast<int32_t*>(base + 2 * fb + qb + sb);
+    const xt_weights* gu[2] = {gate, up};
+    float* gy[2] = {g, u};
+    int rc = in_is_f32 ? linear_f32(gu, 2, static_cast<const float*>(in), M, gy, mode, s)
+                       : linear_q(gu, 2, static_cast<const int8_t*>(in), inv_in, nullptr, M, gy,
+                                  nullptr, s);
+    if (rc) return rc;
+    xt::MidArgs a;
+    memset(&a, 0, sizeof a);
+    a.gate = g;
+    a.up = u;
+    a.ldg = I;
+    a.n = (int)I;
+    a.act = act;
+    a.norm_w = norm_w;
+    a.eps = eps;
+    a.mode = mode;
+    a.q = qm;
+    a.ldq = (int)kpad;
+    a.inv = invm;
+    a.rowsum = rsm;
+    if ((rc = launch_mid(a, M, s))) return rc;
+    float* ys[1] = {y};
+    const xt_weights* dw[1] = {down};
+    return run_product(dw, 1, qm, (int)kpad, invm, rsm, M, ys, nullptr, s);
+}
+
 }  // namespace
 
 extern "C" {
@@ -471,6 +542,67 @@ int xt_ternary_linear_multi_q(const xt_weights* const* ws, int n, const int8_t* 
 int xt_ternary_linear_multi_f32(const xt_weights* const* ws, int n, const float* x, int64_t M,
                                 float* const* ys, int mode, void* stream) {
     return linear_f32(ws, n, x, M, ys, mode, static_cast<hipStream_t>(stream));
+}
+
+int xt_activation_mul(int act, const float* gate, const float* up, int64_t M, int64_t n,
+                      float* out, void* stream) {
+    if (act < XT_ACT_RELU2_MUL || act > XT_ACT_SILU_MUL)
+        return fail(XT_ERR_INVALID, "unknown activation " + std::to_string(act));
+    if (M < 0) return fail(XT_ERR_INVALID, "M must be >= 0");
+    if (int rc = check_row_len(n)) return rc;
+    if (M == 0) return XT_OK;
+    if (!gate || !up || !out) return fail(XT_ERR_INVALID, "NULL pointer");
+    xt::MidArgs a;
+    memset(&a, 0, sizeof a);
+    a.gate = gate;
+    a.up = up;
+    a.ldg = n;
+    a.n = (int)n;
+    a.act = act;
+    a.out = out;
+    a.ldo = n;
+    return launch_mid(a, M, static_cast<hipStream_t>(stream));
+}
+
+int xt_rms_norm(const float* x, const float* weight, int64_t M, int64_t n, float eps, float* y,
+                void* stream) {
+    if (M < 0) return fail(XT_ERR_INVALID, "M must be >= 0");
+    if (int rc = check_row_len(n)) return rc;
+    if (M == 0) return XT_OK;
+    if (!x || !weight || !y) return fail(XT_ERR_INVALID, "NULL pointer");
+    xt::MidArgs a;
+    memset(&a, 0, sizeof a);
+    a.gate = x;
+    a.ldg = n;
+    a.n = (int)n;
+    a.act = xt::kActIdentity;
+    a.norm_w = weight;
+    a.eps = eps;
+    a.out = y;
+    a.ldo = n;
+    return launch_mid(a, M, static_cast<hipStream_t>(stream));
+}
+
+int xt_ternary_mlp_q(const xt_weights* gate, const xt_weights* up, const xt_weights* down,
+                     const float* norm_weight, float eps, int use_silu, const int8_t* q,
+                     const float* inv_scale, int64_t M, float* y, int mode, void* stream) {
+    const int act = !use_silu ? XT_ACT_RELU2_MUL
+                              : (mode == XT_QUANT_SCALAR ? XT_ACT_SILU_INPLACE_SCALAR
+                                                         : XT_ACT_SILU_INPLACE_AVX512);
+    return mlp_run(gate, up, down, norm_weight, eps, act, mode, M, y,
+                   static_cast<hipStream_t>(stream), q, false, inv_scale);
+}
+
+int xt_ternary_mlp_f32(const xt_weights* gate, const xt_weights* up, const xt_weights* down,
+                       const float* norm_weight, float eps, int use_silu, const float* x,
+                       int64_t M, float* y, int mode, void* stream) {
+    int act = XT_ACT_RELU2_MUL;
+    if (use_silu)
+        act = M == 1 ? (mode == XT_QUANT_SCALAR ? XT_ACT_SILU_INPLACE_SCALAR
+                                                : XT_ACT_SILU_INPLACE_AVX512)
+                     : XT_ACT_SILU_MUL;
+    return mlp_run(gate, up, down, norm_weight, eps, act, mode, M, y,
+                   static_cast<hipStream_t>(stream), x, true, nullptr);
 }
 
 }  // extern "C"

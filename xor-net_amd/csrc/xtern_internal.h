@@ -70,6 +70,28 @@ int gemm_ncmax(int fmt);
 hipError_t launch_gemm(int fmt, const MMArgs& a, int ntiles, int splitk, hipStream_t s);
 // Decode GEMV (M <= 16): 16 output rows per workgroup, activations in LDS.
 hipError_t launch_gemv(int fmt, const MMArgs& a, int ntiles, int waves, hipStream_t s);
+// MLP middle stage (xtern_kernels.hip): per row of gate/up, activation,
+// optional RMSNorm, optional f32 output, optional requantisation.
+struct MidArgs {
+    const float* gate;  // [M][ldg]
+    const float* up;    // [M][ldg]
+    int64_t ldg;
+    int n;              // row length (intermediate size)
+    int C;              // set by the launcher
+    int act;            // XT_ACT_*
+    const float* norm_w;  // [n] RMSNorm weight, or null
+    float eps;
+    int mode;             // requantisation rounding (XT_QUANT_*)
+    int8_t* q;            // [M][ldq] (zero padded to ldq), or null
+    int ldq;
+    float* inv;           // [M]
+    int32_t* rowsum;      // [M] or null
+    float* out;           // [M][ldo] f32 activation (+ norm) result, or null
+    int64_t ldo;
+};
+constexpr int kActIdentity = 100;  // MidArgs::act: no activation (up unused)
+int mid_max_cols();
+hipError_t launch_mlp_mid(const MidArgs& a, int M, hipStream_t s);
 // HF prepacked striped bytes [N/f][K] (device) -> tiles (device).
 hipError_t launch_hf_tiles(int fmt, const uint8_t* stored, int64_t K, int64_t N, uint8_t* tiles,
                            hipStream_t s);

@@ -70,6 +70,9 @@ __device__ __forceinline__ T block_reduce(T v, Op op, T* smem) {
 struct MaxOp {
     __device__ float operator()(float a, float b) const { return fmaxf(a, b); }
 };
+struct OrOp {
+    __device__ int operator()(int a, int b) const { return a | b; }
+};
 struct AddOp {
     __device__ int operator()(int a, int b) const { return a + b; }
 };
@@ -1130,6 +1133,390 @@ hipError_t launch_hf_tiles(int fmt, const uint8_t* stored, int64_t K, int64_t N,
     else
         hipLaunchKernelGGL(hf_tiles_kernel<XT_PACK4>, dim3((unsigned)blocks), dim3(256), 0, s,
                            stored, K, N, N / f, nch, nlanes, tiles);
+    return hipGetLastError();
+}
+
+}  // namespace xt
+
+namespace xt {
+
+// ---------------------------------------------------------------------------
+// MLP middle: activation, optional RMSNorm, requantisation
+// ---------------------------------------------------------------------------
+
+// expf of the C library the reference links (glibc 2.28+, from ARM's
+// optimized-routines): x * 32/ln2 rounded to an integer k, 2^(k/32) from a
+// 32-entry table with k/32's integer part added to the exponent bits, and a
+// cubic in the remainder, all in double, rounded once to float.  The two
+// products with InvLn2N are fused multiply-adds, as the FMA build of the
+// library compiles them.  Equal to the host expf on every one of the 2^32
+// float inputs (checked exhaustively on the build host).
+__constant__ uint64_t kExp2Tab[32] = {
+    0x3ff0000000000000ULL, 0x3fefd9b0d3158574ULL, 0x3fefb5586cf9890fULL, 0x3fef9301d0125b51ULL,
+    0x3fef72b83c7d517bULL, 0x3fef54873168b9aaULL, 0x3fef387a6e756238ULL, 0x3fef1e9df51fdee1ULL,
+    0x3fef06fe0a31b715ULL, 0x3feef1a7373aa9cbULL, 0x3feedea64c123422ULL, 0x3feece086061892dULL,
+    0x3feebfdad5362a27ULL, 0x3feeb42b569d4f82ULL, 0x3feeab07dd485429ULL, 0x3feea47eb03a5585ULL,
+    0x3feea09e667f3bcdULL, 0x3fee9f75e8ec5f74ULL, 0x3feea11473eb0187ULL, 0x3feea589994cce13ULL,
+    0x3feeace5422aa0dbULL, 0x3feeb737b0cdc5e5ULL, 0x3feec49182a3f090ULL, 0x3feed503b23e255dULL,
+    0x3feee89f995ad3adULL, 0x3feeff76f2fb5e47ULL, 0x3fef199bdd85529cULL, 0x3fef3720dcef9069ULL,
+    0x3fef5818dcfba487ULL, 0x3fef7c97337b9b5fULL, 0x3fefa4afa2a490daULL, 0x3fefd0765b6e4540ULL};
+
+__device__ __forceinline__ float libc_expf(float x) {
+    const uint32_t ux = __float_as_uint(x);
+    const uint32_t top = (ux >> 20) & 0x7ffu;
+    if (top >= 0x42bu) {  // |x| >= 88, inf, NaN
+        if (ux == 0xff800000u) return 0.0f;
+        if (top >= 0x7f8u) return x + x;
+        if (x > 0x1.62e42ep6f) return __builtin_inff();
+        if (x < -0x1.9fe368p6f) return 0.0f;
+    }
+    const double C0 = 0x1.c6af84b912394p-5 / 32 / 32 / 32, C1 = 0x1.ebfce50fac4f3p-3 / 32 / 32,
+                 C2 = 0x1.62e42ff0c52d6p-1 / 32;
+    const double inv = 0x1.71547652b82fep+0 * 32, shift = 0x1.8p+52;
+    const double xd = (double)x;
+    double kd = __fma_rn(inv, xd, shift);
+    const uint64_t ki = (uint64_t)__double_as_longlong(kd);
+    kd = __dsub_rn(kd, shift);
+    const double r = __fma_rn(inv, xd, -kd);
+    const uint64_t t = kExp2Tab[ki & 31] + (ki << 47);
+    const double s = __longlong_as_double((long long)t);
+    const double z = __fma_rn(C0, r, C1);
+    const double r2 = __dmul_rn(r, r);
+    double y = __fma_rn(C2, r, 1.0);
+    y = __fma_rn(z, r2, y);
+    return (float)__dmul_rn(y, s);
+}
+
+// quantization.rs:213 / :280: g * (1 / (1 + exp(-g))) * u.
+__device__ __forceinline__ float silu_scalar(float g, float u) {
+    const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, libc_expf(-g)));
+    return __fmul_rn(__fmul_rn(g, sig), u);
+}
+// tensor.rs:186-188: (x / (1 + exp(-x))) * u.
+__device__ __forceinline__ float silu_div(float g, float u) {
+    return __fmul_rn(__fdiv_rn(g, __fadd_rn(1.0f, libc_expf(-g))), u);
+}
+// quantization.rs:215-216, :268-270; tensor.rs:223-224: max(g, 0)^2 * u.
+__device__ __forceinline__ float relu2_mul(float g, float u) {
+    const float r = (g > 0.0f) ? g : 0.0f;
+    return __fmul_rn(__fmul_rn(r, r), u);
+}
+// One lane of silu_inplace_avx512's vector body (quantization.rs:243-272).
+__device__ __forceinline__ float silu_poly(float g, float u) {
+    const float inv_ln2 = 1.44269504088896341f, ln2 = 0.693147180559945309f;
+    const float hi = 88.3762626647949f, lo = -88.3762626647949f;
+    float x = __fsub_rn(0.0f, g);
+    x = (x < hi) ? x : hi;  // MINPS: second operand unless x < hi (NaN -> hi)
+    x = (x > lo) ? x : lo;  // MAXPS
+    const float fx = __fmul_rn(x, inv_ln2);
+    const float n_f = __builtin_rintf(fx);
+    const float t = __fsub_rn(x, __fmul_rn(n_f, ln2));
+    float e = __fmaf_rn(1.0f / 24.0f, t, 1.0f / 6.0f);
+    e = __fmaf_rn(e, t, 0.5f);
+    e = __fmaf_rn(e, t, 1.0f);
+    e = __fmaf_rn(e, t, 1.0f);
+    const uint32_t bits = ((uint32_t)(int)n_f + 127u) << 23;
+    const float exp_x = __fmul_rn(e, __uint_as_float(bits));
+    const float sig = __fdiv_rn(1.0f, __fadd_rn(1.0f, exp_x));
+    return __fmul_rn(__fmul_rn(g, sig), u);
+}
+
+__device__ __forceinline__ float apply_act(int act, float g, float u, bool main_lane) {
+    switch (act) {
+        case XT_ACT_SILU_INPLACE_AVX512:
+            return main_lane ? silu_poly(g, u) : silu_scalar(g, u);
+        case XT_ACT_SILU_INPLACE_SCALAR:
+            return silu_scalar(g, u);
+        case XT_ACT_SILU_MUL:
+            return silu_div(g, u);
+        case kActIdentity:
+            return g;
+        default:
+            return relu2_mul(g, u);
+    }
+}
+
+// Binade of a running sum: floor(log2 s) clamped below at -126 (the grid
+// 2^-149 spans [0, 2^-125)); 128 for sums at or beyond 2^128.
+__device__ __forceinline__ int binade_d(double a) {
+    if (a == 0.0) return -126;
+    const int e = (int)((__double_as_longlong(a) >> 52) & 0x7ff) - 1023;
+    return e < -126 ? -126 : (e > 128 ? 128 : e);
+}
+__device__ __forceinline__ int binade_f(float s) {
+    const int e = (int)((__float_as_uint(s) >> 23) & 0xff);
+    return e == 0 ? -126 : e - 127;
+}
+
+constexpr int kMidThreads = 1024;
+constexpr int kMidWaves = kMidThreads / 64;
+constexpr int kMidCmax = 16;                         // row length <= 16 * 1024
+constexpr int kMidRecMax = 1024;                     // piece records in LDS
+constexpr uint32_t kGrid = 1u << 24;                 // grid points per binade
+
+// Sequential float sum t[0] + t[1] + ... (each partial sum rounded to f32,
+// in index order), the order of rms_norm's sum of squares, computed by the
+// whole workgroup.  Within one binade [2^b, 2^(b+1)) of the running sum every
+// f32 add is an integer add on the grid u = 2^(b-23): fl(s + t) = s +
+// u * round(t / u), except when t / u is an exact half (a tie, whose rounding
+// depends on the parity of s) or when the sum leaves the binade.  So:
+//  1. a double prefix sum predicts the binade of the running sum before each
+//     element;
+//  2. elements that are ties, or after which the predicted binade changes,
+//     end a "piece"; every other element contributes its integer increment,
+//     and the increments are prefix-summed;
+//  3. one wave walks the pieces in order: if the actual running sum is in the
+//     piece's predicted binade and stays below its top, the piece's
+//     increments are added at once (exact), otherwise the piece's elements
+//     are added one by one; the piece's end element is always added with a
+//     real f32 add.
+// The result never depends on the prediction being right, only the speed
+// does.  Requires every t finite and >= 0 (the caller handles NaN / inf);
+// `lt` holds t[i] for i < n in LDS; t of element (wave*C + c)*64 + lane is
+// v[c] * v[c] (v = 0 beyond n).
+__device__ __forceinline__ float exact_seq_sum(const float* v, int C, int n, const float* lt, double* l_tot,
+                               uint64_t* l_gp, int* l_cnt, int* rec_idx, uint64_t* rec_gp,
+                               int* rec_b, float* l_res) {
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    // 1. prefix sums in double
+    double incl[kMidCmax];
+    double carry = 0.0;
+#pragma unroll
+    for (int c = 0; c < kMidCmax; ++c) {
+        if (c < C) {
+            double x = (double)__fmul_rn(v[c], v[c]);
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const double y = __shfl_up(x, off, 64);
+                if (lane >= off) x = __dadd_rn(x, y);
+            }
+            incl[c] = __dadd_rn(carry, x);
+            carry = __shfl(incl[c], 63, 64);
+        }
+    }
+    if (lane == 0) l_tot[w] = carry;
+    __syncthreads();
+    double offw = 0.0;
+    for (int j = 0; j < w; ++j) offw = __dadd_rn(offw, l_tot[j]);
+
+    // 2. piece ends, integer increments, their prefix and the end ranks
+    uint64_t gcarry = 0;
+    int ccarry = 0;
+    double last_prev = 0.0;
+    uint64_t gpl[kMidCmax];
+    int meta[kMidCmax];  // bit 0: piece end; bits 1..: binade + 256
+#pragma unroll
+    for (int c = 0; c < kMidCmax; ++c) {
+        gpl[c] = 0;
+        meta[c] = 0;
+        if (c < C) {
+            const int i = (w * C + c) * 64 + lane;
+            const double up = __shfl_up(incl[c], 1, 64);
+            const double excl_local = lane == 0 ? last_prev : up;
+            last_prev = __shfl(incl[c], 63, 64);
+            const double aex = __dadd_rn(offw, excl_local);
+            const double ain = __dadd_rn(offw, incl[c]);
+            const int b = binade_d(aex), bn = binade_d(ain);
+            const uint32_t bits = __float_as_uint(__fmul_rn(v[c], v[c]));
+            const uint32_t et_f = (bits >> 23) & 0xffu;
+            const uint32_t m = et_f ? ((bits & 0x7fffffu) | 0x800000u) : (bits & 0x7fffffu);
+            const int et = et_f ? (int)et_f - 150 : -149;
+            const int shift = (b - 23) - et;
+            uint32_t q = 0;
+            int r = 0;
+            if (shift <= 0) {
+                const int ls = -shift;
+                q = (ls >= 24) ? (m ? kGrid : 0u)
+                               : (uint32_t)min((uint64_t)m << ls, (uint64_t)kGrid);
+            } else if (shift < 26) {
+                q = m >> shift;
+                const uint32_t rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1);
+                r = rem < half ? 0 : (rem == half ? 1 : 2);
+            }
+            const bool valid = i < n;
+            const bool end = valid && (r == 1 || bn != b || i == n - 1);
+            const uint32_t d = (valid && !end) ? min(q + (r == 2 ? 1u : 0u), kGrid) : 0u;
+            meta[c] = (end ? 1 : 0) | ((b + 256) << 1);
+            uint64_t x = d;  // inclusive wave scan
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const uint64_t y = __shfl_up(x, off, 64);
+                if (lane >= off) x += y;
+            }
+            gpl[c] = gcarry + x;
+            gcarry += __shfl(x, 63, 64);
+            ccarry += __popcll(__ballot(end));
+        }
+    }
+    if (lane == 0) {
+        l_gp[w] = gcarry;
+        l_cnt[w] = ccarry;
+    }
+    __syncthreads();
+    uint64_t goff = 0;
+    int coff = 0;
+    for (int j = 0; j < w; ++j) {
+        goff += l_gp[j];
+        coff += l_cnt[j];
+    }
+    int total_ends = 0;
+    for (int j = 0; j < kMidWaves; ++j) total_ends += l_cnt[j];
+    const bool overflow = total_ends > kMidRecMax;
+    int crun = coff;
+#pragma unroll
+    for (int c = 0; c < kMidCmax; ++c) {
+        if (c < C) {
+            const bool end = meta[c] & 1;
+            const uint64_t mask = __ballot(end);
+            if (end && !overflow) {
+                const int rank = crun + __popcll(mask & ((1ull << lane) - 1ull));
+                rec_idx[rank] = (w * C + c) * 64 + lane;
+                // own increment is 0, so the inclusive prefix is the exclusive one
+                rec_gp[rank] = goff + gpl[c];
+                rec_b[rank] = (meta[c] >> 1) - 256;
+            }
+            crun += __popcll(mask);
+        }
+    }
+    __syncthreads();
+
+    // 3. walk the pieces (wave 0, every lane runs the same uniform code)
+    if (w == 0) {
+        float s = 0.0f;
+        if (overflow) {
+            for (int j = 0; j < n; ++j) s = __fadd_rn(s, lt[j]);
+        } else {
+            int prev_idx = -1;
+            uint64_t prev_gp = 0;
+            for (int k = 0; k < total_ends; ++k) {
+                if (__builtin_isinf(s)) break;
+                const int idx = rec_idx[k];
+                const uint64_t gp = rec_gp[k];
+                const int b = rec_b[k];
+                const int start = prev_idx + 1;
+                if (start < idx) {
+                    const uint64_t P = gp - prev_gp;
+                    bool ok = binade_f(s) == b && b <= 127 && P < kGrid;
+                    double S = 0.0;
+                    if (ok) {
+                        S = ldexp((double)s, 23 - b);
+                        ok = S + (double)P < (double)kGrid;
+                    }
+                    if (ok) {
+                        s = (float)ldexp(S + (double)P, b - 23);
+                    } else {
+                        for (int j = start; j < idx; ++j) s = __fadd_rn(s, lt[j]);
+                    }
+                }
+                s = __fadd_rn(s, lt[idx]);
+                prev_idx = idx;
+                prev_gp = gp;
+            }
+        }
+        if (lane == 0) *l_res = s;
+    }
+    __syncthreads();
+    return *l_res;
+}
+
+// One workgroup (16 waves) per row.  Element i = (wave*C + c)*64 + lane is
+// held in registers from the load to the quantisation.
+__global__ __launch_bounds__(kMidThreads) void mlp_mid_kernel(MidArgs a) {
+    extern __shared__ __align__(16) uint8_t lds[];
+    __shared__ double l_tot[kMidWaves];
+    __shared__ uint64_t l_gp[kMidWaves];
+    __shared__ int l_cnt[kMidWaves];
+    __shared__ float l_res;
+    __shared__ float sm_f[kMidWaves];
+    __shared__ int sm_i[kMidWaves];
+    const int m = blockIdx.x;
+    const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+    const int n = a.n, C = a.C;
+    const int nmain = (n / 16) * 16;
+    const float* gr = a.gate + (size_t)m * a.ldg;
+    const float* ur = a.up + (size_t)m * a.ldg;
+    float v[kMidCmax];
+#pragma unroll
+    for (int c = 0; c < kMidCmax; ++c) {
+        const int i = (w * C + c) * 64 + lane;
+        v[c] = (c < C && i < n) ? apply_act(a.act, gr[i], a.up ? ur[i] : 0.0f, i < nmain) : 0.0f;
+    }
+    if (a.norm_w) {
+        float* lt = reinterpret_cast<float*>(lds);
+        int* rec_idx = reinterpret_cast<int*>(lds + (size_t)C * kMidThreads * 4);
+        int* rec_b = rec_idx + kMidRecMax;
+        uint64_t* rec_gp = reinterpret_cast<uint64_t*>(rec_b + kMidRecMax);
+        int flags = 0;
+#pragma unroll
+        for (int c = 0; c < kMidCmax; ++c) {
+            const int i = (w * C + c) * 64 + lane;
+            const float t = __fmul_rn(v[c], v[c]);
+            if (c < C && i < n) {
+                lt[i] = t;
+                if (t != t) flags |= 1;
+                else if (__builtin_isinf(t)) flags |= 2;
+            }
+        }
+        flags = block_reduce(flags, OrOp(), sm_i);
+        float sum;
+        if (flags & 1) sum = __builtin_nanf("");
+        else if (flags & 2) sum = __builtin_inff();
+        else sum = exact_seq_sum(v, C, n, lt, l_tot, l_gp, l_cnt, rec_idx, rec_gp, rec_b, &l_res);
+        // fast_attention_simd.rs:485-486.  sqrtf is correctly rounded on the
+        // host; the hardware f32 square root is not, so take the correctly
+        // rounded double root and round it once (exact: 53 >= 2*24 + 2).
+        const float ms = __fadd_rn(__fdiv_rn(sum, (float)n), a.eps);
+        const float rms = (float)__dsqrt_rn((double)ms);
+        const float invr = __fdiv_rn(1.0f, rms);
+#pragma unroll
+        for (int c = 0; c < kMidCmax; ++c) {
+            const int i = (w * C + c) * 64 + lane;
+            if (c < C && i < n) v[c] = __fmul_rn(__fmul_rn(v[c], invr), a.norm_w[i]);
+        }
+    }
+    if (a.out) {
+        float* orow = a.out + (size_t)m * a.ldo;
+#pragma unroll
+        for (int c = 0; c < kMidCmax; ++c) {
+            const int i = (w * C + c) * 64 + lane;
+            if (c < C && i < n) orow[i] = v[c];
+        }
+    }
+    if (!a.q) return;
+    float mx = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kMidCmax; ++c) mx = fmaxf(mx, fabsf(v[c]));
+    mx = block_reduce(mx, MaxOp(), sm_f);
+    const float scale = (mx > 0.0f) ? __fdiv_rn(127.0f, mx) : 1.0f;
+    const float invs = (mx > 0.0f) ? __fdiv_rn(mx, 127.0f) : 1.0f;
+    int8_t* qr = a.q + (size_t)m * a.ldq;
+    int sum = 0;
+#pragma unroll
+    for (int c = 0; c < kMidCmax; ++c) {
+        const int i = (w * C + c) * 64 + lane;
+        if (c < C && i < n) {
+            const int b = quant_one(v[c], scale, a.mode, i < nmain);
+            qr[i] = (int8_t)b;
+            sum += b;
+        }
+    }
+    for (int i = n + tid; i < a.ldq; i += kMidThreads) qr[i] = 0;
+    sum = block_reduce(sum, AddOp(), sm_i);
+    if (tid == 0) {
+        a.inv[m] = invs;
+        if (a.rowsum) a.rowsum[m] = sum;
+    }
+}
+
+int mid_max_cols() { return kMidCmax * kMidThreads; }
+
+hipError_t launch_mlp_mid(const MidArgs& a0, int M, hipStream_t s) {
+    if (M <= 0) return hipSuccess;
+    MidArgs a = a0;
+    a.C = (a.n + kMidThreads - 1) / kMidThreads;
+    if (a.n <= 0 || a.C > kMidCmax) return hipErrorInvalidValue;
+    const size_t lds = a.norm_w ? (size_t)a.C * kMidThreads * 4 + (size_t)kMidRecMax * 16 : 0;
+    hipLaunchKernelGGL(mlp_mid_kernel, dim3(M), dim3(kMidThreads), lds, s, a);
     return hipGetLastError();
 }
 

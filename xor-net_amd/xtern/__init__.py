@@ -41,6 +41,11 @@ except ImportError:  # the C ABI itself does not need torch
 
 _lib = ctypes.CDLL(LIB_PATH)
 
+XT_ACT_RELU2_MUL = 0
+XT_ACT_SILU_INPLACE_AVX512 = 1
+XT_ACT_SILU_INPLACE_SCALAR = 2
+XT_ACT_SILU_MUL = 3
+
 XT_OK = 0
 XT_ERR_INVALID = -1
 XT_ERR_HIP = -2
@@ -67,6 +72,12 @@ _lib.xt_hf_destripe.argtypes = [ctypes.c_int, _i64, _i64, _vp, _sz, _vp]
 _lib.xt_weights_create_hf.argtypes = [ctypes.c_int, _i64, _i64, _vp, _sz, ctypes.c_float,
                                       ctypes.c_int, ctypes.POINTER(_vp)]
 _lib.xt_weights_read_tiles.argtypes = [_vp, _vp, _sz]
+_lib.xt_activation_mul.argtypes = [ctypes.c_int, _vp, _vp, _i64, _i64, _vp, _vp]
+_lib.xt_rms_norm.argtypes = [_vp, _vp, _i64, _i64, ctypes.c_float, _vp, _vp]
+_lib.xt_ternary_mlp_q.argtypes = [_vp, _vp, _vp, _vp, ctypes.c_float, ctypes.c_int, _vp, _vp,
+                                  _i64, _vp, ctypes.c_int, _vp]
+_lib.xt_ternary_mlp_f32.argtypes = [_vp, _vp, _vp, _vp, ctypes.c_float, ctypes.c_int, _vp, _i64,
+                                    _vp, ctypes.c_int, _vp]
 _lib.xt_quantize_i8.argtypes = [_vp, _i64, _i64, _vp, _vp, ctypes.c_int, _vp]
 _lib.xt_quantize_i8_rowsum.argtypes = [_vp, _i64, _i64, _vp, _vp, _vp, ctypes.c_int, _vp]
 _lib.xt_ternary_linear_q.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp, _vp]
@@ -410,6 +421,76 @@ def linear_f32(w, x, mode=XT_QUANT_AVX512, out=None, stream=None):
     return y
 
 
+def activation_mul(act, gate, up, out=None, stream=None):
+    """xt_activation_mul: act(gate) * up row-wise for [..., n] f32 tensors."""
+    torch = _torch()
+    if gate.shape != up.shape:
+        raise XternError(XT_ERR_INVALID, f"shape mismatch: {tuple(gate.shape)} != {tuple(up.shape)}")
+    n = gate.shape[-1]
+    g2, u2 = gate.reshape(-1, n).contiguous(), up.reshape(-1, n).contiguous()
+    y = out if out is not None else torch.empty_like(g2)
+    _check(_lib.xt_activation_mul(act, _dev_ptr(g2, torch.float32, "gate"),
+                                  _dev_ptr(u2, torch.float32, "up"), g2.shape[0], n,
+                                  _dev_ptr(y, torch.float32, "out"), _stream_ptr(stream)))
+    return y.reshape(gate.shape)
+
+
+def rms_norm(x, weight, eps, out=None, stream=None):
+    """xt_rms_norm: rms_norm of each row of x [..., n]."""
+    torch = _torch()
+    n = x.shape[-1]
+    if weight.numel() != n:
+        raise XternError(XT_ERR_INVALID,
+                         f"FastTensor::rmsnorm weight size mismatch: expected {n}, got {weight.numel()}")
+    x2 = x.reshape(-1, n).contiguous()
+    y = out if out is not None else torch.empty_like(x2)
+    _check(_lib.xt_rms_norm(_dev_ptr(x2, torch.float32, "x"),
+                            _dev_ptr(weight.contiguous(), torch.float32, "weight"), x2.shape[0], n,
+                            float(eps), _dev_ptr(y, torch.float32, "y"), _stream_ptr(stream)))
+    return y.reshape(x.shape)
+
+
+def _mlp_check(gate, up, down, x_last):
+    if x_last != gate.in_dim:
+        raise XternError(XT_ERR_INVALID,
+                         f"Input dimension mismatch: expected {gate.in_dim}, got {x_last}")
+
+
+def mlp_q(gate, up, down, q, inv, norm_w=None, eps=1e-5, use_silu=False,
+          mode=XT_QUANT_AVX512, out=None, stream=None):
+    """xt_ternary_mlp_q: fused_mlp_all on every row of q [M, in_dim] i8."""
+    torch = _torch()
+    _mlp_check(gate, up, down, q.shape[-1])
+    q2 = q.reshape(-1, q.shape[-1]).contiguous()
+    M = q2.shape[0]
+    y = out if out is not None else torch.empty((M, down.out_dim), dtype=torch.float32,
+                                                device=q.device)
+    _check(_lib.xt_ternary_mlp_q(gate.handle, up.handle, down.handle,
+                                 _dev_ptr(norm_w, torch.float32, "norm_w") if norm_w is not None
+                                 else None, float(eps), int(bool(use_silu)),
+                                 _dev_ptr(q2, torch.int8, "q"),
+                                 _dev_ptr(inv.contiguous(), torch.float32, "inv_scale"), M,
+                                 _dev_ptr(y, torch.float32, "y"), mode, _stream_ptr(stream)))
+    return y
+
+
+def mlp_f32(gate, up, down, x, norm_w=None, eps=1e-5, use_silu=False, mode=XT_QUANT_AVX512,
+            out=None, stream=None):
+    """xt_ternary_mlp_f32: Mlp::forward for x [M, in_dim] f32."""
+    torch = _torch()
+    _mlp_check(gate, up, down, x.shape[-1])
+    x2 = x.reshape(-1, x.shape[-1]).contiguous()
+    M = x2.shape[0]
+    y = out if out is not None else torch.empty((M, down.out_dim), dtype=torch.float32,
+                                                device=x.device)
+    _check(_lib.xt_ternary_mlp_f32(gate.handle, up.handle, down.handle,
+                                   _dev_ptr(norm_w, torch.float32, "norm_w") if norm_w is not None
+                                   else None, float(eps), int(bool(use_silu)),
+                                   _dev_ptr(x2, torch.float32, "x"), M,
+                                   _dev_ptr(y, torch.float32, "y"), mode, _stream_ptr(stream)))
+    return y
+
+
 def _multi(ws, ys):
     n = len(ws)
     harr = (_vp * n)(*[w.handle for w in ws])
@@ -440,4 +521,4 @@ def linear_multi_q(ws, q, inv, stream=None):
     return ys
 
 
-from .layers import TernaryLinear, DynamicLinear, TernaryRep  # noqa: E402,F401
+from .layers import TernaryLinear, DynamicLinear, TernaryRep, FastRmsNorm, Mlp  # noqa: E402,F401

@@ -11,7 +11,7 @@ import numpy as np
 
 from . import (XT_ERR_INVALID, XT_PACK4, XT_PACK5, XT_QUANT_AVX512, XT_XORSPARSE,
                DeviceWeights, TernaryPackType, XternError, _ternarise, encode_sparse_tensor,
-               hf_destripe,
+               hf_destripe, mlp_f32, mlp_q, rms_norm,
                linear_f32, linear_multi_q, linear_q, pack_ternary4, pack_ternary5,
                unpack_1_58bit_4pack, unpack_1_58bit_5pack)
 
@@ -205,6 +205,66 @@ class TernaryLinear:
         return tuple(y.reshape(lead + (l.out_dim,)) for y, l in zip(ys, lins))
 
 
+    @staticmethod
+    def fused_mlp_all(xs, quantized_in, inv_scale, gate_lin, up_lin, down_lin, ffn_norm,
+                      use_silu, mode=XT_QUANT_AVX512):
+        """layers.rs:497-645: gate+up on the shared quantised input, SiLU /
+        ReLU^2 (silu_inplace), optional ffn norm, requantisation, down — for
+        every row of quantized_in.  `mode` is the host ISA the reference would
+        run on (it selects silu_inplace's path and the requantisation
+        rounding)."""
+        import torch
+        q = quantized_in.reshape(-1, gate_lin.in_dim).contiguous()
+        if not torch.is_tensor(inv_scale):
+            inv_scale = torch.full((q.shape[0],), float(inv_scale), dtype=torch.float32,
+                                   device=q.device)
+        y = mlp_q(gate_lin.weights, up_lin.weights, down_lin.weights, q, inv_scale,
+                  norm_w=ffn_norm.weight if ffn_norm is not None else None,
+                  eps=ffn_norm.eps if ffn_norm is not None else 0.0, use_silu=use_silu,
+                  mode=mode)
+        return y.reshape(tuple(xs.shape[:-1]) + (down_lin.out_dim,))
+
+
+class FastRmsNorm:
+    """nn::FastRmsNorm: weight [n] (device f32 tensor) and eps; forward is
+    rms_norm on each row (tensor.rs:242-265)."""
+
+    def __init__(self, weight, eps):
+        self.weight = weight.contiguous()
+        self.eps = float(eps)
+
+    def forward(self, xs):
+        return rms_norm(xs, self.weight, self.eps)
+
+
+class Mlp:
+    """models/llama/mlp.rs:33-128 with ternary gate (c_fc1), up (c_fc2) and
+    down (c_proj) projections, optional ffn_layernorm / ffn_sub_norm, and
+    hidden_act "relu2" or "silu"."""
+
+    def __init__(self, c_fc1, c_fc2, c_proj, ffn_layernorm=None, hidden_act="relu2"):
+        if hidden_act not in ("relu2", "silu"):
+            raise XternError(XT_ERR_INVALID, f"unknown activation {hidden_act}")
+        self.c_fc1, self.c_fc2, self.c_proj = c_fc1, c_fc2, c_proj
+        self.ffn_layernorm = ffn_layernorm
+        self.hidden_act = hidden_act
+
+    def forward(self, x, mode=XT_QUANT_AVX512):
+        """One fused launch sequence; one token follows fused_mlp_all, several
+        follow the reference's unfused path (mlp.rs:51-127)."""
+        if x.dim() == 0:
+            raise XternError(XT_ERR_INVALID, "Input must have at least 1 dimension")
+        n = self.ffn_layernorm
+        y = mlp_f32(self.c_fc1.weights, self.c_fc2.weights, self.c_proj.weights, x.contiguous(),
+                    norm_w=n.weight if n is not None else None, eps=n.eps if n is not None else 0.0,
+                    use_silu=self.hidden_act == "silu", mode=mode)
+        return y.reshape(tuple(x.shape[:-1]) + (self.c_proj.out_dim,))
+
+    def weight_bytes(self):
+        """mlp.rs:140-143: packed weight bytes of the three projections."""
+        return sum(l.packed_bytes() for l in (self.c_fc1, self.c_fc2, self.c_proj))
+
+
 class DynamicLinear:
     """dynamic_linear.rs:619-643 — the Ternary arm of LinearKind."""
 
@@ -226,5 +286,5 @@ class DynamicLinear:
         return self.inner.forward_with_quantized(xs, quantized_in, inv_scale)
 
 
-__all__ = ["TernaryLinear", "DynamicLinear", "TernaryRep", "TernaryPackType", "XT_PACK4",
+__all__ = ["TernaryLinear", "DynamicLinear", "TernaryRep", "FastRmsNorm", "Mlp", "TernaryPackType", "XT_PACK4",
            "XT_PACK5"]
