@@ -1138,6 +1138,31 @@ hipError_t launch_hf_tiles(int fmt, const uint8_t* stored, int64_t K, int64_t N,
 
 }  // namespace xt
 
+// XT_MID_STATS (0 in the library) makes the MLP middle kernel record, for
+// its first row, phase timestamps and piece counts into xt_mid_stats, read
+// with xt_debug_mid_stats(); for timing harnesses only.
+#ifndef XT_MID_STATS
+#define XT_MID_STATS 0
+#endif
+#if XT_MID_STATS
+__device__ unsigned long long xt_mid_stats[16];
+#define XT_STAMP(k)                                                             \
+    do {                                                                        \
+        if (blockIdx.x == 0 && threadIdx.x == 0) xt_mid_stats[k] = wall_clock64(); \
+    } while (0)
+#define XT_COUNT(k, v)                                                          \
+    do {                                                                        \
+        if (blockIdx.x == 0 && threadIdx.x == 0) xt_mid_stats[k] = (v);         \
+    } while (0)
+#else
+#define XT_STAMP(k) \
+    do {            \
+    } while (0)
+#define XT_COUNT(k, v) \
+    do {               \
+    } while (0)
+#endif
+
 namespace xt {
 
 // ---------------------------------------------------------------------------
@@ -1240,12 +1265,8 @@ __device__ __forceinline__ float apply_act(int act, float g, float u, bool main_
 // 2^-149 spans [0, 2^-125)); 128 for sums at or beyond 2^128.
 __device__ __forceinline__ int binade_d(double a) {
     if (a == 0.0) return -126;
-    const int e = (int)((__double_as_longlong(a) >> 52) & 0x7ff) - 1023;
+    const int e = __builtin_amdgcn_frexp_exp(a) - 1;  // a = m * 2^(e+1), m in [0.5, 1)
     return e < -126 ? -126 : (e > 128 ? 128 : e);
-}
-__device__ __forceinline__ int binade_f(float s) {
-    const int e = (int)((__float_as_uint(s) >> 23) & 0xff);
-    return e == 0 ? -126 : e - 127;
 }
 
 constexpr int kMidThreads = 1024;
@@ -1254,12 +1275,106 @@ constexpr int kMidCmax = 16;                         // row length <= 16 * 1024
 constexpr int kMidRecMax = 1024;                     // piece records in LDS
 constexpr uint32_t kGrid = 1u << 24;                 // grid points per binade
 
-// Sequential float sum t[0] + t[1] + ... (each partial sum rounded to f32,
-// in index order), the order of rms_norm's sum of squares, computed by the
-// whole workgroup.  Within one binade [2^b, 2^(b+1)) of the running sum every
-// f32 add is an integer add on the grid u = 2^(b-23): fl(s + t) = s +
-// u * round(t / u), except when t / u is an exact half (a tie, whose rounding
-// depends on the parity of s) or when the sum leaves the binade.  So:
+// Wave-wide data movement with DPP (gfx9 encodings): row_shr:n = 0x110 + n
+// shifts within rows of 16 lanes, row_bcast:15 / row_bcast:31 = 0x142 / 0x143
+// broadcast lane 15 / 31 into the following rows, wave_shr:1 = 0x138 and
+// wave_shl:1 = 0x130 shift across the whole wave.  Lanes without a source
+// (or outside ROW_MASK) receive 0.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint32_t dpp32(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, CTRL, ROW_MASK, 0xf, false);
+}
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ uint64_t dpp64(uint64_t v) {
+    const uint32_t lo = dpp32<CTRL, ROW_MASK>((uint32_t)v);
+    const uint32_t hi = dpp32<CTRL, ROW_MASK>((uint32_t)(v >> 32));
+    return ((uint64_t)hi << 32) | lo;
+}
+__device__ __forceinline__ double dpp_d(uint64_t bits) { return __longlong_as_double((long long)bits); }
+__device__ __forceinline__ uint64_t d_bits(double d) { return (uint64_t)__double_as_longlong(d); }
+
+// Inclusive wave scans (Hillis-Steele in rows of 16, then row broadcasts).
+__device__ __forceinline__ double wave_scan_add(double v) {
+    v = __dadd_rn(v, dpp_d(dpp64<0x111, 0xf>(d_bits(v))));
+    v = __dadd_rn(v, dpp_d(dpp64<0x112, 0xf>(d_bits(v))));
+    v = __dadd_rn(v, dpp_d(dpp64<0x114, 0xf>(d_bits(v))));
+    v = __dadd_rn(v, dpp_d(dpp64<0x118, 0xf>(d_bits(v))));
+    v = __dadd_rn(v, dpp_d(dpp64<0x142, 0xa>(d_bits(v))));
+    v = __dadd_rn(v, dpp_d(dpp64<0x143, 0xc>(d_bits(v))));
+    return v;
+}
+__device__ __forceinline__ uint64_t wave_scan_add(uint64_t v) {
+    v += dpp64<0x111, 0xf>(v);
+    v += dpp64<0x112, 0xf>(v);
+    v += dpp64<0x114, 0xf>(v);
+    v += dpp64<0x118, 0xf>(v);
+    v += dpp64<0x142, 0xa>(v);
+    v += dpp64<0x143, 0xc>(v);
+    return v;
+}
+__device__ __forceinline__ uint32_t wave_scan_add(uint32_t v) {
+    v += dpp32<0x111, 0xf>(v);
+    v += dpp32<0x112, 0xf>(v);
+    v += dpp32<0x114, 0xf>(v);
+    v += dpp32<0x118, 0xf>(v);
+    v += dpp32<0x142, 0xa>(v);
+    v += dpp32<0x143, 0xc>(v);
+    return v;
+}
+// Wave maximum of non-negative floats (0 is the identity), in every lane.
+__device__ __forceinline__ float wave_max_nonneg(float v) {
+    v = fmaxf(v, __uint_as_float(dpp32<0x111, 0xf>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(dpp32<0x112, 0xf>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(dpp32<0x114, 0xf>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(dpp32<0x118, 0xf>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(dpp32<0x142, 0xa>(__float_as_uint(v))));
+    v = fmaxf(v, __uint_as_float(dpp32<0x143, 0xc>(__float_as_uint(v))));
+    return __uint_as_float(__builtin_amdgcn_readlane(__float_as_uint(v), 63));
+}
+__device__ __forceinline__ int wave_sum_int(int v) {
+    const uint32_t s = wave_scan_add((uint32_t)v);
+    return (int)__builtin_amdgcn_readlane(s, 63);
+}
+template <typename T>
+__device__ __forceinline__ T lane_read(T v, int k) {
+    if constexpr (sizeof(T) == 8) {
+        const uint64_t b = __builtin_bit_cast(uint64_t, v);
+        const uint32_t lo = __builtin_amdgcn_readlane((uint32_t)b, k);
+        const uint32_t hi = __builtin_amdgcn_readlane((uint32_t)(b >> 32), k);
+        return __builtin_bit_cast(T, ((uint64_t)hi << 32) | lo);
+    } else {
+        return __builtin_bit_cast(T, __builtin_amdgcn_readlane(__builtin_bit_cast(uint32_t, v), k));
+    }
+}
+
+// Integer increment of adding t (finite, >= 0) to a running sum on the grid
+// u = 2^(b-23): q = floor(t / u) (capped at 2^24), r = 0 below half, 1 at an
+// exact half, 2 above.
+__device__ __forceinline__ void grid_split(float t, int b, uint32_t* q, int* r) {
+    const uint32_t bits = __float_as_uint(t);
+    const uint32_t ef = (bits >> 23) & 0xffu;
+    const uint32_t m = ef ? ((bits & 0x7fffffu) | 0x800000u) : (bits & 0x7fffffu);
+    const int et = ef ? (int)ef - 150 : -149;
+    const int shift = (b - 23) - et;
+    // shift <= 0: t is a multiple of u (q = m << -shift, capped at 2^24)
+    const int ls = min(-shift, 24);
+    const uint32_t qup = min(m << max(ls, 0), kGrid);
+    // shift > 0: m < 2^24, so shifts of 25 or more leave q = 0, remainder m
+    const int sc = min(max(shift, 1), 25);
+    const uint32_t qdn = m >> sc;
+    const uint32_t rem = m & ((1u << sc) - 1u), half = 1u << (sc - 1);
+    const int rdn = rem < half ? 0 : (rem == half ? 1 : 2);
+    *q = shift <= 0 ? (m ? qup : 0u) : qdn;
+    *r = shift <= 0 ? 0 : rdn;
+}
+
+// Sequential float sum t[0] + t[1] + ... + t[n-1] (each partial sum rounded
+// to f32, in index order) -- the order of rms_norm's sum of squares --
+// computed by the whole workgroup.  Within one binade [2^b, 2^(b+1)) of the
+// running sum, every f32 add is an integer add on the grid u = 2^(b-23):
+// fl(s + t) = s + u * round(t / u), except when t / u is an exact half (a
+// tie, whose rounding depends on the parity of s) or when the sum leaves the
+// binade.  So:
 //  1. a double prefix sum predicts the binade of the running sum before each
 //     element;
 //  2. elements that are ties, or after which the predicted binade changes,
@@ -1271,162 +1386,183 @@ constexpr uint32_t kGrid = 1u << 24;                 // grid points per binade
 //     are added one by one; the piece's end element is always added with a
 //     real f32 add.
 // The result never depends on the prediction being right, only the speed
-// does.  Requires every t finite and >= 0 (the caller handles NaN / inf);
-// `lt` holds t[i] for i < n in LDS; t of element (wave*C + c)*64 + lane is
-// v[c] * v[c] (v = 0 beyond n).
-__device__ __forceinline__ float exact_seq_sum(const float* v, int C, int n, const float* lt, double* l_tot,
-                               uint64_t* l_gp, int* l_cnt, int* rec_idx, uint64_t* rec_gp,
-                               int* rec_b, float* l_res) {
+// does.  `lt` holds t[0..n) (finite, >= 0) in LDS; thread j handles the
+// contiguous elements [j*E, j*E + E), E = ceil(n / 1024) <= kMidCmax.
+struct SeqSumLds {
+    double wtot[kMidWaves];
+    uint64_t wgp[kMidWaves];
+    int wcnt[kMidWaves];
+    float res;
+};
+
+__device__ __forceinline__ float exact_seq_sum(int n, const float* lt, SeqSumLds& sl,
+                                               int* rec_idx, uint64_t* rec_gp, int* rec_b) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-    // 1. prefix sums in double
-    double incl[kMidCmax];
-    double carry = 0.0;
-#pragma unroll
-    for (int c = 0; c < kMidCmax; ++c) {
-        if (c < C) {
-            double x = (double)__fmul_rn(v[c], v[c]);
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const double y = __shfl_up(x, off, 64);
-                if (lane >= off) x = __dadd_rn(x, y);
-            }
-            incl[c] = __dadd_rn(carry, x);
-            carry = __shfl(incl[c], 63, 64);
-        }
-    }
-    if (lane == 0) l_tot[w] = carry;
+    const int E = (n + kMidThreads - 1) / kMidThreads;
+    const int i0 = tid * E;
+    const int i1 = min(i0 + E, n);  // this thread's elements: [i0, i1)
+    // 1. prefix sums in double: thread-local, then across lanes and waves
+    double acc = 0.0;
+#pragma unroll 1
+    for (int i = i0; i < i1; ++i) acc = __dadd_rn(acc, (double)lt[i]);
+    const double incl = wave_scan_add(acc);
+    const double excl = dpp_d(dpp64<0x138, 0xf>(d_bits(incl)));  // wave_shr:1, lane 0 gets 0
+    const double excl_next = dpp_d(dpp64<0x130, 0xf>(d_bits(excl)));  // wave_shl:1
+    if (lane == 63) sl.wtot[w] = incl;
     __syncthreads();
-    double offw = 0.0;
-    for (int j = 0; j < w; ++j) offw = __dadd_rn(offw, l_tot[j]);
+    XT_STAMP(3);
+    double woff = 0.0;
+    for (int j = 0; j < w; ++j) woff = __dadd_rn(woff, sl.wtot[j]);
+    const double woff_next = __dadd_rn(woff, sl.wtot[w]);
+    // Prefix before this thread's first element, and before the next
+    // thread's first element, computed exactly as that thread computes it.
+    const double off = __dadd_rn(woff, excl);
+    const double off_next = lane < 63 ? __dadd_rn(woff, excl_next) : __dadd_rn(woff_next, 0.0);
 
-    // 2. piece ends, integer increments, their prefix and the end ranks
-    uint64_t gcarry = 0;
-    int ccarry = 0;
-    double last_prev = 0.0;
-    uint64_t gpl[kMidCmax];
-    int meta[kMidCmax];  // bit 0: piece end; bits 1..: binade + 256
-#pragma unroll
-    for (int c = 0; c < kMidCmax; ++c) {
-        gpl[c] = 0;
-        meta[c] = 0;
-        if (c < C) {
-            const int i = (w * C + c) * 64 + lane;
-            const double up = __shfl_up(incl[c], 1, 64);
-            const double excl_local = lane == 0 ? last_prev : up;
-            last_prev = __shfl(incl[c], 63, 64);
-            const double aex = __dadd_rn(offw, excl_local);
-            const double ain = __dadd_rn(offw, incl[c]);
-            const int b = binade_d(aex), bn = binade_d(ain);
-            const uint32_t bits = __float_as_uint(__fmul_rn(v[c], v[c]));
-            const uint32_t et_f = (bits >> 23) & 0xffu;
-            const uint32_t m = et_f ? ((bits & 0x7fffffu) | 0x800000u) : (bits & 0x7fffffu);
-            const int et = et_f ? (int)et_f - 150 : -149;
-            const int shift = (b - 23) - et;
-            uint32_t q = 0;
-            int r = 0;
-            if (shift <= 0) {
-                const int ls = -shift;
-                q = (ls >= 24) ? (m ? kGrid : 0u)
-                               : (uint32_t)min((uint64_t)m << ls, (uint64_t)kGrid);
-            } else if (shift < 26) {
-                q = m >> shift;
-                const uint32_t rem = m & ((1u << shift) - 1u), half = 1u << (shift - 1);
-                r = rem < half ? 0 : (rem == half ? 1 : 2);
-            }
-            const bool valid = i < n;
-            const bool end = valid && (r == 1 || bn != b || i == n - 1);
-            const uint32_t d = (valid && !end) ? min(q + (r == 2 ? 1u : 0u), kGrid) : 0u;
-            meta[c] = (end ? 1 : 0) | ((b + 256) << 1);
-            uint64_t x = d;  // inclusive wave scan
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const uint64_t y = __shfl_up(x, off, 64);
-                if (lane >= off) x += y;
-            }
-            gpl[c] = gcarry + x;
-            gcarry += __shfl(x, 63, 64);
-            ccarry += __popcll(__ballot(end));
+    // 2. The binade before element i is that of off + (local prefix before
+    // i) -- the next thread's `off` after the last element.  Piece ends and
+    // integer increments; run twice (count, then write), recomputing rather
+    // than holding per-element state.
+    uint64_t dsum = 0;
+    uint32_t ends = 0;
+    {
+        double lp = 0.0;
+        int b = binade_d(off);
+#pragma unroll 1
+        for (int i = i0; i < i1; ++i) {
+            const float t = lt[i];
+            lp = __dadd_rn(lp, (double)t);
+            const int bn = (i + 1 < i0 + E) ? binade_d(__dadd_rn(off, lp)) : binade_d(off_next);
+            uint32_t q;
+            int r;
+            grid_split(t, b, &q, &r);
+            const bool end = r == 1 || bn != b || i == n - 1;
+            dsum += end ? 0u : min(q + (r == 2 ? 1u : 0u), kGrid);
+            ends += end ? 1u : 0u;
+            b = bn;
         }
     }
-    if (lane == 0) {
-        l_gp[w] = gcarry;
-        l_cnt[w] = ccarry;
+    const uint64_t gincl = wave_scan_add(dsum);
+    const uint32_t cincl = wave_scan_add(ends);
+    if (lane == 63) {
+        sl.wgp[w] = gincl;
+        sl.wcnt[w] = (int)cincl;
     }
     __syncthreads();
-    uint64_t goff = 0;
-    int coff = 0;
-    for (int j = 0; j < w; ++j) {
-        goff += l_gp[j];
-        coff += l_cnt[j];
-    }
+    XT_STAMP(4);
+    uint64_t goff = gincl - dsum;
+    int coff = (int)(cincl - ends);
     int total_ends = 0;
-    for (int j = 0; j < kMidWaves; ++j) total_ends += l_cnt[j];
+    for (int j = 0; j < kMidWaves; ++j) {
+        if (j < w) {
+            goff += sl.wgp[j];
+            coff += sl.wcnt[j];
+        }
+        total_ends += sl.wcnt[j];
+    }
     const bool overflow = total_ends > kMidRecMax;
-    int crun = coff;
-#pragma unroll
-    for (int c = 0; c < kMidCmax; ++c) {
-        if (c < C) {
-            const bool end = meta[c] & 1;
-            const uint64_t mask = __ballot(end);
-            if (end && !overflow) {
-                const int rank = crun + __popcll(mask & ((1ull << lane) - 1ull));
-                rec_idx[rank] = (w * C + c) * 64 + lane;
-                // own increment is 0, so the inclusive prefix is the exclusive one
-                rec_gp[rank] = goff + gpl[c];
-                rec_b[rank] = (meta[c] >> 1) - 256;
+    if (!overflow && ends) {
+        double lp = 0.0;
+        int b = binade_d(off);
+        int rank = coff;
+        uint64_t gp = goff;
+#pragma unroll 1
+        for (int i = i0; i < i1; ++i) {
+            const float t = lt[i];
+            lp = __dadd_rn(lp, (double)t);
+            const int bn = (i + 1 < i0 + E) ? binade_d(__dadd_rn(off, lp)) : binade_d(off_next);
+            uint32_t q;
+            int r;
+            grid_split(t, b, &q, &r);
+            const bool end = r == 1 || bn != b || i == n - 1;
+            if (end) {
+                rec_idx[rank] = i;
+                rec_gp[rank] = gp;  // own increment is 0
+                rec_b[rank] = b;
+                ++rank;
+            } else {
+                gp += min(q + (r == 2 ? 1u : 0u), kGrid);
             }
-            crun += __popcll(mask);
+            b = bn;
         }
     }
     __syncthreads();
+    XT_STAMP(5);
 
-    // 3. walk the pieces (wave 0, every lane runs the same uniform code)
+    // 3. walk the pieces (wave 0).  Records are loaded 64 at a time, one per
+    // lane, with everything that does not depend on the running sum; the
+    // sequential part reads them with readlane.
     if (w == 0) {
+#if XT_MID_STATS
+        int n_fb = 0, n_fb_el = 0;
+#endif
         float s = 0.0f;
         if (overflow) {
             for (int j = 0; j < n; ++j) s = __fadd_rn(s, lt[j]);
         } else {
-            int prev_idx = -1;
-            uint64_t prev_gp = 0;
-            for (int k = 0; k < total_ends; ++k) {
-                if (__builtin_isinf(s)) break;
-                const int idx = rec_idx[k];
-                const uint64_t gp = rec_gp[k];
-                const int b = rec_b[k];
-                const int start = prev_idx + 1;
-                if (start < idx) {
-                    const uint64_t P = gp - prev_gp;
-                    bool ok = binade_f(s) == b && b <= 127 && P < kGrid;
-                    double S = 0.0;
-                    if (ok) {
-                        S = ldexp((double)s, 23 - b);
-                        ok = S + (double)P < (double)kGrid;
-                    }
-                    if (ok) {
-                        s = (float)ldexp(S + (double)P, b - 23);
-                    } else {
-                        for (int j = start; j < idx; ++j) s = __fadd_rn(s, lt[j]);
-                    }
+            for (int k0 = 0; k0 < total_ends; k0 += 64) {
+                const int k = k0 + lane;
+                int idx = 0, start = 0, rb = 0;
+                uint64_t P = 0;
+                float tend = 0.0f;
+                if (k < total_ends) {
+                    idx = rec_idx[k];
+                    rb = rec_b[k];
+                    const uint64_t gp = rec_gp[k];
+                    start = k > 0 ? rec_idx[k - 1] + 1 : 0;
+                    P = gp - (k > 0 ? rec_gp[k - 1] : 0ull);
+                    tend = lt[idx];
                 }
-                s = __fadd_rn(s, lt[idx]);
-                prev_idx = idx;
-                prev_gp = gp;
+                const int kn = min(64, total_ends - k0);
+                for (int kk = 0; kk < kn; ++kk) {
+                    const int sidx = lane_read(idx, kk), sstart = lane_read(start, kk);
+                    const int sb = lane_read(rb, kk);
+                    const uint64_t sP = lane_read(P, kk);
+                    const float st = lane_read(tend, kk);
+                    if (sstart < sidx) {
+                        // Inside binade b the running sum is S * 2^(b-23) with
+                        // S its significand (implicit bit included; for b =
+                        // -126 the subnormal or smallest-normal encoding).
+                        const uint32_t sbits = __float_as_uint(s);
+                        const int se = (int)(sbits >> 23);  // s >= 0
+                        const int bs = se == 0 ? -126 : se - 127;
+                        const uint32_t S = (sbits & 0x7fffffu) | (se ? 0x800000u : 0u);
+                        const uint64_t T = (uint64_t)S + sP;
+                        if (bs == sb && sb <= 127 && T < kGrid) {
+                            const uint32_t nb = (T >= 0x800000u)
+                                                    ? ((uint32_t)(sb + 127) << 23) | ((uint32_t)T & 0x7fffffu)
+                                                    : (uint32_t)T;  // b = -126, subnormal
+                            s = __uint_as_float(nb);
+                        } else {
+#if XT_MID_STATS
+                            ++n_fb;
+                            n_fb_el += sidx - sstart;
+#endif
+                            for (int j = sstart; j < sidx; ++j) s = __fadd_rn(s, lt[j]);
+                        }
+                    }
+                    s = __fadd_rn(s, st);
+                }
             }
         }
-        if (lane == 0) *l_res = s;
+        if (lane == 0) sl.res = s;
+#if XT_MID_STATS
+        XT_COUNT(8, total_ends);
+        XT_COUNT(9, n_fb);
+        XT_COUNT(10, n_fb_el);
+#endif
     }
+    XT_STAMP(6);
     __syncthreads();
-    return *l_res;
+    return sl.res;
 }
 
 // One workgroup (16 waves) per row.  Element i = (wave*C + c)*64 + lane is
 // held in registers from the load to the quantisation.
+template <int ACT>
 __global__ __launch_bounds__(kMidThreads) void mlp_mid_kernel(MidArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
-    __shared__ double l_tot[kMidWaves];
-    __shared__ uint64_t l_gp[kMidWaves];
-    __shared__ int l_cnt[kMidWaves];
-    __shared__ float l_res;
+    __shared__ SeqSumLds sl;
     __shared__ float sm_f[kMidWaves];
     __shared__ int sm_i[kMidWaves];
     const int m = blockIdx.x;
@@ -1435,33 +1571,42 @@ __global__ __launch_bounds__(kMidThreads) void mlp_mid_kernel(MidArgs a) {
     const int nmain = (n / 16) * 16;
     const float* gr = a.gate + (size_t)m * a.ldg;
     const float* ur = a.up + (size_t)m * a.ldg;
+    XT_STAMP(0);
     float v[kMidCmax];
 #pragma unroll
     for (int c = 0; c < kMidCmax; ++c) {
         const int i = (w * C + c) * 64 + lane;
-        v[c] = (c < C && i < n) ? apply_act(a.act, gr[i], a.up ? ur[i] : 0.0f, i < nmain) : 0.0f;
+        v[c] = (c < C && i < n) ? apply_act(ACT, gr[i], ACT == kActIdentity ? 0.0f : ur[i], i < nmain)
+                                : 0.0f;
     }
+    XT_STAMP(1);
     if (a.norm_w) {
         float* lt = reinterpret_cast<float*>(lds);
         int* rec_idx = reinterpret_cast<int*>(lds + (size_t)C * kMidThreads * 4);
         int* rec_b = rec_idx + kMidRecMax;
         uint64_t* rec_gp = reinterpret_cast<uint64_t*>(rec_b + kMidRecMax);
-        int flags = 0;
+        bool bad_nan = false, bad_inf = false;
 #pragma unroll
         for (int c = 0; c < kMidCmax; ++c) {
             const int i = (w * C + c) * 64 + lane;
             const float t = __fmul_rn(v[c], v[c]);
             if (c < C && i < n) {
                 lt[i] = t;
-                if (t != t) flags |= 1;
-                else if (__builtin_isinf(t)) flags |= 2;
+                bad_nan |= (t != t);
+                bad_inf |= (bool)__builtin_isinf(t);
             }
         }
-        flags = block_reduce(flags, OrOp(), sm_i);
+        const int wf = (__ballot(bad_nan) ? 1 : 0) | (__ballot(bad_inf) ? 2 : 0);
+        if (lane == 0) sm_i[w] = wf;
+        __syncthreads();
+        int flags = 0;
+#pragma unroll
+        for (int j = 0; j < kMidWaves; ++j) flags |= sm_i[j];
+        XT_STAMP(2);
         float sum;
         if (flags & 1) sum = __builtin_nanf("");
         else if (flags & 2) sum = __builtin_inff();
-        else sum = exact_seq_sum(v, C, n, lt, l_tot, l_gp, l_cnt, rec_idx, rec_gp, rec_b, &l_res);
+        else sum = exact_seq_sum(n, lt, sl, rec_idx, rec_gp, rec_b);
         // fast_attention_simd.rs:485-486.  sqrtf is correctly rounded on the
         // host; the hardware f32 square root is not, so take the correctly
         // rounded double root and round it once (exact: 53 >= 2*24 + 2).
@@ -1474,6 +1619,7 @@ __global__ __launch_bounds__(kMidThreads) void mlp_mid_kernel(MidArgs a) {
             if (c < C && i < n) v[c] = __fmul_rn(__fmul_rn(v[c], invr), a.norm_w[i]);
         }
     }
+    XT_STAMP(11);
     if (a.out) {
         float* orow = a.out + (size_t)m * a.ldo;
 #pragma unroll
@@ -1486,7 +1632,12 @@ __global__ __launch_bounds__(kMidThreads) void mlp_mid_kernel(MidArgs a) {
     float mx = 0.0f;
 #pragma unroll
     for (int c = 0; c < kMidCmax; ++c) mx = fmaxf(mx, fabsf(v[c]));
-    mx = block_reduce(mx, MaxOp(), sm_f);
+    mx = wave_max_nonneg(mx);
+    if (lane == 0) sm_f[w] = mx;
+    __syncthreads();
+    mx = 0.0f;
+#pragma unroll
+    for (int j = 0; j < kMidWaves; ++j) mx = fmaxf(mx, sm_f[j]);
     const float scale = (mx > 0.0f) ? __fdiv_rn(127.0f, mx) : 1.0f;
     const float invs = (mx > 0.0f) ? __fdiv_rn(mx, 127.0f) : 1.0f;
     int8_t* qr = a.q + (size_t)m * a.ldq;
@@ -1501,11 +1652,17 @@ __global__ __launch_bounds__(kMidThreads) void mlp_mid_kernel(MidArgs a) {
         }
     }
     for (int i = n + tid; i < a.ldq; i += kMidThreads) qr[i] = 0;
-    sum = block_reduce(sum, AddOp(), sm_i);
+    sum = wave_sum_int(sum);
+    __syncthreads();  // sm_i reuse after the flag reads
+    if (lane == 0) sm_i[w] = sum;
+    __syncthreads();
     if (tid == 0) {
+        int tot = 0;
+        for (int j = 0; j < kMidWaves; ++j) tot += sm_i[j];
         a.inv[m] = invs;
-        if (a.rowsum) a.rowsum[m] = sum;
+        if (a.rowsum) a.rowsum[m] = tot;
     }
+    XT_STAMP(7);
 }
 
 int mid_max_cols() { return kMidCmax * kMidThreads; }
@@ -1516,8 +1673,37 @@ hipError_t launch_mlp_mid(const MidArgs& a0, int M, hipStream_t s) {
     a.C = (a.n + kMidThreads - 1) / kMidThreads;
     if (a.n <= 0 || a.C > kMidCmax) return hipErrorInvalidValue;
     const size_t lds = a.norm_w ? (size_t)a.C * kMidThreads * 4 + (size_t)kMidRecMax * 16 : 0;
-    hipLaunchKernelGGL(mlp_mid_kernel, dim3(M), dim3(kMidThreads), lds, s, a);
+    switch (a.act) {
+        case XT_ACT_RELU2_MUL:
+            hipLaunchKernelGGL(mlp_mid_kernel<XT_ACT_RELU2_MUL>, dim3(M), dim3(kMidThreads), lds, s, a);
+            break;
+        case XT_ACT_SILU_INPLACE_AVX512:
+            hipLaunchKernelGGL(mlp_mid_kernel<XT_ACT_SILU_INPLACE_AVX512>, dim3(M), dim3(kMidThreads),
+                               lds, s, a);
+            break;
+        case XT_ACT_SILU_INPLACE_SCALAR:
+            hipLaunchKernelGGL(mlp_mid_kernel<XT_ACT_SILU_INPLACE_SCALAR>, dim3(M), dim3(kMidThreads),
+                               lds, s, a);
+            break;
+        case XT_ACT_SILU_MUL:
+            hipLaunchKernelGGL(mlp_mid_kernel<XT_ACT_SILU_MUL>, dim3(M), dim3(kMidThreads), lds, s, a);
+            break;
+        case kActIdentity:
+            hipLaunchKernelGGL(mlp_mid_kernel<kActIdentity>, dim3(M), dim3(kMidThreads), lds, s, a);
+            break;
+        default:
+            return hipErrorInvalidValue;
+    }
     return hipGetLastError();
 }
 
 }  // namespace xt
+
+#if XT_MID_STATS
+extern "C" int xt_debug_mid_stats(unsigned long long* out) {
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(xt_mid_stats), sizeof(unsigned long long) * 16) ==
+                   hipSuccess
+               ? 0
+               : -2;
+}
+#endif
