@@ -119,6 +119,51 @@ int xt_weights_create_hf(int fmt, int64_t in_dim, int64_t out_dim, const void* s
                          size_t nbytes, float weight_scale, int is_inverted_scale,
                          xt_weights** out);
 
+/* ---- XorSparse container ("XORSPARE1", SPARSE_FORMAT.md:30-50) ----
+ * Layout as SparseFile::serialize writes it (src/loader/sparse_loader.rs:
+ * 124-139): magic "XORSPARE1" (9 bytes), version u32 = 1 at byte 9,
+ * num_tensors u32 at byte 13, then per tensor name_len u32, name, out_dim
+ * u32, in_dim u32, w_scale f32, blob_len u32, blob (XorSparse row blobs).
+ * The reference's reader reads the version at byte 8 and so rejects every
+ * file; these entry points read what the writer writes. */
+typedef struct xt_sparse_file xt_sparse_file;
+
+/* Parse a container held in memory (copied; the caller may free `data`).
+ * Replaces SparseFile::from_bytes / open (sparse_loader.rs:41-104); every
+ * length is bounds-checked.  A repeated name resolves to its last entry, as
+ * the reference's HashMap insert does. */
+int xt_sparse_file_open(const void* data, size_t len, xt_sparse_file** out);
+int xt_sparse_file_close(xt_sparse_file* f);
+int xt_sparse_file_count(const xt_sparse_file* f, int64_t* n);
+/* Directory entry `idx`; the name and blob pointers stay valid until close. */
+int xt_sparse_file_entry(const xt_sparse_file* f, int64_t idx, const char** name, int64_t* out_dim,
+                         int64_t* in_dim, float* w_scale, const void** blob, size_t* blob_len);
+int xt_sparse_file_find(const xt_sparse_file* f, const char* name, int64_t* idx);
+/* SparseFile::get_sparse (sparse_loader.rs:106-122) plus the sparse arm of
+ * DynamicLinear::load (src/nn/dynamic_linear.rs:697-716): shape check with
+ * the reference's message, w_scales = out_dim copies of the entry's scale,
+ * upload as XT_XORSPARSE. */
+int xt_weights_create_from_sparse_file(const xt_sparse_file* f, const char* name, int64_t in_dim,
+                                       int64_t out_dim, xt_weights** out);
+/* SparseFile::serialize (sparse_loader.rs:124-139) into `out`; the size is
+ * xt_sparse_file_serialized_size(n, names, blob_lens) (0 on bad input). */
+size_t xt_sparse_file_serialized_size(int64_t n, const char* const* names, const size_t* blob_lens);
+int xt_sparse_file_serialize(int64_t n, const char* const* names, const int64_t* out_dims,
+                             const int64_t* in_dims, const float* w_scales,
+                             const void* const* blobs, const size_t* blob_lens, void* out,
+                             size_t out_len);
+/* The per-tensor step of convert_sparse (src/bin/convert_sparse.rs:86-126):
+ * HF striped U8 bytes [out_dim/f][in_dim] -> XorSparse row blob
+ * (encode_sparse_tensor, src/bit1_58/sparse.rs:61-103).  destripe != 0 maps
+ * rows as get_prepacked_ternary does (row j*(out_dim/f) + p from digit j of
+ * byte [p][i]), so the blob's rows are the engine's dense rows; destripe == 0
+ * reproduces the reference converter, which unpacks the bytes linearly
+ * (convert_sparse.rs:104) and so permutes the rows.  *blob_len receives the
+ * size; with blob_out NULL nothing else is written. */
+int xt_hf_to_sparse_blob(int fmt, int64_t in_dim, int64_t out_dim, const void* stored,
+                         size_t nbytes, int destripe, void* blob_out, size_t cap,
+                         size_t* blob_len);
+
 /* Copy a handle's device tiles (xt_tile_bytes() bytes) to host memory, after
  * waiting for the device.  No reference counterpart: lets tests compare
  * tiles built on the device with xt_repack_host's. */

@@ -254,6 +254,56 @@ def mlp_forward(x, gate, up, down, norm_w, eps, use_silu, quant_mode=0, fused=No
     return y.reshape(x.shape[:-1] + (down[2],)), q, inv
 
 
+def sparse_container_serialize(entries):
+    """SparseFile::serialize (src/loader/sparse_loader.rs:124-139):
+    entries = [(name, out_dim, in_dim, w_scale, blob)]."""
+    import struct
+    out = bytearray(b"XORSPARE1")
+    out += struct.pack("<I", 1)
+    out += struct.pack("<I", len(entries))
+    for name, od, idim, ws, blob in entries:
+        nb = name.encode()
+        out += struct.pack("<I", len(nb)) + nb
+        out += struct.pack("<IIfI", od, idim, ws, len(blob))
+        out += bytes(blob)
+    return bytes(out)
+
+
+def sparse_container_parse(data):
+    """The layout serialize writes (SPARSE_FORMAT.md:30-50): a dict
+    name -> (out_dim, in_dim, w_scale, blob); later duplicates win."""
+    import struct
+    if data[:9] != b"XORSPARE1":
+        raise ValueError("bad magic")
+    ver, n = struct.unpack_from("<II", data, 9)
+    if ver != 1:
+        raise ValueError("version")
+    p, out = 17, {}
+    for _ in range(n):
+        (nl,) = struct.unpack_from("<I", data, p)
+        name = data[p + 4:p + 4 + nl].decode()
+        p += 4 + nl
+        od, idim, ws, bl = struct.unpack_from("<IIfI", data, p)
+        p += 16
+        out[name] = (od, idim, ws, bytes(data[p:p + bl]))
+        p += bl
+    return out
+
+
+def convert_sparse_tensor(stored, in_dim, out_dim, destripe=True):
+    """convert_sparse.rs:101-105 for one Pack4 tensor: the linear unpack of
+    the stored bytes (destripe=False, as the reference does) or the
+    get_prepacked_ternary destripe (loader/mod.rs:351-390), then
+    encode_sparse_tensor (sparse.rs:90-103).  Returns the blob."""
+    if destripe:
+        packed = hf_destripe(0, in_dim, out_dim, stored)
+        vals = np.concatenate([unpack4(packed[o * ((in_dim + 3) // 4):(o + 1) * ((in_dim + 3) // 4)],
+                                       in_dim) for o in range(out_dim)])
+    else:
+        vals = unpack4(np.asarray(stored, np.uint8).ravel(), in_dim * out_dim)
+    return sparse_encode_tensor(vals.astype(np.int8), in_dim, out_dim)[0]
+
+
 class Lcg:
     """The reference's test RNG (simd.rs:556-565)."""
 

@@ -317,6 +317,9 @@ int mlp_run(const xt_weights* gate, const xt_weights* up, const xt_weights* down
 
 }  // namespace
 
+// Error reporting for the other host source files (xtern_container.cpp).
+int xt_internal_fail(int code, const std::string& msg) { return fail(code, msg); }
+
 extern "C" {
 
 const char* xt_version(void) { return "xtern 0.1 gfx950"; }

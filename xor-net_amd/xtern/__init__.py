@@ -78,6 +78,21 @@ _lib.xt_ternary_mlp_q.argtypes = [_vp, _vp, _vp, _vp, ctypes.c_float, ctypes.c_i
                                   _i64, _vp, ctypes.c_int, _vp]
 _lib.xt_ternary_mlp_f32.argtypes = [_vp, _vp, _vp, _vp, ctypes.c_float, ctypes.c_int, _vp, _i64,
                                     _vp, ctypes.c_int, _vp]
+_lib.xt_sparse_file_open.argtypes = [_vp, _sz, ctypes.POINTER(_vp)]
+_lib.xt_sparse_file_close.argtypes = [_vp]
+_lib.xt_sparse_file_count.argtypes = [_vp, ctypes.POINTER(_i64)]
+_lib.xt_sparse_file_entry.argtypes = [_vp, _i64, ctypes.POINTER(ctypes.c_char_p),
+                                      ctypes.POINTER(_i64), ctypes.POINTER(_i64),
+                                      ctypes.POINTER(ctypes.c_float), ctypes.POINTER(_vp),
+                                      ctypes.POINTER(_sz)]
+_lib.xt_sparse_file_find.argtypes = [_vp, ctypes.c_char_p, ctypes.POINTER(_i64)]
+_lib.xt_weights_create_from_sparse_file.argtypes = [_vp, ctypes.c_char_p, _i64, _i64,
+                                                    ctypes.POINTER(_vp)]
+_lib.xt_sparse_file_serialized_size.argtypes = [_i64, _vp, _vp]
+_lib.xt_sparse_file_serialized_size.restype = _sz
+_lib.xt_sparse_file_serialize.argtypes = [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz]
+_lib.xt_hf_to_sparse_blob.argtypes = [ctypes.c_int, _i64, _i64, _vp, _sz, ctypes.c_int, _vp, _sz,
+                                      ctypes.POINTER(_sz)]
 _lib.xt_quantize_i8.argtypes = [_vp, _i64, _i64, _vp, _vp, ctypes.c_int, _vp]
 _lib.xt_quantize_i8_rowsum.argtypes = [_vp, _i64, _i64, _vp, _vp, _vp, ctypes.c_int, _vp]
 _lib.xt_ternary_linear_q.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp, _vp]
@@ -343,6 +358,133 @@ def get_prepacked_ternary(stored, stored_dtype, expected_shape, pack_type, weigh
     ws = np.float32(1.0) / s if is_inverted_scale else s
     packed = hf_destripe(pack_type.value, in_dim, out_dim, stored)
     return packed, np.full(out_dim, ws, dtype=np.float32), in_dim, out_dim
+
+
+class SparseFile:
+    """sparse_loader.rs:34-140 — a parsed XorSparse container (xt_sparse_file)."""
+
+    def __init__(self, handle):
+        self.handle = handle
+
+    @classmethod
+    def from_bytes(cls, data):
+        buf = np.frombuffer(bytes(data), dtype=np.uint8)
+        h = ctypes.c_void_p()
+        _check(_lib.xt_sparse_file_open(buf.ctypes.data_as(_vp), buf.size, ctypes.byref(h)))
+        return cls(h)
+
+    @classmethod
+    def open(cls, path):
+        with open(path, "rb") as f:
+            return cls.from_bytes(f.read())
+
+    def __len__(self):
+        n = _i64()
+        _check(_lib.xt_sparse_file_count(self.handle, ctypes.byref(n)))
+        return n.value
+
+    def entry(self, idx):
+        """(name, out_dim, in_dim, w_scale, blob bytes) of entry idx."""
+        name, od, idim = ctypes.c_char_p(), _i64(), _i64()
+        ws, blob, bl = ctypes.c_float(), _vp(), _sz()
+        _check(_lib.xt_sparse_file_entry(self.handle, idx, ctypes.byref(name), ctypes.byref(od),
+                                         ctypes.byref(idim), ctypes.byref(ws), ctypes.byref(blob),
+                                         ctypes.byref(bl)))
+        data = ctypes.string_at(blob.value, bl.value) if bl.value else b""
+        return name.value.decode("utf-8", "surrogateescape"), od.value, idim.value, ws.value, data
+
+    def names(self):
+        return [self.entry(i)[0] for i in range(len(self))]
+
+    def get_sparse(self, name, in_dim, out_dim):
+        """sparse_loader.rs:106-122: (blob, w_scale) after the shape check."""
+        idx = _i64()
+        _check(_lib.xt_sparse_file_find(self.handle, name.encode(), ctypes.byref(idx)))
+        _, od, idim, ws, blob = self.entry(idx.value)
+        if od != out_dim or idim != in_dim:
+            raise XternError(XT_ERR_INVALID,
+                             f"XorSparse '{name}' shape mismatch: expected [{out_dim}, {in_dim}], "
+                             f"got [{od}, {idim}]")
+        return blob, ws
+
+    def device_weights(self, name, in_dim, out_dim):
+        """xt_weights_create_from_sparse_file: the entry uploaded as XorSparse."""
+        h = ctypes.c_void_p()
+        _check(_lib.xt_weights_create_from_sparse_file(self.handle, name.encode(), in_dim, out_dim,
+                                                       ctypes.byref(h)))
+        dw = DeviceWeights.__new__(DeviceWeights)
+        dw.handle = h
+        dw.fmt, dw.in_dim, dw.out_dim = XT_XORSPARSE, in_dim, out_dim
+        return dw
+
+    @staticmethod
+    def serialize(entries):
+        """sparse_loader.rs:124-139: entries = [(name, out_dim, in_dim, w_scale, blob)]."""
+        n = len(entries)
+        names = (ctypes.c_char_p * max(n, 1))(*[e[0].encode() for e in entries])
+        od = (ctypes.c_int64 * max(n, 1))(*[e[1] for e in entries])
+        idim = (ctypes.c_int64 * max(n, 1))(*[e[2] for e in entries])
+        ws = (ctypes.c_float * max(n, 1))(*[e[3] for e in entries])
+        blobs_b = [bytes(e[4]) for e in entries]
+        blobs = (ctypes.c_void_p * max(n, 1))(*[ctypes.cast(ctypes.c_char_p(b), ctypes.c_void_p)
+                                                 for b in blobs_b])
+        lens = (ctypes.c_size_t * max(n, 1))(*[len(b) for b in blobs_b])
+        size = _lib.xt_sparse_file_serialized_size(n, names, lens)
+        out = np.zeros(size, np.uint8)
+        _check(_lib.xt_sparse_file_serialize(n, names, od, idim, ws, blobs, lens,
+                                             out.ctypes.data_as(_vp), out.size))
+        return out.tobytes()
+
+    def close(self):
+        if self.handle:
+            _lib.xt_sparse_file_close(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+
+def hf_to_sparse_blob(fmt, in_dim, out_dim, stored, destripe=True):
+    """xt_hf_to_sparse_blob: HF striped U8 bytes -> XorSparse row blob."""
+    src = np.ascontiguousarray(np.asarray(stored, dtype=np.uint8).ravel())
+    n = _sz()
+    _check(_lib.xt_hf_to_sparse_blob(fmt, in_dim, out_dim, src.ctypes.data_as(_vp), src.size,
+                                     int(bool(destripe)), None, 0, ctypes.byref(n)))
+    out = np.zeros(n.value, np.uint8)
+    _check(_lib.xt_hf_to_sparse_blob(fmt, in_dim, out_dim, src.ctypes.data_as(_vp), src.size,
+                                     int(bool(destripe)), out.ctypes.data_as(_vp), out.size,
+                                     ctypes.byref(n)))
+    return out.tobytes()
+
+
+def convert_sparse(tensors, invert=True, destripe=True):
+    """convert_sparse (src/bin/convert_sparse.rs:86-139) over already-read
+    checkpoint tensors: `tensors` maps names to arrays; every 2-D uint8
+    `*.weight` with a `<name>_scale` companion is converted (Pack4, out_dim =
+    4 * stored rows) with scale 1/s (invert) or s.  Returns the container
+    bytes.  destripe=False reproduces the reference converter's row order."""
+    entries = []
+    for name in sorted(tensors):
+        arr = np.asarray(tensors[name])
+        if not name.endswith(".weight") or arr.dtype != np.uint8 or arr.ndim != 2:
+            continue
+        sk = name + "_scale"
+        if sk not in tensors:
+            continue
+        stored_out, in_dim = arr.shape
+        out_dim = stored_out * 4
+        if out_dim == 0 or in_dim == 0:
+            continue
+        s = np.float32(np.asarray(tensors[sk], dtype=np.float32).ravel()[0])
+        ws = np.float32(1.0) / s if invert else s
+        blob = hf_to_sparse_blob(XT_PACK4, in_dim, out_dim, arr, destripe=destripe)
+        entries.append((name, out_dim, in_dim, float(ws), blob))
+    if not entries:
+        raise XternError(XT_ERR_INVALID, "no packed-ternary weight tensors found to convert")
+    return SparseFile.serialize(entries)
 
 
 def quantize_i8(x, mode=XT_QUANT_AVX512, stream=None):

@@ -138,6 +138,15 @@ class TernaryLinear:
                                     is_inverted_scale)
         return cls(TernaryRep.Dense, in_dim, out_dim, pack_type, ws, None, weights=dev)
 
+    @classmethod
+    def from_sparse_file(cls, sparse_file, name, in_dim, out_dim,
+                         pack_type=TernaryPackType.Pack4):
+        """DynamicLinear::load's XorSparse-container arm (dynamic_linear.rs:
+        697-716): the named entry, w_scales = out_dim copies of its scale."""
+        blob, ws = sparse_file.get_sparse(name, in_dim, out_dim)
+        return cls(TernaryRep.Sparse, in_dim, out_dim, pack_type,
+                   np.full(out_dim, ws, np.float32), np.frombuffer(blob, np.uint8))
+
     # --- queries ----------------------------------------------------------
 
     def packed_bytes(self):
