@@ -43,7 +43,13 @@ enum {
  *   XT_XORSPARSE the XorSparse row blob: per row u32 num_blocks, then per
  *                64-block u64 mask + ceil(popcount/8) set-order sign bytes
  *                (src/bit1_58/sparse.rs:9-17, :61-86)                        */
-enum { XT_PACK4 = 0, XT_PACK5 = 1, XT_XORSPARSE = 2 };
+/*   XT_INT8      Int8Linear::weight_i8, [out_dim][in_dim] i8 with per-row
+ *                scales (src/nn/dynamic_linear.rs:229-258)
+ *   XT_INT4      Int4Linear::weight_i4, [out_dim][ceil(in_dim/2)] bytes, two
+ *                two's-complement nibbles per byte, column 2c low
+ *                (dynamic_linear.rs:382-410).  As in Int4Linear's dot, the
+ *                last column of an odd in_dim contributes nothing. */
+enum { XT_PACK4 = 0, XT_PACK5 = 1, XT_XORSPARSE = 2, XT_INT8 = 3, XT_INT4 = 4 };
 
 /* Activation rounding: which of the reference's two quantiser paths to
  * reproduce bit for bit (src/bit1_58/quantization.rs:170-195).
@@ -88,7 +94,10 @@ const char* xt_last_error(void);
  * host layout (see the enum above); `w_scales` holds out_dim floats (one per
  * output row, as TernaryLinear::w_scales).  The bytes are repacked once into
  * the device tile layout on the calling thread and copied to the current
- * device.  Replaces DynamicLinear::new_ternary_direct
+ * device.  XT_INT8 / XT_INT4 handles (the LM head's Int8Linear / Int4Linear)
+ * work with the same product entry points (xt_ternary_linear_q / _f32),
+ * computing (f32)dot_i32 * inv_scale * scale[o] as Int8Linear::forward /
+ * Int4Linear::forward do (dynamic_linear.rs:260-375, :412-535).  Replaces DynamicLinear::new_ternary_direct
  * (src/nn/dynamic_linear.rs:670-680), TernaryLinear::new_sparse_from_packed
  * (src/bit1_58/layers.rs:183-210) and, for XT_XORSPARSE,
  * SparseTernary::from_blob (src/bit1_58/sparse.rs:135-194). */
@@ -168,6 +177,15 @@ int xt_hf_to_sparse_blob(int fmt, int64_t in_dim, int64_t out_dim, const void* s
  * waiting for the device.  No reference counterpart: lets tests compare
  * tiles built on the device with xt_repack_host's. */
 int xt_weights_read_tiles(const xt_weights* w, void* host_out, size_t nbytes);
+
+/* Int8Linear::new (bits = 8, dynamic_linear.rs:236-258) / Int4Linear::new
+ * (bits = 4, :389-410) on the host: per output row scale = absmax / 127
+ * (or / 7; 1.0 for an all-zero row) and q = round(w / scale) clamped to
+ * [-127, 127] ([-8, 7]).  `out` receives out_dim * in_dim (Int8) or
+ * out_dim * ceil(in_dim / 2) (Int4) bytes in the XT_INT8 / XT_INT4 host
+ * layout, `scales` out_dim floats. */
+int xt_int_quantize_host(int bits, const float* w, int64_t out_dim, int64_t in_dim, void* out,
+                         float* scales);
 
 /* Free a handle (NULL is a no-op).  Waits for the device first. */
 int xt_weights_destroy(xt_weights* w);

@@ -46,6 +46,8 @@ _o.or_silu_inplace.argtypes = [_vp, _vp, _i64, ctypes.c_int, ctypes.c_int]
 _o.or_act_mul_inplace.argtypes = [_vp, _vp, _i64, ctypes.c_int]
 _o.or_rms_norm.argtypes = [_vp, _vp, _i64, ctypes.c_float]
 _o.or_rms_norm.restype = ctypes.c_float
+_o.or_int_new.argtypes = [ctypes.c_int, _vp, _i64, _i64, _vp, _vp]
+_o.or_int_forward.argtypes = [ctypes.c_int, _vp, _vp, _i64, _i64, _vp, _i64, _vp, _vp, ctypes.c_int]
 _o.or_lcg_next.argtypes = [ctypes.POINTER(ctypes.c_uint64)]
 _o.or_lcg_next.restype = ctypes.c_uint64
 _o.or_cpu_has_vnni.restype = ctypes.c_int
@@ -302,6 +304,26 @@ def convert_sparse_tensor(stored, in_dim, out_dim, destripe=True):
     else:
         vals = unpack4(np.asarray(stored, np.uint8).ravel(), in_dim * out_dim)
     return sparse_encode_tensor(vals.astype(np.int8), in_dim, out_dim)[0]
+
+
+def int_new(bits, w, N, K):
+    """Int8Linear::new / Int4Linear::new: (weight bytes, scales)."""
+    wv = _c(w, np.float32).reshape(N, K)
+    out = np.zeros(N * (K if bits == 8 else (K + 1) // 2), np.uint8)
+    sc = np.zeros(N, np.float32)
+    _o.or_int_new(bits, _p(wv), N, K, _p(out), _p(sc))
+    return out, sc
+
+
+def int_forward(bits, wbytes, scales, K, N, x, quant_mode=0):
+    """Int8Linear::forward / Int4Linear::forward: (y, acc)."""
+    xv = _c(x, np.float32).reshape(-1, K)
+    M = xv.shape[0]
+    y = np.zeros((M, N), np.float32)
+    acc = np.zeros((M, N), np.int32)
+    _o.or_int_forward(bits, _p(_c(wbytes, np.uint8)), _p(_c(scales, np.float32)), K, N, _p(xv), M,
+                      _p(y), _p(acc), quant_mode)
+    return y, acc
 
 
 class Lcg:

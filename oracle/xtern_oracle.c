@@ -551,6 +551,60 @@ float or_rms_norm(float* x, const float* w, int64_t n, float eps) {
     return sum;
 }
 
+void or_int_new(int bits, const float* w, int64_t N, int64_t K, uint8_t* out, float* scales) {
+    const float qmax = bits == 8 ? 127.0f : 7.0f;
+    const float lo = bits == 8 ? -127.0f : -8.0f, hi = bits == 8 ? 127.0f : 7.0f;
+    const int64_t bpr = bits == 8 ? K : (K + 1) / 2;
+    for (int64_t o = 0; o < N; ++o) {
+        const float* row = w + o * K;
+        float mx = 0.0f; /* row.iter().map(abs).fold(0.0, f32::max) */
+        for (int64_t k = 0; k < K; ++k) mx = fmaxf(mx, fabsf(row[k]));
+        const float scale = mx > 0.0f ? mx / qmax : 1.0f;
+        scales[o] = scale;
+        for (int64_t c = 0; c < bpr; ++c) {
+            int q[2];
+            const int per = bits == 8 ? 1 : 2;
+            for (int t = 0; t < per; ++t) {
+                const int64_t k = c * per + t;
+                const float v = k < K ? row[k] : 0.0f;
+                float r = roundf(v / scale);
+                r = fmaxf(r, lo); /* Rust max: NaN -> lo */
+                r = fminf(r, hi);
+                q[t] = (int)r;
+            }
+            out[o * bpr + c] = bits == 8 ? (uint8_t)(int8_t)q[0]
+                                         : (uint8_t)(((unsigned)q[0] & 15u) | ((unsigned)q[1] << 4));
+        }
+    }
+}
+
+void or_int_forward(int bits, const uint8_t* wbytes, const float* scales, int64_t K, int64_t N,
+                    const float* x, int64_t M, float* y, int32_t* acc, int quant_mode) {
+    int8_t* q = (int8_t*)malloc((size_t)K);
+    const int64_t bpr = bits == 8 ? K : (K + 1) / 2;
+    for (int64_t m = 0; m < M; ++m) {
+        const float inv = quant_mode == 1 ? or_quantize_scalar(x + m * K, K, q)
+                                          : or_quantize_avx512(x + m * K, K, q);
+        for (int64_t o = 0; o < N; ++o) {
+            const uint8_t* wr = wbytes + o * bpr;
+            int32_t dot = 0;
+            if (bits == 8) {
+                for (int64_t k = 0; k < K; ++k) dot += (int32_t)q[k] * (int32_t)(int8_t)wr[k];
+            } else {
+                for (int64_t c = 0; c < K / 2; ++c) { /* zip with chunks_exact(2) */
+                    const int q0 = (int8_t)(uint8_t)(wr[c] << 4) >> 4;
+                    const int q1 = (int8_t)(wr[c] & 0xF0) >> 4;
+                    dot += (int32_t)q[2 * c] * q0 + (int32_t)q[2 * c + 1] * q1;
+                }
+            }
+            if (acc) acc[m * N + o] = dot;
+            const float a = (float)dot * inv;
+            y[m * N + o] = a * scales[o];
+        }
+    }
+    free(q);
+}
+
 /* simd.rs:556-565: x = x*6364136223846793005 + 1442695040888963407; x >> 33. */
 uint64_t or_lcg_next(uint64_t* state) {
     *state = *state * 6364136223846793005ull + 1442695040888963407ull;

@@ -106,6 +106,19 @@ void or_act_mul_inplace(float* x, const float* up, int64_t n, int use_silu);
  * x[i] = x[i] * inv * w[i].  In place.  Returns sum. */
 float or_rms_norm(float* x, const float* w, int64_t n, float eps);
 
+/* ---- Int8 / Int4 LM head: src/nn/dynamic_linear.rs:229-535 ----
+ * or_int_new: Int8Linear::new (bits 8, :236-258) / Int4Linear::new (bits 4,
+ * :389-410): per row scale = max|w| / 127 (/ 7), 1.0 for a zero row;
+ * q = round(w / scale) clamped; writes [N][K] i8 or [N][ceil(K/2)] nibbles.
+ * or_int_forward: Int8Linear::forward / Int4Linear::forward (:260-375,
+ * :412-535): per row absmax quantisation (quant_mode as or_linear_forward),
+ * exact i32 dot (Int4: bytes paired with chunks_exact(2) of the activations,
+ * so an odd in_dim's last column is skipped), y = (f32)dot * inv * scale[o].
+ * acc (nullable) receives the dots. */
+void or_int_new(int bits, const float* w, int64_t N, int64_t K, uint8_t* out, float* scales);
+void or_int_forward(int bits, const uint8_t* wbytes, const float* scales, int64_t K, int64_t N,
+                    const float* x, int64_t M, float* y, int32_t* acc, int quant_mode);
+
 /* ---- the reference's deterministic test RNG: simd.rs:556-565 ---- */
 uint64_t or_lcg_next(uint64_t* state);
 

@@ -8,6 +8,7 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <algorithm>
 #include <map>
 #include <mutex>
 #include <string>
@@ -114,10 +115,49 @@ int check_weights(const xt_weights* w) {
 
 // Shared tail of every product entry point: quantised activations (ldq with
 // zero padding up to nch*CH, 16-byte aligned) are ready; launch the product.
+// Int8 / Int4 weights: the GEMV (which sums the activation rows itself) over
+// blocks of at most 16 rows that fit its LDS activation stage.
+int run_product_int(const xt_weights* const* ws, int n, const int8_t* q, int ldq, const float* inv,
+                    int64_t M, float* const* ys, int32_t* acc, hipStream_t s) {
+    const int fmt = ws[0]->fmt;
+    const int nch = (int)ws[0]->nch;
+    int mb = 16;
+    while (mb > 1 && !xt::gemv_fits(fmt, mb, nch, 16, xt::gemv_ncw(16))) mb >>= 1;
+    if (!xt::gemv_fits(fmt, mb, nch, 16, xt::gemv_ncw(16)))
+        return fail(XT_ERR_UNSUPPORTED, "in_dim too large for the Int8/Int4 product");
+    for (int64_t m0 = 0; m0 < M; m0 += mb) {
+        const int mr = (int)std::min<int64_t>(mb, M - m0);
+        xt::MMArgs a;
+        memset(&a, 0, sizeof a);
+        int tiles = 0;
+        for (int p = 0; p < n; ++p) {
+            const int ng = (int)((ws[p]->N + 15) / 16);
+            a.proj[p].tiles = ws[p]->tiles;
+            a.proj[p].ws = ws[p]->ws;
+            a.proj[p].y = ys[p] + m0 * ws[p]->N;
+            a.proj[p].acc = (n == 1 && acc) ? acc + m0 * ws[p]->N : nullptr;
+            a.proj[p].N = (int)ws[p]->N;
+            a.proj[p].tile0 = tiles;
+            tiles += ng;
+        }
+        a.nproj = n;
+        a.q = q + m0 * ldq;
+        a.inv = inv + m0;
+        a.M = mr;
+        a.ldq = ldq;
+        a.nch = nch;
+        a.cps = nch;
+        hipError_t e = xt::launch_gemv(fmt, a, tiles, 16, s);
+        if (e != hipSuccess) return hip_fail(e, "Int8/Int4 GEMV launch");
+    }
+    return XT_OK;
+}
+
 int run_product(const xt_weights* const* ws, int n, const int8_t* q, int ldq, const float* inv,
                 const int32_t* rowsum, int64_t M, float* const* ys, int32_t* acc,
                 hipStream_t s) {
     const int fmt = ws[0]->fmt;
+    if (xt::is_int_format(fmt)) return run_product_int(ws, n, q, ldq, inv, M, ys, acc, s);
     int ng_total = 0;
     for (int p = 0; p < n; ++p) ng_total += (int)((ws[p]->N + 15) / 16);
     const xt::MMConfig cfg =
@@ -206,7 +246,7 @@ int linear_q(const xt_weights* const* ws, int n, const int8_t* q, const float* i
     const int64_t K = ws[0]->K;
     const int64_t kpad = ws[0]->nch * xt::chunk_cols(ws[0]->fmt);
     const xt::MMConfig probe = xt::choose_config(ws[0]->fmt, (int)M, 0, 0, true);
-    const bool need_rowsum = probe.kind == 1;
+    const bool need_rowsum = probe.kind == 1 && !xt::is_int_format(ws[0]->fmt);
     const bool direct = (kpad == K) && ((((uintptr_t)q) & 15) == 0);
     if (direct && user_rowsum)
         return run_product(ws, n, q, (int)K, inv, user_rowsum, M, ys, acc, s);
@@ -267,6 +307,8 @@ int mlp_run(const xt_weights* gate, const xt_weights* up, const xt_weights* down
     if (check_weights(gate) || check_weights(up) || check_weights(down)) return XT_ERR_INVALID;
     if (gate->K != up->K || gate->N != up->N || gate->fmt != up->fmt)
         return fail(XT_ERR_INVALID, "gate and up projections must have the same shape and format");
+    if (xt::is_int_format(gate->fmt))
+        return fail(XT_ERR_UNSUPPORTED, "gate/up projections must be ternary");
     if (down->K != gate->N)
         return fail(XT_ERR_INVALID, "down in_dim " + std::to_string(down->K) +
                                         " != intermediate size " + std::to_string(gate->N));
@@ -327,7 +369,7 @@ const char* xt_version(void) { return "xtern 0.1 gfx950"; }
 const char* xt_last_error(void) { return g_err.c_str(); }
 
 size_t xt_tile_bytes(int fmt, int64_t in_dim, int64_t out_dim) {
-    if (in_dim <= 0 || out_dim <= 0 || fmt < 0 || fmt > 2) return 0;
+    if (in_dim <= 0 || out_dim <= 0 || fmt < 0 || fmt > 4) return 0;
     return xt::tile_bytes(fmt, in_dim, out_dim);
 }
 
@@ -374,7 +416,7 @@ int xt_weights_create(int fmt, int64_t in_dim, int64_t out_dim, const void* host
     if (!out) return fail(XT_ERR_INVALID, "out is NULL");
     *out = nullptr;
     if (!host_bytes || !w_scales) return fail(XT_ERR_INVALID, "NULL weight bytes or w_scales");
-    if (fmt < 0 || fmt > 2) return fail(XT_ERR_INVALID, "unknown weight format");
+    if (fmt < 0 || fmt > 4) return fail(XT_ERR_INVALID, "unknown weight format");
     if (in_dim <= 0 || out_dim <= 0) return fail(XT_ERR_INVALID, "in_dim and out_dim must be positive");
     const size_t tb = xt::tile_bytes(fmt, in_dim, out_dim);
     std::vector<uint8_t> host;
@@ -599,13 +641,26 @@ int xt_ternary_mlp_q(const xt_weights* gate, const xt_weights* up, const xt_weig
 int xt_ternary_mlp_f32(const xt_weights* gate, const xt_weights* up, const xt_weights* down,
                        const float* norm_weight, float eps, int use_silu, const float* x,
                        int64_t M, float* y, int mode, void* stream) {
+    // mlp.rs:51-100: one token with ternary gate/up and a ternary or Int8
+    // down takes the fused path (silu_inplace); everything else the unfused
+    // one (silu_mul_inplace).
     int act = XT_ACT_RELU2_MUL;
+    const bool fused = M == 1 && down && (down->fmt != XT_INT4);
     if (use_silu)
-        act = M == 1 ? (mode == XT_QUANT_SCALAR ? XT_ACT_SILU_INPLACE_SCALAR
-                                                : XT_ACT_SILU_INPLACE_AVX512)
-                     : XT_ACT_SILU_MUL;
+        act = fused ? (mode == XT_QUANT_SCALAR ? XT_ACT_SILU_INPLACE_SCALAR
+                                               : XT_ACT_SILU_INPLACE_AVX512)
+                    : XT_ACT_SILU_MUL;
     return mlp_run(gate, up, down, norm_weight, eps, act, mode, M, y,
                    static_cast<hipStream_t>(stream), x, true, nullptr);
+}
+
+int xt_int_quantize_host(int bits, const float* w, int64_t out_dim, int64_t in_dim, void* out,
+                         float* scales) {
+    if (bits != 8 && bits != 4) return fail(XT_ERR_INVALID, "bits must be 8 or 4");
+    if (out_dim <= 0 || in_dim <= 0) return fail(XT_ERR_INVALID, "in_dim and out_dim must be positive");
+    if (!w || !out || !scales) return fail(XT_ERR_INVALID, "NULL buffer");
+    xt::int_quantize(bits, w, out_dim, in_dim, static_cast<uint8_t*>(out), scales);
+    return XT_OK;
 }
 
 }  // extern "C"

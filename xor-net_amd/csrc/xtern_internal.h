@@ -21,8 +21,16 @@ namespace xt {
 // Codes are the weight plus one (0 = -1, 1 = 0, 2 = +1); padding holds code
 // 1.  The kernels multiply codes, not weights, and subtract the activation
 // row sum once at the end: sum_k a*(w+1) - sum_k a = sum_k a*w, exactly.
+//   Int8 / Int4 weights (formats 3 / 4, the reference's Int8Linear /
+//     Int4Linear): CH = 256 columns, 4 k-steps, in 4 (Int8) or 2 (Int4)
+//     consecutive 1 KiB tiles per chunk.  Int8 tile w holds k-step w as the
+//     signed weights themselves; Int4 tile w holds k-steps 2w (low nibbles)
+//     and 2w+1 (high nibbles) as codes q + 8 in [0, 15].
 constexpr int kTileBytes = 1024;
 inline int chunk_cols(int fmt) { return fmt == 1 ? 320 : 256; }
+// 1 KiB tiles per 16-row chunk.
+inline int tiles_per_chunk(int fmt) { return fmt == 3 ? 4 : (fmt == 4 ? 2 : 1); }
+inline bool is_int_format(int fmt) { return fmt == 3 || fmt == 4; }
 
 // Up to four projections that share one input, in one launch.
 struct Proj {
@@ -70,6 +78,8 @@ int gemm_ncmax(int fmt);
 hipError_t launch_gemm(int fmt, const MMArgs& a, int ntiles, int splitk, hipStream_t s);
 // Decode GEMV (M <= 16): 16 output rows per workgroup, activations in LDS.
 hipError_t launch_gemv(int fmt, const MMArgs& a, int ntiles, int waves, hipStream_t s);
+int gemv_ncw(int waves);
+bool gemv_fits(int fmt, int M, int nch, int waves, int ncw);
 // MLP middle stage (xtern_kernels.hip): per row of gate/up, activation,
 // optional RMSNorm, optional f32 output, optional requantisation.
 struct MidArgs {

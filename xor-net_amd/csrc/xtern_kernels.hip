@@ -505,6 +505,10 @@ template <int FMT, int WAVES, int NCW>
 __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const MMArgs a) {
     constexpr int STEPS = (FMT == XT_PACK5) ? 5 : 4;
     constexpr int CH = STEPS * 64;
+    // 1 KiB tiles per chunk, and the weight code offset the activation row
+    // sum removes: ternary codes are w + 1, Int4 codes q + 8, Int8 none.
+    constexpr int TPC = (FMT == XT_INT8) ? 4 : (FMT == XT_INT4 ? 2 : 1);
+    constexpr int OFF = (FMT == XT_INT8) ? 0 : (FMT == XT_INT4 ? 8 : 1);
     constexpr int SEGS = CH / 16;
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ v4i red[WAVES][64];
@@ -539,11 +543,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const MMArgs a) {
     if (threadIdx.x < 16) rsum[threadIdx.x] = 0;
 
     // weights first: they come from HBM and take longest
-    v4i wv[NCW];
+    v4i wv[NCW][TPC];
 #pragma unroll
     for (int t = 0; t < NCW; ++t) {
         const int c = wave + t * WAVES;
-        wv[t] = c < nch ? ld_stream(tiles + ((size_t)(G * nch + c) * 64 + lane) * 16) : v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int u = 0; u < TPC; ++u)
+            wv[t][u] = c < nch ? ld_stream(tiles + (((size_t)(G * nch + c) * TPC + u) * 64 + lane) * 16)
+                               : v4i{0, 0, 0, 0};
     }
     // epilogue operands, so no memory round trip is left after the MFMAs
     const int o = G * 16 + j;
@@ -581,8 +588,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const MMArgs a) {
                 int E[4], O[4];
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
-                    E[d] = wv[t][d] & 0x00ff00ff;
-                    O[d] = ((unsigned)wv[t][d] >> 8) & 0x00ff00ff;
+                    E[d] = wv[t][0][d] & 0x00ff00ff;
+                    O[d] = ((unsigned)wv[t][0][d] >> 8) & 0x00ff00ff;
                 }
 #pragma unroll
                 for (int s = 0; s < STEPS; ++s) {
@@ -605,7 +612,17 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const MMArgs a) {
                     v4i av = v4i{0, 0, 0, 0};
                     if (j < M)
                         av = *reinterpret_cast<const v4i*>(lds + ((((c * STEPS + s) * 4 + g) * M + j) << 4));
-                    acc[s] = mfma(av, decode4(wv[t][s]), acc[s]);
+                    v4i b;
+                    if constexpr (FMT == XT_INT8) {
+                        b = wv[t][s];
+                    } else if constexpr (FMT == XT_INT4) {
+#pragma unroll
+                        for (int d = 0; d < 4; ++d)  // tiles hold the codes q + 8
+                            b[d] = (int)(((unsigned)wv[t][s >> 1][d] >> (4 * (s & 1))) & 0x0f0f0f0fu);
+                    } else {
+                        b = decode4(wv[t][0][s]);
+                    }
+                    acc[s] = mfma(av, b, acc[s]);
                 }
             }
         }
@@ -624,7 +641,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const MMArgs a) {
     for (int r = 0; r < 4; ++r) {
         const int i = 4 * g + r;
         if (i >= M) continue;
-        const int d = sum[r] - rsum[i];
+        const int d = sum[r] - OFF * rsum[i];
         // layers.rs:294 — (dot as f32 * inv_scale) * w_scale, two roundings.
         y[(size_t)i * N + o] = __fmul_rn(__fmul_rn((float)d, invr[r]), wscale);
         if (accout) accout[(size_t)i * N + o] = d;
@@ -650,6 +667,10 @@ hipError_t launch_gemv(int fmt, const MMArgs& a, int ntiles, int waves, hipStrea
     if (waves == W_) {                                                                           \
         if (fmt == XT_PACK5)                                                                     \
             hipLaunchKernelGGL((gemv_kernel<XT_PACK5, W_, NCW_>), dim3(ntiles), dim3(W_ * 64), lds, s, a); \
+        else if (fmt == XT_INT8)                                                                 \
+            hipLaunchKernelGGL((gemv_kernel<XT_INT8, W_, NCW_>), dim3(ntiles), dim3(W_ * 64), lds, s, a); \
+        else if (fmt == XT_INT4)                                                                 \
+            hipLaunchKernelGGL((gemv_kernel<XT_INT4, W_, NCW_>), dim3(ntiles), dim3(W_ * 64), lds, s, a); \
         else                                                                                     \
             hipLaunchKernelGGL((gemv_kernel<XT_PACK4, W_, NCW_>), dim3(ntiles), dim3(W_ * 64), lds, s, a); \
         return hipGetLastError();                                                                \

@@ -5,6 +5,7 @@
 //   Pack4      src/bit1_58/quantization.rs:7-46   ([N][ceil(K/4)] bytes)
 //   Pack5      src/bit1_58/quantization.rs:48-91  ([N][ceil(K/5)] bytes)
 //   XorSparse  src/bit1_58/sparse.rs:9-17, :135-194 (row blobs)
+#include <math.h>
 #include <string.h>
 
 #include <string>
@@ -18,7 +19,7 @@ size_t tile_bytes(int fmt, int64_t K, int64_t N) {
     const int64_t ch = chunk_cols(fmt);
     const int64_t nch = (K + ch - 1) / ch;
     const int64_t ng = (N + 15) / 16;
-    return (size_t)(ng * nch * kTileBytes);
+    return (size_t)(ng * nch * tiles_per_chunk(fmt) * kTileBytes);
 }
 
 namespace {
@@ -153,7 +154,93 @@ int repack_pack5(int64_t K, int64_t N, const uint8_t* src, size_t nbytes, uint8_
     return 0;
 }
 
+// Int8Linear weight_i8 [N][K] (dynamic_linear.rs:236-258) -> Int8 tiles.
+int repack_int8(int64_t K, int64_t N, const uint8_t* src, size_t nbytes, uint8_t* tiles,
+                std::string* err) {
+    if ((uint64_t)nbytes < (uint64_t)(K * N)) {
+        *err = "Int8 weights: expected " + std::to_string(K * N) + " bytes ([out_dim][in_dim]), got " +
+               std::to_string(nbytes);
+        return -1;
+    }
+    const int64_t nch = (K + 255) / 256;
+    memset(tiles, 0, tile_bytes(3, K, N));
+    for (int64_t o = 0; o < N; ++o) {
+        const int64_t G = o >> 4, j = o & 15;
+        for (int64_t k = 0; k < K; ++k) {
+            const int64_t c = k >> 8, kk = k & 255, s = kk >> 6, g = (kk & 63) >> 4, b = kk & 15;
+            tiles[(((G * nch + c) * 4 + s) * 64 + g * 16 + j) * 16 + b] = src[o * K + k];
+        }
+    }
+    return 0;
+}
+
+// Int4Linear weight_i4 [N][ceil(K/2)] (dynamic_linear.rs:389-410: column 2c
+// in the low nibble, 2c+1 in the high one, two's complement) -> Int4 tiles
+// of codes q + 8.  Int4Linear's dot pairs the bytes with
+// quantized_in.chunks_exact(2) (:442-449), so for odd K the last column never
+// contributes: it is stored as q = 0.
+int repack_int4(int64_t K, int64_t N, const uint8_t* src, size_t nbytes, uint8_t* tiles,
+                std::string* err) {
+    const int64_t bpr = (K + 1) / 2;
+    if ((uint64_t)nbytes < (uint64_t)(bpr * N)) {
+        *err = "Int4 weights: expected " + std::to_string(bpr * N) +
+               " bytes ([out_dim][ceil(in_dim/2)]), got " + std::to_string(nbytes);
+        return -1;
+    }
+    const int64_t nch = (K + 255) / 256;
+    memset(tiles, 0x88, tile_bytes(4, K, N));  // code 8 = weight 0 everywhere
+    const int64_t kuse = K & ~(int64_t)1;       // columns the reference's dot reads
+    for (int64_t o = 0; o < N; ++o) {
+        const int64_t G = o >> 4, j = o & 15;
+        for (int64_t k = 0; k < kuse; ++k) {
+            const unsigned byte = src[o * bpr + (k >> 1)];
+            const unsigned nib = (k & 1) ? (byte >> 4) : (byte & 15u);
+            const unsigned code = nib ^ 8u;  // q + 8 for the two's-complement nibble q
+            const int64_t c = k >> 8, kk = k & 255, s = kk >> 6, g = (kk & 63) >> 4, b = kk & 15;
+            uint8_t* p = tiles + (((G * nch + c) * 2 + (s >> 1)) * 64 + g * 16 + j) * 16 + b;
+            const int sh = (s & 1) ? 4 : 0;
+            *p = (uint8_t)((*p & ~(15u << sh)) | (code << sh));
+        }
+    }
+    return 0;
+}
+
 }  // namespace
+
+// Int8Linear::new / Int4Linear::new (dynamic_linear.rs:236-258, :389-410).
+int int_quantize(int bits, const float* w, int64_t N, int64_t K, uint8_t* out, float* scales) {
+    const float qmax = bits == 8 ? 127.0f : 7.0f;
+    const int64_t bpr = bits == 8 ? K : (K + 1) / 2;
+    for (int64_t o = 0; o < N; ++o) {
+        const float* row = w + o * K;
+        float mx = 0.0f;
+        for (int64_t k = 0; k < K; ++k) {
+            const float a = fabsf(row[k]);
+            mx = (a > mx) ? a : mx;  // f32::max fold: NaN never replaces the max
+        }
+        const float scale = mx > 0.0f ? mx / qmax : 1.0f;
+        scales[o] = scale;
+        auto q_of = [&](float v) {
+            // (v / scale).round().max(lo).min(hi) as i8; NaN -> lo
+            float r = roundf(v / scale);
+            const float lo = bits == 8 ? -127.0f : -8.0f, hi = bits == 8 ? 127.0f : 7.0f;
+            r = (r != r) ? lo : (r < lo ? lo : r);
+            r = r > hi ? hi : r;
+            return (int)r;
+        };
+        uint8_t* dst = out + o * bpr;
+        if (bits == 8) {
+            for (int64_t k = 0; k < K; ++k) dst[k] = (uint8_t)(int8_t)q_of(row[k]);
+        } else {
+            for (int64_t c = 0; c < bpr; ++c) {
+                const int q0 = q_of(row[2 * c]);
+                const int q1 = 2 * c + 1 < K ? q_of(row[2 * c + 1]) : q_of(0.0f);
+                dst[c] = (uint8_t)(((unsigned)q0 & 15u) | ((unsigned)q1 << 4));
+            }
+        }
+    }
+    return 0;
+}
 
 // loader/mod.rs:351-390 without the f32 round trip: the value of (row o,
 // column i) is digit j of stored byte [p][i] with o = j*R + p, R = N/f; it
@@ -206,10 +293,14 @@ int repack(int fmt, int64_t K, int64_t N, const void* src, size_t nbytes, void* 
         *err = "in_dim/out_dim above 2^30 are not supported";
         return -1;
     }
-    if (fmt != 0 && fmt != 1 && fmt != 2) {
+    if (fmt < 0 || fmt > 4) {
         *err = "unknown weight format " + std::to_string(fmt);
         return -1;
     }
+    if (fmt == 3) return repack_int8(K, N, static_cast<const uint8_t*>(src), nbytes,
+                                     static_cast<uint8_t*>(dst), err);
+    if (fmt == 4) return repack_int4(K, N, static_cast<const uint8_t*>(src), nbytes,
+                                     static_cast<uint8_t*>(dst), err);
     const size_t tb = tile_bytes(fmt, K, N);
     uint8_t* tiles = static_cast<uint8_t*>(dst);
     if (fmt == 1) return repack_pack5(K, N, static_cast<const uint8_t*>(src), nbytes, tiles, err);

@@ -16,4 +16,7 @@ int repack(int fmt, int64_t K, int64_t N, const void* src, size_t nbytes, void* 
 // [N][ceil(K/f)], f = 4 (fmt 0) or 5 (fmt 1).  Returns 0, or -1 with *err set.
 int hf_destripe(int fmt, int64_t K, int64_t N, const uint8_t* stored, size_t nbytes,
                 uint8_t* out, std::string* err);
+// Int8Linear::new (bits 8: out [N][K] i8) / Int4Linear::new (bits 4: out
+// [N][ceil(K/2)] nibbles) with per-row scales.
+int int_quantize(int bits, const float* w, int64_t N, int64_t K, uint8_t* out, float* scales);
 }  // namespace xt

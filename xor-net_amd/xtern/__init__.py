@@ -41,6 +41,9 @@ except ImportError:  # the C ABI itself does not need torch
 
 _lib = ctypes.CDLL(LIB_PATH)
 
+XT_INT8 = 3
+XT_INT4 = 4
+
 XT_ACT_RELU2_MUL = 0
 XT_ACT_SILU_INPLACE_AVX512 = 1
 XT_ACT_SILU_INPLACE_SCALAR = 2
@@ -93,6 +96,7 @@ _lib.xt_sparse_file_serialized_size.restype = _sz
 _lib.xt_sparse_file_serialize.argtypes = [_i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz]
 _lib.xt_hf_to_sparse_blob.argtypes = [ctypes.c_int, _i64, _i64, _vp, _sz, ctypes.c_int, _vp, _sz,
                                       ctypes.POINTER(_sz)]
+_lib.xt_int_quantize_host.argtypes = [ctypes.c_int, _vp, _i64, _i64, _vp, _vp]
 _lib.xt_quantize_i8.argtypes = [_vp, _i64, _i64, _vp, _vp, ctypes.c_int, _vp]
 _lib.xt_quantize_i8_rowsum.argtypes = [_vp, _i64, _i64, _vp, _vp, _vp, ctypes.c_int, _vp]
 _lib.xt_ternary_linear_q.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp, _vp]
@@ -328,6 +332,18 @@ def repack_host(fmt, in_dim, out_dim, host_bytes):
     _check(_lib.xt_repack_host(fmt, in_dim, out_dim, src.ctypes.data_as(_vp), src.size,
                                out.ctypes.data_as(_vp)))
     return out
+
+
+def int_quantize_host(bits, weights_f32, out_dim, in_dim):
+    """xt_int_quantize_host: Int8Linear::new / Int4Linear::new -> (bytes, scales)."""
+    w = np.ascontiguousarray(np.asarray(weights_f32, dtype=np.float32).ravel())
+    if w.size != out_dim * in_dim:
+        raise XternError(XT_ERR_INVALID, "Weight length must match in_dim * out_dim")
+    out = np.zeros(out_dim * (in_dim if bits == 8 else (in_dim + 1) // 2), np.uint8)
+    sc = np.zeros(out_dim, np.float32)
+    _check(_lib.xt_int_quantize_host(bits, w.ctypes.data_as(_vp), out_dim, in_dim,
+                                     out.ctypes.data_as(_vp), sc.ctypes.data_as(_vp)))
+    return out, sc
 
 
 def hf_destripe(fmt, in_dim, out_dim, stored):
@@ -663,4 +679,5 @@ def linear_multi_q(ws, q, inv, stream=None):
     return ys
 
 
-from .layers import TernaryLinear, DynamicLinear, TernaryRep, FastRmsNorm, Mlp  # noqa: E402,F401
+from .layers import (TernaryLinear, DynamicLinear, TernaryRep, FastRmsNorm, Mlp,  # noqa: E402,F401
+                     Int8Linear, Int4Linear)

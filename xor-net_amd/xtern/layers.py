@@ -11,7 +11,7 @@ import numpy as np
 
 from . import (XT_ERR_INVALID, XT_PACK4, XT_PACK5, XT_QUANT_AVX512, XT_XORSPARSE,
                DeviceWeights, TernaryPackType, XternError, _ternarise, encode_sparse_tensor,
-               hf_destripe, mlp_f32, mlp_q, rms_norm,
+               hf_destripe, mlp_f32, mlp_q, rms_norm, XT_INT8, XT_INT4, int_quantize_host,
                linear_f32, linear_multi_q, linear_q, pack_ternary4, pack_ternary5,
                unpack_1_58bit_4pack, unpack_1_58bit_5pack)
 
@@ -234,6 +234,57 @@ class TernaryLinear:
         return y.reshape(tuple(xs.shape[:-1]) + (down_lin.out_dim,))
 
 
+class _IntLinear:
+    """Int8Linear / Int4Linear (dynamic_linear.rs:229-535): per-row scaled
+    integer weights; forward quantises each activation row (absmax i8) and
+    computes (f32)dot * inv_scale * scales[o] on the GPU."""
+
+    BITS = 8
+    NAME = "Int8Linear"
+
+    def __init__(self, weight_bytes, scales, in_dim, out_dim):
+        self.in_dim, self.out_dim = int(in_dim), int(out_dim)
+        self.weight_bytes = np.asarray(weight_bytes, np.uint8)
+        self.scales = np.asarray(scales, np.float32)
+        fmt = XT_INT8 if self.BITS == 8 else XT_INT4
+        self.weights = DeviceWeights(fmt, self.in_dim, self.out_dim, self.weight_bytes, self.scales)
+
+    @classmethod
+    def new(cls, weights_f32, out_dim, in_dim):
+        b, sc = int_quantize_host(cls.BITS, weights_f32, out_dim, in_dim)
+        return cls(b, sc, in_dim, out_dim)
+
+    def _check(self, xs):
+        if xs.dim() == 0:
+            raise XternError(XT_ERR_INVALID, "Input must have at least 1 dimension")
+        if xs.shape[-1] != self.in_dim:
+            raise XternError(XT_ERR_INVALID, f"{self.NAME} shape mismatch")
+        return tuple(xs.shape[:-1]) + (self.out_dim,)
+
+    def forward(self, xs, mode=XT_QUANT_AVX512):
+        shape = self._check(xs)
+        return linear_f32(self.weights, xs.contiguous(), mode=mode).reshape(shape)
+
+    def forward_with_quantized(self, xs, quantized_in, inv_scale):
+        import torch
+        shape = self._check(xs)
+        q = quantized_in.reshape(-1, self.in_dim).contiguous()
+        if not torch.is_tensor(inv_scale):
+            inv_scale = torch.full((q.shape[0],), float(inv_scale), dtype=torch.float32,
+                                   device=q.device)
+        return linear_q(self.weights, q, inv_scale.contiguous()).reshape(shape)
+
+
+class Int8Linear(_IntLinear):
+    BITS = 8
+    NAME = "Int8Linear"
+
+
+class Int4Linear(_IntLinear):
+    BITS = 4
+    NAME = "Int4Linear"
+
+
 class FastRmsNorm:
     """nn::FastRmsNorm: weight [n] (device f32 tensor) and eps; forward is
     rms_norm on each row (tensor.rs:242-265)."""
@@ -288,6 +339,16 @@ class DynamicLinear:
     def new_ternary_direct(cls, packed, in_dim, out_dim, pack_type, w_scales):
         return cls(TernaryLinear.new_direct(packed, in_dim, out_dim, pack_type, w_scales))
 
+    @classmethod
+    def new_int8(cls, weights_f32, out_dim, in_dim):
+        """dynamic_linear.rs:655-659"""
+        return cls(Int8Linear.new(weights_f32, out_dim, in_dim))
+
+    @classmethod
+    def new_int4(cls, weights_f32, out_dim, in_dim):
+        """dynamic_linear.rs:661-665"""
+        return cls(Int4Linear.new(weights_f32, out_dim, in_dim))
+
     def forward(self, xs):
         return self.inner.forward(xs)
 
@@ -295,5 +356,6 @@ class DynamicLinear:
         return self.inner.forward_with_quantized(xs, quantized_in, inv_scale)
 
 
-__all__ = ["TernaryLinear", "DynamicLinear", "TernaryRep", "FastRmsNorm", "Mlp", "TernaryPackType", "XT_PACK4",
+__all__ = ["TernaryLinear", "DynamicLinear", "TernaryRep", "FastRmsNorm", "Mlp", "Int8Linear",
+           "Int4Linear", "TernaryPackType", "XT_PACK4",
            "XT_PACK5"]
