@@ -125,6 +125,7 @@ int run_product_int(const xt_weights* const* ws, int n, const int8_t* q, int ldq
     while (mb > 1 && !xt::gemv_fits(fmt, mb, nch, 16, xt::gemv_ncw(16))) mb >>= 1;
     if (!xt::gemv_fits(fmt, mb, nch, 16, xt::gemv_ncw(16)))
         return fail(XT_ERR_UNSUPPORTED, "in_dim too large for the Int8/Int4 product");
+    const int waves = xt::int_gemv_waves(fmt, mb, nch);
     for (int64_t m0 = 0; m0 < M; m0 += mb) {
         const int mr = (int)std::min<int64_t>(mb, M - m0);
         xt::MMArgs a;
@@ -147,7 +148,7 @@ int run_product_int(const xt_weights* const* ws, int n, const int8_t* q, int ldq
         a.ldq = ldq;
         a.nch = nch;
         a.cps = nch;
-        hipError_t e = xt::launch_gemv(fmt, a, tiles, 16, s);
+        hipError_t e = xt::launch_gemv(fmt, a, tiles, waves, s);
         if (e != hipSuccess) return hip_fail(e, "Int8/Int4 GEMV launch");
     }
     return XT_OK;

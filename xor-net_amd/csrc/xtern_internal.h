@@ -79,6 +79,7 @@ hipError_t launch_gemm(int fmt, const MMArgs& a, int ntiles, int splitk, hipStre
 // Decode GEMV (M <= 16): 16 output rows per workgroup, activations in LDS.
 hipError_t launch_gemv(int fmt, const MMArgs& a, int ntiles, int waves, hipStream_t s);
 int gemv_ncw(int waves);
+int int_gemv_waves(int fmt, int mb, int nch);
 bool gemv_fits(int fmt, int M, int nch, int waves, int ncw);
 // MLP middle stage (xtern_kernels.hip): per row of gate/up, activation,
 // optional RMSNorm, optional f32 output, optional requantisation.

@@ -1023,6 +1023,16 @@ bool env_config(MMConfig* c) {
 //            slice, else 16 tokens x 64 rows with 4 waves splitting K.
 // Split-K across workgroups (gridDim.z > 1) is only taken when forced: its
 // device-scope release/acquire costs more than it saves at these sizes.
+// Waves per workgroup of the Int8 / Int4 GEMV for row blocks of mb tokens.
+int int_gemv_waves(int fmt, int mb, int nch) {
+    MMConfig c;
+    if (env_config(&c) && c.kind == 2 && gemv_fits(fmt, mb, nch, c.waves, gemv_ncw(c.waves)))
+        return c.waves;
+    // Measured on the 128256 x 2560 LM head: Int4 streams fastest with 8
+    // waves (46.5 vs 58 us at M = 1), Int8 with 16.
+    return (fmt == XT_INT4 && gemv_fits(fmt, mb, nch, 8, gemv_ncw(8))) ? 8 : 16;
+}
+
 MMConfig choose_config(int fmt, int M, int ntiles_nb1, int nch, bool have_rowsum) {
     MMConfig c;
     if (env_config(&c)) {
