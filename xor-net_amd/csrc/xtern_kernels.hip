@@ -54,17 +54,24 @@ __device__ __forceinline__ int quant_one(float x, float scale, int mode, bool ma
     return (int)r;
 }
 
-template <typename T, typename Op>
-__device__ __forceinline__ T block_reduce(T v, Op op, T* smem) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = op(v, __shfl_xor(v, off, 64));
-    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
-    if ((threadIdx.x & 63) == 0) smem[wave] = v;
-    __syncthreads();
-    T r = smem[0];
-    for (int w = 1; w < nw; ++w) r = op(r, smem[w]);
-    __syncthreads();
-    return r;
+// Wave reductions over DPP (gfx9 row_shr within rows of 16, then
+// row_bcast:15 / row_bcast:31 into the following rows; lane 63 ends with the
+// full result, which readlane broadcasts).  Lanes without a source read the
+// identity (`old` = 0: the sum identity, and the max identity for the
+// non-negative values the quantisers reduce).
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ int dpp_id(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, CTRL, ROW_MASK, 0xf, false);
+}
+template <typename Op>
+__device__ __forceinline__ int wave_reduce_bits(int v, Op op) {
+    v = op(v, dpp_id<0x111, 0xf>(v));
+    v = op(v, dpp_id<0x112, 0xf>(v));
+    v = op(v, dpp_id<0x114, 0xf>(v));
+    v = op(v, dpp_id<0x118, 0xf>(v));
+    v = op(v, dpp_id<0x142, 0xa>(v));
+    v = op(v, dpp_id<0x143, 0xc>(v));
+    return __builtin_amdgcn_readlane(v, 63);
 }
 
 struct MaxOp {
@@ -76,6 +83,29 @@ struct OrOp {
 struct AddOp {
     __device__ int operator()(int a, int b) const { return a + b; }
 };
+
+// Workgroup reduction: DPP inside each wave, then the per-wave values
+// through LDS.  MaxOp is only used on non-negative values (absmax).
+template <typename T, typename Op>
+__device__ __forceinline__ T block_reduce(T v, Op op, T* smem) {
+    int bits;
+    if constexpr (sizeof(T) == 4 && __is_same(T, float)) {
+        bits = wave_reduce_bits(__float_as_int(v), [op](int x, int y) {
+            return __float_as_int(op(__int_as_float(x), __int_as_float(y)));
+        });
+        v = __int_as_float(bits);
+    } else {
+        v = (T)wave_reduce_bits((int)v, [op](int x, int y) { return (int)op((T)x, (T)y); });
+    }
+    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    if ((threadIdx.x & 63) == 0) smem[wave] = v;
+    __syncthreads();
+    T r = smem[0];
+    for (int w = 1; w < nw; ++w) r = op(r, smem[w]);
+    __syncthreads();
+    return r;
+}
+
 
 // One workgroup per row.  Pass 1: absmax (fmaxf ignores NaN; NaN inputs are
 // off-contract).  Pass 2: quantise, write i8 (zero-filling [K, ldq)), and the
@@ -136,16 +166,17 @@ __global__ __launch_bounds__(256) void quantize_kernel(const float* __restrict__
     }
 }
 
-// Single-pass variant for K <= 1024 * NV with 16-byte aligned rows: each
+// Single-pass variant for K <= 4 * NT * NV with 16-byte aligned rows: each
 // thread keeps its NV float4 of the row in registers between the absmax
 // reduction and the quantisation, so the row is read from memory once.
-template <int NV>
-__global__ __launch_bounds__(256) void quantize_reg_kernel(const float* __restrict__ x, int64_t ldx,
-                                                           int K, int8_t* __restrict__ q, int ldq,
-                                                           float* __restrict__ inv,
-                                                           int32_t* __restrict__ rowsum, int mode) {
-    __shared__ float sm_f[4];
-    __shared__ int sm_i[4];
+// NT = 1024 for long rows (more loads in flight per row).
+template <int NV, int NT>
+__global__ __launch_bounds__(NT) void quantize_reg_kernel(const float* __restrict__ x, int64_t ldx,
+                                                          int K, int8_t* __restrict__ q, int ldq,
+                                                          float* __restrict__ inv,
+                                                          int32_t* __restrict__ rowsum, int mode) {
+    __shared__ float sm_f[NT / 64];
+    __shared__ int sm_i[NT / 64];
     const int m = blockIdx.x;
     const float4* x4 = reinterpret_cast<const float4*>(x + (size_t)m * ldx);
     uint32_t* q4 = reinterpret_cast<uint32_t*>(q + (size_t)m * ldq);
@@ -154,7 +185,7 @@ __global__ __launch_bounds__(256) void quantize_reg_kernel(const float* __restri
     float mx = 0.0f;
 #pragma unroll
     for (int u = 0; u < NV; ++u) {
-        const int i = threadIdx.x + u * 256;
+        const int i = threadIdx.x + u * NT;
         v[u] = i < K4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
         mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
     }
@@ -165,7 +196,7 @@ __global__ __launch_bounds__(256) void quantize_reg_kernel(const float* __restri
     int sum = 0;
 #pragma unroll
     for (int u = 0; u < NV; ++u) {
-        const int i = threadIdx.x + u * 256;
+        const int i = threadIdx.x + u * NT;
         if (i >= K4) continue;
         const float e[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
         int b[4];
@@ -175,7 +206,7 @@ __global__ __launch_bounds__(256) void quantize_reg_kernel(const float* __restri
         q4[i] = (uint32_t)(b[0] & 255) | ((uint32_t)(b[1] & 255) << 8) |
                 ((uint32_t)(b[2] & 255) << 16) | ((uint32_t)(b[3] & 255) << 24);
     }
-    for (int i = K4 + threadIdx.x; i < (ldq >> 2); i += 256) q4[i] = 0u;  // padding
+    for (int i = K4 + threadIdx.x; i < (ldq >> 2); i += NT) q4[i] = 0u;  // padding
     sum = block_reduce(sum, AddOp(), sm_i);
     if (threadIdx.x == 0) {
         inv[m] = invs;
@@ -208,17 +239,17 @@ hipError_t launch_quantize(const float* x, int64_t ldx, int M, int K, int8_t* q,
     const bool aligned = (K % 4 == 0) && (ldx % 4 == 0) && (ldq % 4 == 0) &&
                          ((uintptr_t)x % 16 == 0) && ((uintptr_t)q % 4 == 0);
     if (aligned && K <= 16384) {
-#define XT_QREG(NV_)                                                                            \
-    if (K <= 1024 * NV_) {                                                                      \
-        hipLaunchKernelGGL(quantize_reg_kernel<NV_>, dim3(M), dim3(256), 0, s, x, ldx, K, q, ldq, \
-                           inv, rowsum, mode);                                                  \
-        return hipGetLastError();                                                               \
+#define XT_QREG(NV_, NT_)                                                                        \
+    if (K <= 4 * NT_ * NV_) {                                                                    \
+        hipLaunchKernelGGL((quantize_reg_kernel<NV_, NT_>), dim3(M), dim3(NT_), 0, s, x, ldx, K, q, \
+                           ldq, inv, rowsum, mode);                                              \
+        return hipGetLastError();                                                                \
     }
-        XT_QREG(1)
-        XT_QREG(2)
-        XT_QREG(4)
-        XT_QREG(8)
-        XT_QREG(16)
+        XT_QREG(1, 256)
+        XT_QREG(2, 256)
+        XT_QREG(1, 1024)
+        XT_QREG(2, 1024)
+        XT_QREG(4, 1024)
 #undef XT_QREG
     }
     hipLaunchKernelGGL(quantize_kernel, dim3(M), dim3(256), 0, s, x, ldx, K, q, ldq, inv, rowsum,
@@ -986,7 +1017,18 @@ hipError_t launch_gemm(int fmt, const MMArgs& a, int ntiles, int splitk, hipStre
     X(2, 4, 4, 2)        \
     X(2, 8, 4, 2)        \
     X(4, 4, 4, 1)        \
-    X(4, 2, 4, 1)
+    X(4, 2, 4, 1)        \
+    X(1, 5, 4, 2)        \
+    X(1, 5, 8, 2)        \
+    X(1, 4, 8, 2)        \
+    X(2, 5, 8, 2)        \
+    X(1, 5, 16, 1)       \
+    X(1, 5, 8, 1)        \
+    X(1, 5, 16, 2)       \
+    X(1, 10, 8, 2)       \
+    X(2, 8, 8, 2)        \
+    X(1, 8, 8, 2)        \
+    X(4, 4, 8, 1)
 
 namespace {
 bool shape_known(const MMConfig& c, bool own) {
@@ -1061,7 +1103,23 @@ MMConfig choose_config(int fmt, int M, int ntiles_nb1, int nch, bool have_rowsum
         (void)ntiles_nb1;
         return c;
     }
-    return MMConfig{1, 4, 4, 2, 1};
+    // Long K (activation slice too big for the GEMM's LDS): 16 tokens per
+    // workgroup, K over 8 waves, and the row-block width that fills the
+    // chip in the fewest rounds of workgroups -- e.g. C1 down (M 128, 160
+    // row groups): 80 rows -> 256 workgroups in one round, 8.6 us, against
+    // 64 rows -> 320 workgroups in two rounds, 12.5 us.
+    const int tb = (M + 15) / 16;
+    int best_nb = 4;
+    long best_cost = -1;
+    for (int nb : {4, 5, 8}) {
+        const long wgs = (long)((ntiles_nb1 + nb - 1) / nb) * tb;
+        const long cost = ((wgs + 255) / 256) * nb;
+        if (best_cost < 0 || cost < best_cost) {
+            best_cost = cost;
+            best_nb = nb;
+        }
+    }
+    return MMConfig{1, best_nb, 8, 2, 1};
 }
 
 hipError_t launch_mm(int fmt, const MMConfig& cfg, const MMArgs& a, int ntiles_total,
