@@ -425,3 +425,33 @@ def test_forced_splitk_configs(cfg, monkeypatch):
         _, acc = xtern.linear_q(w, torch.from_numpy(q).to(DEV), torch.ones(M, device=DEV),
                                 acc=True)
         assert np.array_equal(acc.cpu().numpy(), exact_acc(t, q))
+
+
+@pytest.mark.parametrize("mode", [xtern.XT_QUANT_AVX512, xtern.XT_QUANT_SCALAR])
+@pytest.mark.parametrize("fmt", FMTS)
+@pytest.mark.parametrize("M,K", [(1, 4), (1, 16), (1, 20), (2, 100), (3, 2560), (1, 8192),
+                                 (4, 2048), (1, 2561), (16, 512)])
+def test_small_forward_quantiser_ties(fmt, mode, M, K):
+    """Small M*K forwards quantise inside the GEMV.  Rows whose absmax is 127
+    make the scale exactly 1, so x.5 values are exact ties: half-to-even in
+    the AVX-512 body, half-away in its tail and in scalar mode."""
+    log(f"fused quant fmt={fmt} mode={mode} M={M} K={K}")
+    rng = np.random.default_rng(zlib.crc32(f"fq{fmt}{mode}{M}{K}".encode()))
+    N = 40
+    t = tern(rng, N, K)
+    wb = make_bytes(t, fmt)
+    ws = np.full(N, 0.7, np.float32)
+    w = xtern.DeviceWeights(fmt, K, N, wb, ws)
+    x = (rng.integers(-60, 61, size=(M, K)) + 0.5).astype(np.float32)
+    x[:, 0] = 127.0
+    if M > 1:
+        x[1] *= np.float32(0.37)  # a row without ties
+    y = xtern.linear_f32(w, torch.from_numpy(x).to(DEV), mode=mode).cpu().numpy()
+    q = np.stack([oracle.quantize(x[m], mode)[0] for m in range(M)])
+    inv = np.array([oracle.quantize(x[m], mode)[1] for m in range(M)], np.float32)
+    check_y(y, oracle_q(fmt, t, q, inv, ws)[0])
+    # multi-projection forward on the same input
+    w2 = xtern.DeviceWeights(fmt, K, N, wb, ws * np.float32(2))
+    ys = xtern.linear_multi_f32([w, w2], torch.from_numpy(x).to(DEV), mode=mode)
+    check_y(ys[0].cpu().numpy(), y)
+    check_y(ys[1].cpu().numpy(), oracle_q(fmt, t, q, inv, ws * np.float32(2))[0])

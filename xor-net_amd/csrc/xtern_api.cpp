@@ -6,6 +6,7 @@
 // is a negative status plus xt_last_error() instead of anyhow::bail!.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <algorithm>
@@ -265,12 +266,63 @@ int linear_q(const xt_weights* const* ws, int n, const int8_t* q, const float* i
                        s);
 }
 
+// Small inputs on the GEMV: the kernel quantises the f32 rows itself (no
+// separate quantiser launch).  Returns 1 when the case does not apply.
+int gemv_fused_quant(const xt_weights* const* ws, int n, const float* x, int64_t M,
+                     float* const* ys, int mode, hipStream_t s) {
+    static const bool disabled = getenv("XTERN_NO_FUSED_QUANT") != nullptr;
+    const int fmt = ws[0]->fmt;
+    const int64_t K = ws[0]->K;
+    const int nch = (int)ws[0]->nch;
+    if (disabled || M > 16 || M * K > xt::kGemvFusedQuantMax || (((uintptr_t)x) & 15) ||
+        (K & 3))
+        return 1;
+    int ng_total = 0;
+    for (int p = 0; p < n; ++p) ng_total += (int)((ws[p]->N + 15) / 16);
+    int waves = 0;
+    if (xt::is_int_format(fmt)) {
+        waves = xt::int_gemv_waves(fmt, (int)M, nch);
+    } else {
+        const xt::MMConfig cfg = xt::choose_config(fmt, (int)M, ng_total, nch, false);
+        if (cfg.kind != 2) return 1;
+        waves = cfg.waves;
+    }
+    const int segs = xt::chunk_cols(fmt) / 16;
+    if (!xt::gemv_fits(fmt, (int)M, nch, waves, xt::gemv_ncw(waves)) ||
+        M * nch * segs > (int64_t)waves * 64)
+        return 1;
+    xt::MMArgs a;
+    memset(&a, 0, sizeof a);
+    int tiles = 0;
+    for (int p = 0; p < n; ++p) {
+        a.proj[p].tiles = ws[p]->tiles;
+        a.proj[p].ws = ws[p]->ws;
+        a.proj[p].y = ys[p];
+        a.proj[p].N = (int)ws[p]->N;
+        a.proj[p].tile0 = tiles;
+        tiles += (int)((ws[p]->N + 15) / 16);
+    }
+    a.nproj = n;
+    a.M = (int)M;
+    a.nch = nch;
+    a.cps = nch;
+    a.x = x;
+    a.ldx = K;
+    a.K = (int)K;
+    a.mode = mode;
+    hipError_t e = xt::launch_gemv(fmt, a, tiles, waves, s);
+    if (e != hipSuccess) return hip_fail(e, "fused GEMV launch");
+    return XT_OK;
+}
+
 int linear_f32(const xt_weights* const* ws, int n, const float* x, int64_t M, float* const* ys,
                int mode, hipStream_t s) {
     if (int rc = check_group(ws, n, x, M, ys)) return rc;
     if (mode != XT_QUANT_AVX512 && mode != XT_QUANT_SCALAR)
         return fail(XT_ERR_INVALID, "unknown quantisation mode");
     if (M == 0) return XT_OK;
+    const int fr = gemv_fused_quant(ws, n, x, M, ys, mode, s);
+    if (fr <= 0) return fr;
     const int64_t K = ws[0]->K;
     const int64_t kpad = ws[0]->nch * xt::chunk_cols(ws[0]->fmt);
     const size_t qbytes = align_up((size_t)M * kpad, 256);

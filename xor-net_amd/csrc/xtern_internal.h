@@ -56,7 +56,16 @@ struct MMArgs {
     int32_t* part;          // split-K partial sums [M][ldp], all zero between calls
     int ldp;
     unsigned* cnt;          // split-K arrival counters, one per (x, y) tile, zero between calls
+    // GEMV only: when x is set the kernel quantises the f32 rows x [M][ldx]
+    // (in_dim K, rounding `mode`) itself instead of reading q / inv.
+    const float* x;
+    int64_t ldx;
+    int K;
+    int mode;
 };
+// GEMV with the quantiser fused when M * K is at most this (every workgroup
+// re-reads the f32 rows, so only for small inputs).
+constexpr int kGemvFusedQuantMax = 8192;
 
 struct MMConfig {
     int mb, nb, waves, pf;  // tokens per WG = 16*mb, rows per WG = 16*nb

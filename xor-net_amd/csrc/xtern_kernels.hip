@@ -544,6 +544,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const MMArgs a) {
     extern __shared__ __align__(16) uint8_t lds[];
     __shared__ v4i red[WAVES][64];
     __shared__ int rsum[16];
+    __shared__ unsigned rmax[16];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -587,25 +588,92 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const MMArgs a) {
     const int o = G * 16 + j;
     const float wscale = (wave == 0 && o < N) ? ws[o] : 0.0f;
     float invr[4];
+    const bool fused = a.x != nullptr;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) invr[r] = (wave == 0 && 4 * g + r < M) ? a.inv[4 * g + r] : 0.0f;
-    __syncthreads();  // rsum cleared
+    for (int r = 0; r < 4; ++r) invr[r] = (!fused && wave == 0 && 4 * g + r < M) ? a.inv[4 * g + r] : 0.0f;
+    if (threadIdx.x < 16) rmax[threadIdx.x] = 0u;
+    __syncthreads();  // rsum / rmax cleared
 
-    // activations -> LDS, with exact per-token byte sums (v_dot4 by 1s)
     const int pieces = M * nch * SEGS;
-    for (int p = threadIdx.x; p < pieces; p += WAVES * 64) {
+    if (fused) {
+        // Quantiser fused (quantization.rs:95-195, as quantize_kernel): every
+        // piece (16 columns of one row) is read as f32, the row absmax is
+        // gathered through LDS, then the piece is quantised into the stage.
+        // The caller guarantees at most one piece per thread.
+        const int p = threadIdx.x;
         const int m = p % M;
         const int seg = (p / M) % SEGS;
         const int c = p / (M * SEGS);
-        const v4i v = ld_cached(a.q + (size_t)m * a.ldq + (size_t)c * CH + seg * 16);
-        int part = 0;
+        const int col = c * CH + seg * 16;
+        float f[16];
+        float mx = 0.0f;
+        if (p < pieces) {
+            const float* xr = a.x + (size_t)m * a.ldx + col;
+            if (col + 16 <= a.K && ((((uintptr_t)xr) & 15) == 0)) {
 #pragma unroll
-        for (int d = 0; d < 4; ++d) part = __builtin_amdgcn_sdot4(v[d], 0x01010101, part, false);
-        atomicAdd(&rsum[m], part);
-        const int st = seg >> 2, gg = seg & 3;
-        *reinterpret_cast<v4i*>(lds + ((((c * STEPS + st) * 4 + gg) * M + m) << 4)) = v;
+                for (int t = 0; t < 4; ++t) {
+                    const float4 v = reinterpret_cast<const float4*>(xr)[t];
+                    f[4 * t] = v.x;
+                    f[4 * t + 1] = v.y;
+                    f[4 * t + 2] = v.z;
+                    f[4 * t + 3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int t = 0; t < 16; ++t) f[t] = col + t < a.K ? xr[t] : 0.0f;
+            }
+#pragma unroll
+            for (int t = 0; t < 16; ++t) mx = fmaxf(mx, fabsf(f[t]));  // NaN ignored
+            atomicMax(&rmax[m], __float_as_uint(mx));  // non-negative floats order as ints
+        }
+        __syncthreads();
+        if (p < pieces) {
+            const float rmx = __uint_as_float(rmax[m]);
+            const float scale = (rmx > 0.0f) ? __fdiv_rn(127.0f, rmx) : 1.0f;
+            const int kmain = (a.K / 16) * 16;
+            v4i v;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                unsigned w4 = 0;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int k = col + 4 * d + t;
+                    const int b = k < a.K ? quant_one(f[4 * d + t], scale, a.mode, k < kmain) : 0;
+                    w4 |= (unsigned)(b & 255) << (8 * t);
+                }
+                v[d] = (int)w4;
+            }
+            int part = 0;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) part = __builtin_amdgcn_sdot4(v[d], 0x01010101, part, false);
+            atomicAdd(&rsum[m], part);
+            const int st = seg >> 2, gg = seg & 3;
+            *reinterpret_cast<v4i*>(lds + ((((c * STEPS + st) * 4 + gg) * M + m) << 4)) = v;
+        }
+        __syncthreads();
+        if (wave == 0) {
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const float rmx = __uint_as_float(rmax[4 * g + r]);
+                invr[r] = (4 * g + r < M) ? ((rmx > 0.0f) ? __fdiv_rn(rmx, 127.0f) : 1.0f) : 0.0f;
+            }
+        }
+    } else {
+        // activations -> LDS, with exact per-token byte sums (v_dot4 by 1s)
+        for (int p = threadIdx.x; p < pieces; p += WAVES * 64) {
+            const int m = p % M;
+            const int seg = (p / M) % SEGS;
+            const int c = p / (M * SEGS);
+            const v4i v = ld_cached(a.q + (size_t)m * a.ldq + (size_t)c * CH + seg * 16);
+            int part = 0;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) part = __builtin_amdgcn_sdot4(v[d], 0x01010101, part, false);
+            atomicAdd(&rsum[m], part);
+            const int st = seg >> 2, gg = seg & 3;
+            *reinterpret_cast<v4i*>(lds + ((((c * STEPS + st) * 4 + gg) * M + m) << 4)) = v;
+        }
+        __syncthreads();
     }
-    __syncthreads();
 
     // one accumulator per k-step: short dependent MFMA chains
     v4i acc[STEPS];
@@ -820,17 +888,27 @@ __global__ __launch_bounds__(256 * KG) void gemm_kernel(const MMArgs a) {
     // Activation slice -> LDS, A-operand order.  Pieces are taken in LDS
     // order (lane fastest), so the LDS stores are sequential; the global side
     // reads 64-byte runs of 16 token rows.
+    // All of a thread's loads are issued before its first LDS store, so the
+    // slice costs one memory round trip, not one per piece.
     const int pieces = 32 * nc * SEGS;
-    for (int p = threadIdx.x; p < pieces; p += NT) {
+    constexpr int PPT = (32 * NCMAX * SEGS + NT - 1) / NT;  // pieces per thread
+    v4i stage[PPT];
+#pragma unroll
+    for (int r = 0; r < PPT; ++r) {
+        const int p = threadIdx.x + r * NT;
         const int ln = p & 63;
         const int blk = p >> 6;                 // (cc * STEPS + st) * MB + mb
         const int mb = blk % MB;
         const int cs = blk / MB;                // cc * STEPS + st
         const int row = mbase + mb * 16 + (ln & 15);
-        v4i v = v4i{0, 0, 0, 0};
-        if (!(XT_ABLATE & 2) && row < M)
-            v = ld_cached(a.q + (size_t)row * a.ldq + (size_t)cbeg * CH + cs * 64 + (ln >> 4) * 16);
-        if (!(XT_ABLATE & 16)) *reinterpret_cast<v4i*>(lds_a + ((size_t)p << 4)) = v;
+        stage[r] = v4i{0, 0, 0, 0};
+        if (!(XT_ABLATE & 2) && p < pieces && row < M)
+            stage[r] = ld_cached(a.q + (size_t)row * a.ldq + (size_t)cbeg * CH + cs * 64 + (ln >> 4) * 16);
+    }
+#pragma unroll
+    for (int r = 0; r < PPT; ++r) {
+        const int p = threadIdx.x + r * NT;
+        if (!(XT_ABLATE & 16) && p < pieces) *reinterpret_cast<v4i*>(lds_a + ((size_t)p << 4)) = stage[r];
     }
     __syncthreads();
 
