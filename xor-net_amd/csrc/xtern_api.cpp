@@ -279,13 +279,14 @@ int gemv_fused_quant(const xt_weights* const* ws, int n, const float* x, int64_t
         return 1;
     int ng_total = 0;
     for (int p = 0; p < n; ++p) ng_total += (int)((ws[p]->N + 15) / 16);
-    int waves = 0;
+    // The fused GEMV saves the quantiser launch (~4 us), which outweighs the
+    // K-split kernel's edge on every measured shape except many rows of
+    // Pack4 / XorSparse (N >= 8192), where that kernel is ~2.5 us faster.
+    int waves = 16;
     if (xt::is_int_format(fmt)) {
         waves = xt::int_gemv_waves(fmt, (int)M, nch);
-    } else {
-        const xt::MMConfig cfg = xt::choose_config(fmt, (int)M, ng_total, nch, false);
-        if (cfg.kind != 2) return 1;
-        waves = cfg.waves;
+    } else if (fmt != XT_PACK5 && ng_total * 16 >= 8192) {
+        return 1;
     }
     const int segs = xt::chunk_cols(fmt) / 16;
     if (!xt::gemv_fits(fmt, (int)M, nch, waves, xt::gemv_ncw(waves)) ||

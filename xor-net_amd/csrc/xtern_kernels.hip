@@ -1164,6 +1164,21 @@ MMConfig choose_config(int fmt, int M, int ntiles_nb1, int nch, bool have_rowsum
         }
     }
     if (M <= 16) {
+        // Measured (MI355X, rotating weights, M = 1..16): Pack5 decodes
+        // faster with K split over 8 waves of 16-row workgroups; many rows
+        // (N >= 8192) make the GEMV's 16-row workgroups overhead-bound, 32
+        // rows x 4 waves win (C3 4096 -> 14336: 5.9 vs 8.4 us at M = 1);
+        // long K and M >= 4 favour the K-split kernel too.  Short K with few
+        // rows stays on the GEMV.
+        const int nrows = ntiles_nb1 * 16;
+        const int kc = nch * (fmt == XT_PACK5 ? 320 : 256);
+        if (ntiles_nb1 > 0) {
+            if (fmt == XT_PACK5) return MMConfig{1, 1, 8, 2, 1};
+            if (nrows >= 8192 && kc <= 8192) return MMConfig{1, 2, 4, 4, 1};
+            if (kc > 4096) return MMConfig{1, 1, 8, 2, 1};
+            if (nrows >= 4096 && M >= 8) return MMConfig{1, 2, 4, 4, 1};
+            if (nrows >= 4096 && M >= 4) return MMConfig{1, 1, 8, 2, 1};
+        }
         const int w = 16;
         if (gemv_fits(fmt, M, nch, w, gemv_ncw(w))) {
             c = MMConfig{1, 1, w, 1, 1};
