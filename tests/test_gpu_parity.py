@@ -410,7 +410,7 @@ def test_splitk_workspace_alternating_shapes():
             assert np.array_equal(acc.cpu().numpy(), ref)
 
 
-@pytest.mark.parametrize("cfg", ["1,1,4,4,3", "1,4,4,2,2", "2,8,4,2,4"])
+@pytest.mark.parametrize("cfg", ["1,1,4,4,3", "1,4,4,2,2", "2,8,4,2,4", "g32,2", "g32,3", "g32,5"])
 def test_forced_splitk_configs(cfg, monkeypatch):
     """Split-K across workgroups (only taken when forced) stays exact, across
     shape changes that move the partial-sum planes."""

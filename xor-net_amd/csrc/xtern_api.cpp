@@ -194,7 +194,7 @@ int run_product(const xt_weights* const* ws, int n, const int8_t* q, int ldq, co
         if (e != hipSuccess) return hip_fail(e, "ternary GEMV launch");
         return XT_OK;
     }
-    if (cfg.kind == 1) {
+    if (cfg.kind == 1 || cfg.kind == 3) {
         if (cfg.splitk > 1) {
             void* wsp = nullptr;
             size_t region = 0;
@@ -203,7 +203,8 @@ int run_product(const xt_weights* const* ws, int n, const int8_t* q, int ldq, co
             a.part = reinterpret_cast<int32_t*>(static_cast<char*>(wsp) + region);
         }
         a.ldp = cols;
-        hipError_t e = xt::launch_gemm(fmt, a, tiles, cfg.splitk, s);
+        hipError_t e = cfg.kind == 3 ? xt::launch_gemm32(a, tiles, cfg.splitk, s)
+                                     : xt::launch_gemm(fmt, a, tiles, cfg.splitk, s);
         if (e != hipSuccess) return hip_fail(e, "ternary GEMM launch");
         return XT_OK;
     }
@@ -248,7 +249,7 @@ int linear_q(const xt_weights* const* ws, int n, const int8_t* q, const float* i
     const int64_t K = ws[0]->K;
     const int64_t kpad = ws[0]->nch * xt::chunk_cols(ws[0]->fmt);
     const xt::MMConfig probe = xt::choose_config(ws[0]->fmt, (int)M, 0, 0, true);
-    const bool need_rowsum = probe.kind == 1 && !xt::is_int_format(ws[0]->fmt);
+    const bool need_rowsum = (probe.kind == 1 || probe.kind == 3) && !xt::is_int_format(ws[0]->fmt);
     const bool direct = (kpad == K) && ((((uintptr_t)q) & 15) == 0);
     if (direct && user_rowsum)
         return run_product(ws, n, q, (int)K, inv, user_rowsum, M, ys, acc, s);

@@ -70,7 +70,8 @@ constexpr int kGemvFusedQuantMax = 8192;
 struct MMConfig {
     int mb, nb, waves, pf;  // tokens per WG = 16*mb, rows per WG = 16*nb
     int splitk;             // workgroups along K (blockIdx.z)
-    int kind = 0;           // 0 mm_kernel, 1 prefill GEMM, 2 decode GEMV (waves used)
+    int kind = 0;           // 0 mm_kernel, 1 prefill GEMM, 2 decode GEMV (waves used),
+                            // 3 prefill GEMM on 32x32x32 MFMA (Pack4 tiles)
 };
 
 // Kernel launchers (xtern_kernels.hip).  Return the hipError_t of the launch.
@@ -85,6 +86,11 @@ MMConfig choose_config(int fmt, int M, int ntiles_nb1, int nch, bool have_rowsum
 // workgroup, at most gemm_ncmax(fmt) chunks per split-K slice.
 int gemm_ncmax(int fmt);
 hipError_t launch_gemm(int fmt, const MMArgs& a, int ntiles, int splitk, hipStream_t s);
+// Prefill GEMM on 32x32x32 MFMA (Pack4 tiles, M > 16, row sums required):
+// 32 tokens x 128 rows per workgroup, at most gemm32_ncmax() chunks per slice.
+int gemm32_ncmax();
+int g32_splitk(int nch);
+hipError_t launch_gemm32(const MMArgs& a, int ntiles, int splitk, hipStream_t s);
 // Decode GEMV (M <= 16): 16 output rows per workgroup, activations in LDS.
 hipError_t launch_gemv(int fmt, const MMArgs& a, int ntiles, int waves, hipStream_t s);
 int gemv_ncw(int waves);
