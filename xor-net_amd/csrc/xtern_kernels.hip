@@ -287,6 +287,41 @@ __device__ __forceinline__ int xcd_remap(int lin, int total) {
     return xcd * q + min(xcd, r) + slot;
 }
 
+// The projection workgroup column bx belongs to, read through the kernel
+// argument segment (scalar loads; the selected projection is one load at a
+// computed offset -- selecting among by-value fields instead makes the
+// compiler copy the arguments to scratch memory).
+struct ProjView {
+    const uint8_t* tiles;
+    const float* ws;
+    float* y;
+    int32_t* acc;
+    int N, tile0, col0;
+};
+typedef const __attribute__((address_space(4))) MMArgs* KArgPtr;
+struct ProjBounds {
+    int np, t1, t2, t3;
+};
+// Read at kernel entry, in the same round of scalar loads as the grid size.
+__device__ __forceinline__ ProjBounds proj_bounds() {
+    KArgPtr ka = (KArgPtr)__builtin_amdgcn_kernarg_segment_ptr();
+    return ProjBounds{ka->nproj, ka->proj[1].tile0, ka->proj[2].tile0, ka->proj[3].tile0};
+}
+__device__ __forceinline__ ProjView select_proj(const ProjBounds& pb, int bx) {
+    KArgPtr ka = (KArgPtr)__builtin_amdgcn_kernarg_segment_ptr();
+    const int sel = ((pb.np > 1) & (bx >= pb.t1)) + ((pb.np > 2) & (bx >= pb.t2)) +
+                    ((pb.np > 3) & (bx >= pb.t3));
+    ProjView v;
+    v.tiles = ka->proj[sel].tiles;
+    v.ws = ka->proj[sel].ws;
+    v.y = ka->proj[sel].y;
+    v.acc = ka->proj[sel].acc;
+    v.N = ka->proj[sel].N;
+    v.tile0 = ka->proj[sel].tile0;
+    v.col0 = ka->proj[sel].col0;
+    return v;
+}
+
 // Pack4 tile dword -> four code dwords (columns 4jj..4jj+3 in byte order).
 __device__ __forceinline__ v4i decode4(int x) {
     v4i b;
@@ -329,25 +364,14 @@ __global__ __launch_bounds__(WAVES * 64) void mm_kernel(const MMArgs a) {
     // Which projection this workgroup belongs to (constant-index selects keep
     // the kernel-argument struct out of scratch memory).
     const int bx = blockIdx.x;
-    const uint8_t* tiles = a.proj[0].tiles;
-    const float* ws = a.proj[0].ws;
-    float* y = a.proj[0].y;
-    int32_t* accout = a.proj[0].acc;
-    int N = a.proj[0].N;
-    int tile0 = 0;
-    int col0 = a.proj[0].col0;
-#pragma unroll
-    for (int p = 1; p < 4; ++p) {
-        if (p < a.nproj && bx >= a.proj[p].tile0) {
-            tiles = a.proj[p].tiles;
-            ws = a.proj[p].ws;
-            y = a.proj[p].y;
-            accout = a.proj[p].acc;
-            N = a.proj[p].N;
-            tile0 = a.proj[p].tile0;
-            col0 = a.proj[p].col0;
-        }
-    }
+    const ProjView pv = select_proj(proj_bounds(), bx);
+    const uint8_t* tiles = pv.tiles;
+    const float* ws = pv.ws;
+    float* y = pv.y;
+    int32_t* accout = pv.acc;
+    const int N = pv.N;
+    const int tile0 = pv.tile0;
+    const int col0 = pv.col0;
     const int ntile = bx - tile0;
     const int NG = (N + 15) >> 4;
     const int M = a.M;
@@ -553,23 +577,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemv_kernel(const MMArgs a) {
     const int j = lane & 15;
 
     const int bx = blockIdx.x;
-    const uint8_t* tiles = a.proj[0].tiles;
-    const float* ws = a.proj[0].ws;
-    float* y = a.proj[0].y;
-    int32_t* accout = a.proj[0].acc;
-    int N = a.proj[0].N;
-    int tile0 = 0;
-#pragma unroll
-    for (int p = 1; p < 4; ++p) {
-        if (p < a.nproj && bx >= a.proj[p].tile0) {
-            tiles = a.proj[p].tiles;
-            ws = a.proj[p].ws;
-            y = a.proj[p].y;
-            accout = a.proj[p].acc;
-            N = a.proj[p].N;
-            tile0 = a.proj[p].tile0;
-        }
-    }
+    const ProjView pv = select_proj(proj_bounds(), bx);
+    const uint8_t* tiles = pv.tiles;
+    const float* ws = pv.ws;
+    float* y = pv.y;
+    int32_t* accout = pv.acc;
+    const int N = pv.N;
+    const int tile0 = pv.tile0;
     const int G = bx - tile0;
     const int M = a.M;
     const int nch = a.nch;
@@ -760,7 +774,139 @@ bool gemv_fits(int fmt, int M, int nch, int waves, int ncw) {
            (nch + waves - 1) / waves <= ncw;
 }
 
+// ---------------------------------------------------------------------------
+// Decode GEMV for ternary formats without staging (M <= 16, q given)
+// ---------------------------------------------------------------------------
+//
+// Workgroup x owns the 16 output rows of row group x (of the projection x
+// falls in) over all of K; wave w takes chunks w, w + WAVES, ...  Every lane
+// loads its weight slot and its four (Pack5: five) 16-byte activation pieces
+// straight from memory -- no LDS stage, no barrier before the MFMAs -- and all
+// loads are unconditional (clamped indices, zero-selected afterwards), so
+// they issue back to back.  Codes are decoded to signed weights with one
+// v_perm_b32 (code 0 -> -1, 1 -> 0, 2 -> +1, 3 -> 0), so no activation row
+// sum is needed.  Waves are summed through LDS once at the end.
+__device__ __forceinline__ int signed_codes(int c) {
+    // byte i of the result = byte c_i of 0x000100ff: codes 0..3 -> -1, 0, +1, 0
+    return (int)__builtin_amdgcn_perm(0u, 0x000100ffu, (unsigned)c);
+}
+
+template <int FMT, int WAVES, int NCW>
+__global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
+    constexpr int STEPS = (FMT == XT_PACK5) ? 5 : 4;
+    constexpr int CH = STEPS * 64;
+    __shared__ v4i red[WAVES][64];
+    const int lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6;
+    const int g = lane >> 4;
+    const int j = lane & 15;
+    const int bx = blockIdx.x;
+    const int M = a.M;
+    const int nch = a.nch;
+    const int ldq = a.ldq;
+    const int8_t* q = a.q;
+    const float* inv = a.inv;
+    const ProjBounds pb = proj_bounds();
+    __builtin_amdgcn_sched_barrier(0);  // one round of argument loads
+    const ProjView pv = select_proj(pb, bx);
+    const int G = bx - pv.tile0;
+    const int N = pv.N;
+
+    // epilogue operands (wave 0 finishes: tokens 4g + r, output row o)
+    const int o = G * 16 + j;
+    const float wscale = pv.ws[min(o, N - 1)];
+    float invr[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) invr[r] = inv[min(4 * g + r, M - 1)];
+
+    const uint8_t* wsrc = pv.tiles + ((size_t)G * nch * 64 + lane) * 16;
+    const int8_t* arow = q + (size_t)min(j, M - 1) * ldq + 16 * g;
+    v4i wv[NCW];
+    v4i av[NCW][STEPS];
+#pragma unroll
+    for (int t = 0; t < NCW; ++t) {
+        const int c = min(wave + t * WAVES, nch - 1);
+        wv[t] = ld_stream(wsrc + (size_t)c * kTileBytes);
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s) av[t][s] = ld_cached(arow + (size_t)c * CH + s * 64);
+    }
+    v4i acc[STEPS];
+#pragma unroll
+    for (int s = 0; s < STEPS; ++s) acc[s] = v4i{0, 0, 0, 0};
+#pragma unroll
+    for (int t = 0; t < NCW; ++t) {
+        const bool live = wave + t * WAVES < nch;
+        if constexpr (FMT == XT_PACK5) {
+            int E[4], O[4];
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                E[d] = wv[t][d] & 0x00ff00ff;
+                O[d] = ((unsigned)wv[t][d] >> 8) & 0x00ff00ff;
+            }
+#pragma unroll
+            for (int s = 0; s < STEPS; ++s) {
+                v4i b;
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    const int pE = E[d] * 3, pO = O[d] * 3;
+                    b[d] = signed_codes((int)__builtin_amdgcn_perm((unsigned)pO, (unsigned)pE, 0x07030501u));
+                    E[d] = pE & 0x00ff00ff;
+                    O[d] = pO & 0x00ff00ff;
+                }
+                const v4i x = (live && j < M) ? av[t][s] : v4i{0, 0, 0, 0};
+                acc[s] = mfma(x, b, acc[s]);
+            }
+        } else {
+#pragma unroll
+            for (int s = 0; s < STEPS; ++s) {
+                v4i b = decode4(wv[t][s]);
+#pragma unroll
+                for (int d = 0; d < 4; ++d) b[d] = signed_codes(b[d]);
+                const v4i x = (live && j < M) ? av[t][s] : v4i{0, 0, 0, 0};
+                acc[s] = mfma(x, b, acc[s]);
+            }
+        }
+    }
+#pragma unroll
+    for (int s = 1; s < STEPS; ++s) acc[0] += acc[s];
+    red[wave][lane] = acc[0];
+    __syncthreads();
+    if (wave != 0 || o >= N) return;
+    v4i sum = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) sum += red[w][lane];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int i = 4 * g + r;
+        if (i >= M) continue;
+        // layers.rs:294 — (dot as f32 * inv_scale) * w_scale, two roundings.
+        pv.y[(size_t)i * N + o] = __fmul_rn(__fmul_rn((float)sum[r], invr[r]), wscale);
+        if (pv.acc) pv.acc[(size_t)i * N + o] = sum[r];
+    }
+}
+
+// The staging-free GEMV applies to ternary tiles with caller-quantised rows.
+static hipError_t launch_gemv2(int fmt, const MMArgs& a, int ntiles, hipStream_t s) {
+    const int nch = a.nch;
+#define XT_GV2(W_, NCW_)                                                                         \
+    if (nch <= W_ * NCW_) {                                                                      \
+        if (fmt == XT_PACK5)                                                                     \
+            hipLaunchKernelGGL((gemv2_kernel<XT_PACK5, W_, NCW_>), dim3(ntiles), dim3(W_ * 64), 0, s, a); \
+        else                                                                                     \
+            hipLaunchKernelGGL((gemv2_kernel<XT_PACK4, W_, NCW_>), dim3(ntiles), dim3(W_ * 64), 0, s, a); \
+        return hipGetLastError();                                                                \
+    }
+    XT_GV2(4, 1) XT_GV2(8, 1) XT_GV2(10, 1) XT_GV2(16, 1) XT_GV2(16, 2) XT_GV2(16, 3)
+    XT_GV2(16, 4)
+#undef XT_GV2
+    return hipErrorInvalidValue;
+}
+
 hipError_t launch_gemv(int fmt, const MMArgs& a, int ntiles, int waves, hipStream_t s) {
+    static const bool staged = getenv("XTERN_GEMV_STAGED") != nullptr;
+    if (!staged && (fmt == XT_PACK4 || fmt == XT_PACK5 || fmt == XT_XORSPARSE) && a.x == nullptr &&
+        a.nch <= 64)
+        return launch_gemv2(fmt == XT_PACK5 ? XT_PACK5 : XT_PACK4, a, ntiles, s);
     const int ch = fmt == XT_PACK5 ? 320 : 256;
     const size_t lds = (size_t)a.M * a.nch * ch;
 #define XT_GEMV(W_, NCW_)                                                                        \
@@ -826,25 +972,14 @@ __global__ __launch_bounds__(256 * KG) void gemm_kernel(const MMArgs a) {
     const int by = t % gy;
     const int bx = (t / gy) % gx;
     const int bz = t / (gx * gy);
-    const uint8_t* tiles = a.proj[0].tiles;
-    const float* ws = a.proj[0].ws;
-    float* y = a.proj[0].y;
-    int32_t* accout = a.proj[0].acc;
-    int N = a.proj[0].N;
-    int tile0 = 0;
-    int col0 = a.proj[0].col0;
-#pragma unroll
-    for (int p = 1; p < 4; ++p) {
-        if (p < a.nproj && bx >= a.proj[p].tile0) {
-            tiles = a.proj[p].tiles;
-            ws = a.proj[p].ws;
-            y = a.proj[p].y;
-            accout = a.proj[p].acc;
-            N = a.proj[p].N;
-            tile0 = a.proj[p].tile0;
-            col0 = a.proj[p].col0;
-        }
-    }
+    const ProjView pv = select_proj(proj_bounds(), bx);
+    const uint8_t* tiles = pv.tiles;
+    const float* ws = pv.ws;
+    float* y = pv.y;
+    int32_t* accout = pv.acc;
+    const int N = pv.N;
+    const int tile0 = pv.tile0;
+    const int col0 = pv.col0;
     const int NG = (N + 15) >> 4;
     const int M = a.M;
     const int mbase = by * 32;
@@ -1136,51 +1271,17 @@ __device__ __forceinline__ void wait_vmcnt(int vm) {
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
     return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)p;
 }
-// ds_read_b128 whose completion the caller waits for with lgkm_wait5.
+// ds_read_b128 whose completion the caller waits for with lgkm_wait4.
 __device__ __forceinline__ v4i ds_read16(uint32_t addr) {
     v4i v;
     __asm__ volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
     return v;
 }
 // Wait for all LDS reads; the operands tie the wait to the values read.
-__device__ __forceinline__ void lgkm_wait5(v4i& a, v4i& b, v4i& c, v4i& d, v4i& e) {
-    __asm__ volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d), "+v"(e));
+__device__ __forceinline__ void lgkm_wait4(v4i& a, v4i& b, v4i& c, v4i& d) {
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
 }
 
-// The projection workgroup column bx belongs to, read through the kernel
-// argument segment (scalar loads; the selected projection is one load at a
-// computed offset -- selecting among by-value fields instead makes the
-// compiler copy the arguments to scratch memory).
-struct ProjView {
-    const uint8_t* tiles;
-    const float* ws;
-    float* y;
-    int32_t* acc;
-    int N, tile0, col0;
-};
-typedef const __attribute__((address_space(4))) MMArgs* KArgPtr;
-struct ProjBounds {
-    int np, t1, t2, t3;
-};
-// Read at kernel entry, in the same round of scalar loads as the grid size.
-__device__ __forceinline__ ProjBounds proj_bounds() {
-    KArgPtr ka = (KArgPtr)__builtin_amdgcn_kernarg_segment_ptr();
-    return ProjBounds{ka->nproj, ka->proj[1].tile0, ka->proj[2].tile0, ka->proj[3].tile0};
-}
-__device__ __forceinline__ ProjView select_proj(const ProjBounds& pb, int bx) {
-    KArgPtr ka = (KArgPtr)__builtin_amdgcn_kernarg_segment_ptr();
-    const int sel = ((pb.np > 1) & (bx >= pb.t1)) + ((pb.np > 2) & (bx >= pb.t2)) +
-                    ((pb.np > 3) & (bx >= pb.t3));
-    ProjView v;
-    v.tiles = ka->proj[sel].tiles;
-    v.ws = ka->proj[sel].ws;
-    v.y = ka->proj[sel].y;
-    v.acc = ka->proj[sel].acc;
-    v.N = ka->proj[sel].N;
-    v.tile0 = ka->proj[sel].tile0;
-    v.col0 = ka->proj[sel].col0;
-    return v;
-}
 
 // ---------------------------------------------------------------------------
 // Prefill GEMM, warp-specialised: loader waves stream chunks into LDS while
@@ -1202,8 +1303,13 @@ __device__ __forceinline__ ProjView select_proj(const ProjBounds& pb, int bx) {
 // L are added through LDS, the 32 x 128 code-domain tile is staged in LDS
 // and written as whole 16-byte row pieces.  With gridDim.z > 1 the slice's
 // code-domain sums go to plane z of `part` and gemm_reduce_kernel finishes.
-constexpr int kG32sSlot = 16384;
-constexpr int kG32sAhead = 4;
+constexpr int kG32sSlot = 8192;
+// First LDS slot of the epilogue's exchange (2 slots) and output tile (2).
+__host__ __device__ constexpr int g32s_xch_slot(int ncmax) { return ncmax >= 3 ? 0 : ncmax; }
+#ifndef XT_G32S_AHEAD
+#define XT_G32S_AHEAD 4
+#endif
+constexpr int kG32sAhead = XT_G32S_AHEAD;
 
 template <int NCMAX>
 __global__ __launch_bounds__(768) void gemm32s_kernel(const MMArgs a) {
@@ -1231,45 +1337,43 @@ __global__ __launch_bounds__(768) void gemm32s_kernel(const MMArgs a) {
     const int nc = min(nch - cbeg, cps);  // chunks of this slice, 1..NCMAX
     const int gblk = (bx - pv.tile0) * 8;  // first row group of the block
 
+    // The gy token blocks that share the weights start at different quarters
+    // of the slice (different HBM lines in flight; integer sums do not depend
+    // on the order).  Chunk c of the loop is slice chunk chunk_at(c); chunks
+    // past the slice re-read its last chunk and count as code 0.
+    const int rot = ((by & 3) * nc) >> 2;
+    auto chunk_at = [&](int c) {
+        const int cr = c + rot;
+        return c < nc ? (cr >= nc ? cr - nc : cr) : nc - 1;
+    };
+
     if (wave >= 8) {
-        // Loader wave lw: activation rows 8 lw .. 8 lw + 7 (two 1 KiB copies)
-        // and weight tiles 2 lw, 2 lw + 1 of every chunk.  Chunks past the
-        // slice re-read its last chunk (the MFMA waves zero their weights),
-        // so every loader issues exactly four copies per chunk and the vmcnt
-        // of each chunk is a compile-time number.  The gy token blocks that
-        // share the weights start at different quarters of the slice
-        // (different HBM lines in flight; integer sums do not depend on the
-        // order).
+        // Loader wave lw copies activation rows 8 lw .. 8 lw + 7 of every
+        // chunk (two 1 KiB direct-to-LDS copies), so each chunk's vmcnt is a
+        // compile-time number, and signals landed chunks with barriers.
         const int lw = wave - 8;
-        const int rot = ((by & 3) * nc) >> 2;
         const int8_t* as[2];
-        const uint8_t* wsrc[2];
 #pragma unroll
         for (int jj = 0; jj < 2; ++jj) {
             const int tk = 4 * (2 * lw + jj) + (lane >> 4);
             const int trow = min(mbase + tk, M - 1);
             as[jj] = a.q + (size_t)trow * a.ldq + (size_t)cbeg * CH + ((lane & 15) ^ (tk & 15)) * 16;
-            const int G = min(gblk + 2 * lw + jj, NG - 1);
-            wsrc[jj] = pv.tiles + ((size_t)(G * nch + cbeg) * 64 + lane) * 16;
         }
         constexpr int D = kG32sAhead < NCMAX ? kG32sAhead : NCMAX;
 #pragma unroll
         for (int c = 0; c < NCMAX; ++c) {
-            const int cr = c + rot;
-            const int cc = c < nc ? (cr >= nc ? cr - nc : cr) : nc - 1;
+            const int cc = chunk_at(c);
             uint8_t* slot = lds + c * kG32sSlot;
             load_lds16(as[0] + cc * CH, slot + (2 * lw) * 1024);
             load_lds16(as[1] + cc * CH, slot + (2 * lw + 1) * 1024);
-            load_lds16(wsrc[0] + (size_t)cc * kTileBytes, slot + 8192 + (2 * lw) * 1024);
-            load_lds16(wsrc[1] + (size_t)cc * kTileBytes, slot + 8192 + (2 * lw + 1) * 1024);
             if (c >= D - 1) {  // chunk c - D + 1 has landed
-                wait_vmcnt(4 * (D - 1));
+                wait_vmcnt(2 * (D - 1));
                 __builtin_amdgcn_s_barrier();
             }
         }
 #pragma unroll
         for (int c = NCMAX - D + 1; c < NCMAX; ++c) {
-            wait_vmcnt(4 * (NCMAX - 1 - c));
+            wait_vmcnt(2 * (NCMAX - 1 - c));
             __builtin_amdgcn_s_barrier();
         }
         __builtin_amdgcn_s_barrier();  // the MFMA waves' exchange
@@ -1300,52 +1404,73 @@ __global__ __launch_bounds__(768) void gemm32s_kernel(const MMArgs a) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) sws[e] = pv.ws[min(ob + sc4 + e, N - 1)];
 
+    // This wave's weights: its 16-byte tile slot of every chunk, loaded into
+    // registers kG32sAhead chunks ahead of use.
+    const int G = min((bx - pv.tile0) * 8 + 2 * n + (r >> 4), NG - 1);
+    const uint8_t* wsrc = pv.tiles + ((size_t)(G * nch + cbeg) * 64 + 16 * (2 * L + h) + (r & 15)) * 16;
+    constexpr int DW = kG32sAhead < NCMAX ? kG32sAhead : NCMAX;
+    v4i wv[NCMAX];
+#pragma unroll
+    for (int c = 0; c < DW; ++c)
+        wv[c] = *reinterpret_cast<const v4i*>(wsrc + (size_t)chunk_at(c) * kTileBytes);
+
+    // Software-pipelined by one chunk: after the barrier that says chunk
+    // c + 1 has landed, the wave reads its A fragments while chunk c's four
+    // MFMAs (one accumulator per k-step, so none waits for another) run.
     const uint32_t abase = lds_addr(lds) + r * CH;
-    const uint32_t bbase = lds_addr(lds) + 8192 + (2 * n + (r >> 4)) * 1024 +
-                           (16 * (2 * L + h) + (r & 15)) * 16;
-    v16i acc, acc2;
-#pragma unroll
-    for (int k = 0; k < 16; ++k) acc[k] = acc2[k] = 0;
-#pragma unroll
-    for (int c = 0; c < NCMAX; ++c) {
-        __syncthreads();  // chunk c has landed
-        v4i av[4];
+    auto read_a = [&](int c, v4i* av) {
 #pragma unroll
         for (int s = 0; s < 4; ++s) {
             const int p = 4 * s + 2 * L + h;
             av[s] = ds_read16(abase + c * kG32sSlot + ((p ^ (r & 15)) << 4));
         }
-        v4i bv = ds_read16(bbase + c * kG32sSlot);
-        lgkm_wait5(av[0], av[1], av[2], av[3], bv);
-        if (c >= nc) bv = v4i{0, 0, 0, 0};
-        acc = mfma32(av[0], decode4(bv[0]), acc);
-        acc2 = mfma32(av[1], decode4(bv[1]), acc2);
-        acc = mfma32(av[2], decode4(bv[2]), acc);
-        acc2 = mfma32(av[3], decode4(bv[3]), acc2);
+        lgkm_wait4(av[0], av[1], av[2], av[3]);
+    };
+    v16i acc[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s)
+#pragma unroll
+        for (int k = 0; k < 16; ++k) acc[s][k] = 0;
+    v4i acur[4];
+    __syncthreads();  // chunk 0 has landed
+    read_a(0, acur);
+#pragma unroll
+    for (int c = 0; c < NCMAX; ++c) {
+        if (c + DW < NCMAX)
+            wv[c + DW] = *reinterpret_cast<const v4i*>(wsrc + (size_t)chunk_at(c + DW) * kTileBytes);
+        const v4i bv = (c < nc) ? wv[c] : v4i{0, 0, 0, 0};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc[s] = mfma32(acur[s], decode4(bv[s]), acc[s]);
+        if (c + 1 < NCMAX) {
+            __syncthreads();  // chunk c + 1 has landed
+            read_a(c + 1, acur);
+        }
     }
-    acc += acc2;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) acc[0][k] += acc[1][k] + acc[2][k] + acc[3][k];
 
-    // Add the halves L through LDS (slot 0: every wave is past chunk 0's
-    // reads, which completed before the last chunk's barrier).  Slot [L][n]
-    // [k][lane] carries registers 8(1 - L) + k for the other wave of the pair.
-    int32_t* xch = reinterpret_cast<int32_t*>(lds);
+    // Add the halves L through LDS, in slots 0-1 when every wave is past
+    // their reads (their chunks completed before the last chunk's barrier),
+    // else after the chunk slots.  Entry [L][n][k][lane] carries registers
+    // 8(1 - L) + k for the other wave of the pair.
+    int32_t* xch = reinterpret_cast<int32_t*>(lds + g32s_xch_slot(NCMAX) * kG32sSlot);
     int keep[8];
     if (L == 0) {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            xch[((0 * 4 + n) * 8 + k) * 64 + lane] = acc[8 + k];
-            keep[k] = acc[k];
+            xch[((0 * 4 + n) * 8 + k) * 64 + lane] = acc[0][8 + k];
+            keep[k] = acc[0][k];
         }
     } else {
 #pragma unroll
         for (int k = 0; k < 8; ++k) {
-            xch[((1 * 4 + n) * 8 + k) * 64 + lane] = acc[k];
-            keep[k] = acc[8 + k];
+            xch[((1 * 4 + n) * 8 + k) * 64 + lane] = acc[0][k];
+            keep[k] = acc[0][8 + k];
         }
     }
     __syncthreads();
     // Code-domain sums of the 32 x 128 tile -> LDS (slot 1), then whole rows.
-    int32_t* dtile = reinterpret_cast<int32_t*>(lds + kG32sSlot);  // [32][128]
+    int32_t* dtile = reinterpret_cast<int32_t*>(xch + 4096);  // [32][128], two slots on
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         const int il = 8 * (2 * L + (k >> 2)) + 4 * h + (k & 3);
@@ -1389,18 +1514,20 @@ __global__ __launch_bounds__(768) void gemm32s_kernel(const MMArgs a) {
     }
 }
 
-int gemm32s_ncmax() { return 10; }
+int gemm32s_ncmax() { return 18; }
 
 hipError_t launch_gemm32s(const MMArgs& a, int ntiles, int splitk, hipStream_t s) {
     const dim3 grid(ntiles, (a.M + 31) / 32, splitk);
     const int ncm = a.cps;
     if (ncm < 1 || ncm > gemm32s_ncmax()) return hipErrorInvalidValue;
-    const size_t lds = (size_t)(ncm < 2 ? 2 : ncm) * kG32sSlot;
+    const int xs = g32s_xch_slot(ncm) + 4;
+    const size_t lds = (size_t)(ncm < xs ? xs : ncm) * kG32sSlot;
     switch (ncm) {
 #define XT_G32S(V) \
     case V: hipLaunchKernelGGL((gemm32s_kernel<V>), grid, dim3(768), lds, s, a); break;
         XT_G32S(1) XT_G32S(2) XT_G32S(3) XT_G32S(4) XT_G32S(5) XT_G32S(6) XT_G32S(7)
-        XT_G32S(8) XT_G32S(9) XT_G32S(10)
+        XT_G32S(8) XT_G32S(9) XT_G32S(10) XT_G32S(11) XT_G32S(12) XT_G32S(13) XT_G32S(14)
+        XT_G32S(15) XT_G32S(16) XT_G32S(17) XT_G32S(18)
 #undef XT_G32S
         default: return hipErrorInvalidValue;
     }
