@@ -289,9 +289,14 @@ int gemv_fused_quant(const xt_weights* const* ws, int n, const float* x, int64_t
     } else if (fmt != XT_PACK5 && ng_total * 16 >= 8192) {
         return 1;
     }
+    // Ternary tiles take the staging-free GEMV (one chunk per wave, so
+    // K <= 16 chunks); Int8 / Int4 the staged one (one piece per thread).
+    static const bool staged = getenv("XTERN_GEMV_STAGED") != nullptr;
+    const bool direct = !xt::is_int_format(fmt) && !staged;
     const int segs = xt::chunk_cols(fmt) / 16;
-    if (!xt::gemv_fits(fmt, (int)M, nch, waves, xt::gemv_ncw(waves)) ||
-        M * nch * segs > (int64_t)waves * 64)
+    if (direct ? nch > 16
+               : (!xt::gemv_fits(fmt, (int)M, nch, waves, xt::gemv_ncw(waves)) ||
+                  M * nch * segs > (int64_t)waves * 64))
         return 1;
     xt::MMArgs a;
     memset(&a, 0, sizeof a);

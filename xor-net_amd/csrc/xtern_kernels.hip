@@ -791,11 +791,16 @@ __device__ __forceinline__ int signed_codes(int c) {
     return (int)__builtin_amdgcn_perm(0u, 0x000100ffu, (unsigned)c);
 }
 
-template <int FMT, int WAVES, int NCW>
+// FUSED: the kernel quantises the f32 rows a.x itself (quantization.rs:95-195,
+// as quantize_kernel): each lane reads its pieces as f32, the per-token
+// absmax goes through the waves' shuffles and LDS (one barrier), then each
+// lane quantises its own pieces.  No separate quantiser launch.
+template <int FMT, int WAVES, int NCW, bool FUSED>
 __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
     constexpr int STEPS = (FMT == XT_PACK5) ? 5 : 4;
     constexpr int CH = STEPS * 64;
     __shared__ v4i red[WAVES][64];
+    __shared__ unsigned tmax[WAVES][16];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int g = lane >> 4;
@@ -816,19 +821,93 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
     const int o = G * 16 + j;
     const float wscale = pv.ws[min(o, N - 1)];
     float invr[4];
+    if constexpr (!FUSED) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) invr[r] = inv[min(4 * g + r, M - 1)];
+        for (int r = 0; r < 4; ++r) invr[r] = inv[min(4 * g + r, M - 1)];
+    }
 
     const uint8_t* wsrc = pv.tiles + ((size_t)G * nch * 64 + lane) * 16;
-    const int8_t* arow = q + (size_t)min(j, M - 1) * ldq + 16 * g;
     v4i wv[NCW];
     v4i av[NCW][STEPS];
+    if constexpr (!FUSED) {
+        const int8_t* arow = q + (size_t)min(j, M - 1) * ldq + 16 * g;
 #pragma unroll
-    for (int t = 0; t < NCW; ++t) {
-        const int c = min(wave + t * WAVES, nch - 1);
-        wv[t] = ld_stream(wsrc + (size_t)c * kTileBytes);
+        for (int t = 0; t < NCW; ++t) {
+            const int c = min(wave + t * WAVES, nch - 1);
+            wv[t] = ld_stream(wsrc + (size_t)c * kTileBytes);
 #pragma unroll
-        for (int s = 0; s < STEPS; ++s) av[t][s] = ld_cached(arow + (size_t)c * CH + s * 64);
+            for (int s = 0; s < STEPS; ++s) av[t][s] = ld_cached(arow + (size_t)c * CH + s * 64);
+        }
+    } else {
+        // Cooperative quantisation: thread t takes float4 pieces t, t + NT,
+        // ... of the M x K rows (K % 4 == 0, so a piece never straddles two
+        // rows), gathers each token's absmax through LDS, quantises its
+        // pieces into the A-operand stage [chunk][step][g][token 0..15][16 B],
+        // and after a barrier every lane reads its fragments.  Stage bytes of
+        // columns >= K are never written; their weights are padding code 1,
+        // which decodes to 0.
+        extern __shared__ __align__(16) uint8_t stage[];
+        const int K = a.K;
+        constexpr int NT = WAVES * 64;
+        const int n4 = (M * K) >> 2;
+        if (threadIdx.x < 16) tmax[0][threadIdx.x] = 0u;
+#pragma unroll
+        for (int t = 0; t < NCW; ++t) {
+            const int c = min(wave + t * WAVES, nch - 1);
+            wv[t] = ld_stream(wsrc + (size_t)c * kTileBytes);
+        }
+        float4 xv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int f = threadIdx.x + u * NT;
+            if (f < n4) {
+                const int m = (4 * f) / K, col = 4 * f - m * K;
+                xv[u] = *reinterpret_cast<const float4*>(a.x + (size_t)m * a.ldx + col);
+            }
+        }
+        __syncthreads();  // tmax cleared
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int f = threadIdx.x + u * NT;
+            if (f < n4) {
+                const int m = (4 * f) / K;
+                const float mx = fmaxf(fmaxf(fabsf(xv[u].x), fabsf(xv[u].y)),
+                                       fmaxf(fabsf(xv[u].z), fabsf(xv[u].w)));  // NaN ignored
+                atomicMax(&tmax[0][m], __float_as_uint(mx));  // non-negative floats order as ints
+            }
+        }
+        __syncthreads();
+        const int kmain = (K / 16) * 16;
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int f = threadIdx.x + u * NT;
+            if (f < n4) {
+                const int m = (4 * f) / K, col = 4 * f - m * K;
+                const float rmx = __uint_as_float(tmax[0][m]);
+                const float scale = (rmx > 0.0f) ? __fdiv_rn(127.0f, rmx) : 1.0f;
+                const float e4[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+                unsigned w4 = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    w4 |= (unsigned)(quant_one(e4[e], scale, a.mode, col + e < kmain) & 255) << (8 * e);
+                const int c = col / CH, r = col - c * CH, st = r >> 6, gg = (r >> 4) & 3;
+                *reinterpret_cast<unsigned*>(stage + ((((c * STEPS + st) * 4 + gg) * 16 + m) << 4) + (col & 15)) = w4;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int t = 0; t < NCW; ++t) {
+            const int c = min(wave + t * WAVES, nch - 1);
+#pragma unroll
+            for (int s = 0; s < STEPS; ++s)
+                av[t][s] = *reinterpret_cast<const v4i*>(stage + ((((c * STEPS + s) * 4 + g) * 16 + j) << 4));
+        }
+        // inverse scales of tokens 4g + r (wave 0 finishes)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float x2 = __uint_as_float(tmax[0][min(4 * g + r, 15)]);
+            invr[r] = (x2 > 0.0f) ? __fdiv_rn(x2, 127.0f) : 1.0f;
+        }
     }
     v4i acc[STEPS];
 #pragma unroll
@@ -872,7 +951,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
     red[wave][lane] = acc[0];
     __syncthreads();
     if (wave != 0 || o >= N) return;
-    v4i sum = red[0][lane];
+    v4i sum = red[0][lane];  // (tmax is not reused: no barrier needed before red)
 #pragma unroll
     for (int w = 1; w < WAVES; ++w) sum += red[w][lane];
 #pragma unroll
@@ -888,12 +967,23 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
 // The staging-free GEMV applies to ternary tiles with caller-quantised rows.
 static hipError_t launch_gemv2(int fmt, const MMArgs& a, int ntiles, hipStream_t s) {
     const int nch = a.nch;
+    // fused rows: at most 8 float4 per thread, A stage of 1 KiB per k-step
+    const size_t stage = (size_t)nch * (fmt == XT_PACK5 ? 5 : 4) * 1024;
 #define XT_GV2(W_, NCW_)                                                                         \
     if (nch <= W_ * NCW_) {                                                                      \
-        if (fmt == XT_PACK5)                                                                     \
-            hipLaunchKernelGGL((gemv2_kernel<XT_PACK5, W_, NCW_>), dim3(ntiles), dim3(W_ * 64), 0, s, a); \
-        else                                                                                     \
-            hipLaunchKernelGGL((gemv2_kernel<XT_PACK4, W_, NCW_>), dim3(ntiles), dim3(W_ * 64), 0, s, a); \
+        if (a.x) {                                                                               \
+            if (NCW_ != 1 || (size_t)a.M * a.K > (size_t)W_ * 64 * 32) {                       \
+                return hipErrorInvalidValue; /* fused rows: one chunk per wave */                \
+            } else if (fmt == XT_PACK5) {                                                        \
+                hipLaunchKernelGGL((gemv2_kernel<XT_PACK5, W_, NCW_, true>), dim3(ntiles), dim3(W_ * 64), stage, s, a); \
+            } else {                                                                             \
+                hipLaunchKernelGGL((gemv2_kernel<XT_PACK4, W_, NCW_, true>), dim3(ntiles), dim3(W_ * 64), stage, s, a); \
+            }                                                                                    \
+        } else if (fmt == XT_PACK5) {                                                            \
+            hipLaunchKernelGGL((gemv2_kernel<XT_PACK5, W_, NCW_, false>), dim3(ntiles), dim3(W_ * 64), 0, s, a); \
+        } else {                                                                                 \
+            hipLaunchKernelGGL((gemv2_kernel<XT_PACK4, W_, NCW_, false>), dim3(ntiles), dim3(W_ * 64), 0, s, a); \
+        }                                                                                        \
         return hipGetLastError();                                                                \
     }
     XT_GV2(4, 1) XT_GV2(8, 1) XT_GV2(10, 1) XT_GV2(16, 1) XT_GV2(16, 2) XT_GV2(16, 3)
@@ -904,8 +994,8 @@ static hipError_t launch_gemv2(int fmt, const MMArgs& a, int ntiles, hipStream_t
 
 hipError_t launch_gemv(int fmt, const MMArgs& a, int ntiles, int waves, hipStream_t s) {
     static const bool staged = getenv("XTERN_GEMV_STAGED") != nullptr;
-    if (!staged && (fmt == XT_PACK4 || fmt == XT_PACK5 || fmt == XT_XORSPARSE) && a.x == nullptr &&
-        a.nch <= 64)
+    if (!staged && (fmt == XT_PACK4 || fmt == XT_PACK5 || fmt == XT_XORSPARSE) &&
+        a.nch <= (a.x ? 16 : 64))
         return launch_gemv2(fmt == XT_PACK5 ? XT_PACK5 : XT_PACK4, a, ntiles, s);
     const int ch = fmt == XT_PACK5 ? 320 : 256;
     const size_t lds = (size_t)a.M * a.nch * ch;
