@@ -168,7 +168,8 @@ def gemv_m1(np, torch, xtern, rng, reps=400):
             "forward_f32_GBs": round(fwd_alg / (fwd_ms * 1e-3) / 1e9, 1),
             "alg_bytes_per_call": alg,
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
-                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None},
+                         "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
+                         "traffic": (recorded_traffic() or {}).get("gemv_c0")},
             "weight_copies": len(copies)}
 
 
@@ -285,11 +286,12 @@ def main():
     prod_ops = [2 * wl["M"] * s["N"] * s["K"] for s in wl["sets"]]
     ach = sum(prod_ops) / (sum(prod_ms) * 1e-3) / 1e12
     tr = recorded_traffic()
+    prod_tr = {k: v for k, v in (tr or {}).items() if k in ("gemm32s_up", "mm_down")}
     roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": INT8_PEAK_TOPS,
             "unit": "TFLOP/s", "frac": round(ach / INT8_PEAK_TOPS, 4),
-            "traffic": (sum(tr.values()) // len(tr)) if tr else None,
-            "traffic_per_launch": tr,
-            "kernel": "product launches (gemm_kernel up, mm_kernel down)",
+            "traffic": (sum(prod_tr.values()) // len(prod_tr)) if prod_tr else None,
+            "traffic_per_launch": prod_tr or None,
+            "kernel": "product launches (gemm32s_kernel up, mm_kernel down)",
             "us_per_launch": {s["name"]: round(m * 1e3, 3) for s, m in zip(wl["sets"], prod_ms)}}
 
     out = {"metric": "ternary GEMM int8 TOPS at M=128 (Pack4, BitNet-2B up+down)",
