@@ -10,6 +10,9 @@ totalling more than 2x the 256 MB MALL, so every step streams its weights
 from HBM.  `value` is whole-job int8 TOPS (2*M*N*K per matrix / step time).
 
 Also reported, from the same process:
+  configs      BASELINE configs[2..4]: Pack5 and XorSparse GEMV µs per call and
+               GB/s at their M values, and the 30-layer BitNet-2B decode linear
+               stack at M = 1, 8, 32
   roofline     the product kernel (mm_kernel) alone: algorithmic ops per
                launch / average launch duration from HIP events on the
                launch stream, against the 5.0 POP/s dense int8 MFMA peak
@@ -43,7 +46,8 @@ def log(*a):
 def tern_bytes(np, rng, N, K, fmt, p0=0.35):
     import xtern
     p = (1 - p0) / 2
-    t = rng.choice(np.array([-1, 0, 1], np.int8), size=(N, K), p=[p, p0, p])
+    u = rng.random((N, K), dtype=np.float32)
+    t = np.where(u < p, -1, np.where(u < p + p0, 0, 1)).astype(np.int8)
     if fmt == xtern.XT_PACK4:
         codes = np.where(t < 0, 0, np.where(t > 0, 2, 1)).astype(np.uint8)
         pad = (-K) % 4
@@ -171,6 +175,104 @@ def gemv_m1(np, torch, xtern, rng, reps=400):
                          "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4),
                          "traffic": (recorded_traffic() or {}).get("gemv_c0")},
             "weight_copies": len(copies)}
+
+
+def sparse_tern(np, rng, N, K):
+    """BASELINE configs[3] weights: ternary with a zero fraction drawn from
+    U[0.3, 0.7] per 64-block."""
+    nb = K // 64
+    zf = rng.uniform(0.3, 0.7, (N, nb, 1)).astype(np.float32)
+    u = rng.random((N, nb, 64), dtype=np.float32)
+    sign = np.where(rng.random((N, nb, 64), dtype=np.float32) < 0.5, -1, 1)
+    return np.where(u < zf, 0, sign).astype(np.int8).reshape(N, K)
+
+
+def time_product(np, torch, xtern, copies, K, N, M, rng, reps=200):
+    """Product (i8 q given) and forward (f32 x) µs per call over rotating
+    weight copies, HIP graphs timed with events on the replay stream."""
+    x = torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).cuda()
+    q, inv = xtern.quantize_i8(x)
+    y = torch.empty((M, N), dtype=torch.float32, device="cuda")
+    torch.cuda.synchronize()
+    n = len(copies)
+    gq = Graph(torch, lambda i: xtern.linear_q(copies[i], q, inv, out=y), n)
+    gf = Graph(torch, lambda i: xtern.linear_f32(copies[i], x, out=y), n)
+    return gq.time_ms(max(1, reps // n)) * 1e3, gf.time_ms(max(1, reps // n)) * 1e3
+
+
+def gemv_configs(np, torch, xtern, rng):
+    """BASELINE configs[2] (Pack5) and configs[3] (XorSparse): µs per call,
+    GB/s of algorithmic bytes (device weight bytes + M*K i8 + scales + f32
+    out) against the 8 TB/s HBM peak; weights rotate over > 2x the MALL."""
+    out = []
+    cases = [("c2_pack5", xtern.XT_PACK5, 3200, 8640, (1, 8)),
+             ("c2_pack5", xtern.XT_PACK5, 8640, 3200, (1, 8)),
+             ("c3_xorsparse", xtern.XT_XORSPARSE, 4096, 14336, (1, 4, 16)),
+             ("c3_xorsparse", xtern.XT_XORSPARSE, 14336, 4096, (1, 4, 16))]
+    for name, fmt, K, N, Ms in cases:
+        if fmt == xtern.XT_PACK5:
+            wb, _ = tern_bytes(np, rng, N, K, fmt, p0=0.4)
+            wbytes = N * ((K + 4) // 5)
+            blob = None
+        else:
+            t = sparse_tern(np, rng, N, K)
+            wb = np.frombuffer(xtern.encode_sparse_tensor(t, K, N)[0], np.uint8)
+            wbytes = N * (K // 64) * 16  # lane-order mask/sign form, as the reference's runtime
+            blob = int(wb.size)
+            del t
+        ws = np.full(N, 0.8, np.float32)
+        copies = make_copies(np, xtern, fmt, K, N, wb, ws, 2 * MALL_BYTES)
+        for M in Ms:
+            us_q, us_f = time_product(np, torch, xtern, copies, K, N, M, rng)
+            alg = wbytes + M * K + 4 * M + 4 * N + 4 * M * N
+            gbs = alg / (us_q * 1e-6) / 1e9
+            r = {"workload": name, "K": K, "N": N, "M": M, "us_product": round(us_q, 3),
+                 "us_forward_f32": round(us_f, 3), "GBs": round(gbs, 1),
+                 "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
+            if blob:
+                r["compact_blob_bytes"] = blob
+            out.append(r)
+        del copies
+        torch.cuda.empty_cache()
+    return out
+
+
+def stack_c4(np, torch, xtern, rng, Ms=(1, 8, 32), layers=30):
+    """the BitNet-2B decode-step linear stack, 30 layers
+    x {q, k, v, o, gate, up, down}, f32 activations, back to back (q/k/v and
+    gate/up share one quantised input, as fused_forward_qkv / _mlp).  Weights
+    are distinct device buffers (521 MB, > 2x the MALL); one HIP graph per
+    stack."""
+    shapes = {"q": (2560, 2560), "k": (2560, 640), "v": (2560, 640), "o": (2560, 2560),
+              "gate": (2560, 6912), "up": (2560, 6912), "down": (6912, 2560)}
+    proto = {n: tern_bytes(np, rng, N, K, xtern.XT_PACK4)[0] for n, (K, N) in shapes.items()}
+    W = [{n: xtern.DeviceWeights(xtern.XT_PACK4, K, N, proto[n], np.full(N, 0.9, np.float32))
+          for n, (K, N) in shapes.items()} for _ in range(layers)]
+    wbytes = layers * sum(N * K // 4 for K, N in shapes.values())
+    ops1 = layers * sum(2 * N * K for K, N in shapes.values())
+    res = []
+    for M in Ms:
+        xa = torch.from_numpy(rng.standard_normal((M, 2560)).astype(np.float32)).cuda()
+        xd = torch.from_numpy(rng.standard_normal((M, 6912)).astype(np.float32)).cuda()
+        ys = {n: torch.empty((M, N), dtype=torch.float32, device="cuda")
+              for n, (K, N) in shapes.items()}
+
+        def stack(_i):
+            for L in W:
+                xtern.linear_multi_f32([L["q"], L["k"], L["v"]], xa,
+                                       outs=[ys["q"], ys["k"], ys["v"]])
+                xtern.linear_f32(L["o"], xa, out=ys["o"])
+                xtern.linear_multi_f32([L["gate"], L["up"]], xa, outs=[ys["gate"], ys["up"]])
+                xtern.linear_f32(L["down"], xd, out=ys["down"])
+        g = Graph(torch, stack, 1)
+        us = g.time_ms(10) * 1e3
+        res.append({"workload": "c4_bitnet2b_stack", "M": M, "layers": layers,
+                    "us_per_stack": round(us, 1), "weight_GBs": round(wbytes / (us * 1e-6) / 1e9, 1),
+                    "hbm_frac": round(wbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                    "TOPS": round(ops1 * M / (us * 1e-6) / 1e12, 2)})
+    del W
+    torch.cuda.empty_cache()
+    return res
 
 
 def cpu_baseline(np, wl, budget_s=12.0):
@@ -303,6 +405,10 @@ def main():
     if not args.no_extra:
         log("c0 gemv ...")
         out["gemv_m1"] = gemv_m1(np, torch, xtern, rng)
+        log("c2 / c3 gemv ...")
+        out["configs"] = gemv_configs(np, torch, xtern, rng)
+        log("c4 stack ...")
+        out["configs"] += stack_c4(np, torch, xtern, rng)
     if not args.no_cpu:
         log("cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline(np, wl)

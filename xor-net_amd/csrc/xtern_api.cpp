@@ -271,12 +271,15 @@ int linear_q(const xt_weights* const* ws, int n, const int8_t* q, const float* i
 // separate quantiser launch).  Returns 1 when the case does not apply.
 int gemv_fused_quant(const xt_weights* const* ws, int n, const float* x, int64_t M,
                      float* const* ys, int mode, hipStream_t s) {
-    static const bool disabled = getenv("XTERN_NO_FUSED_QUANT") != nullptr;
+    const bool disabled = getenv("XTERN_NO_FUSED_QUANT") != nullptr;
     const int fmt = ws[0]->fmt;
     const int64_t K = ws[0]->K;
     const int nch = (int)ws[0]->nch;
-    if (disabled || M > 16 || M * K > xt::kGemvFusedQuantMax || (((uintptr_t)x) & 15) ||
-        (K & 3))
+    static const bool staged = getenv("XTERN_GEMV_STAGED") != nullptr;
+    const bool direct = !xt::is_int_format(fmt) && !staged;
+    const int64_t fmax = xt::kGemv2FusedQuantMax;
+    if (disabled || M > 16 || M * K > (direct ? fmax : xt::kGemvFusedQuantMax) ||
+        (((uintptr_t)x) & 15) || (K & 3))
         return 1;
     int ng_total = 0;
     for (int p = 0; p < n; ++p) ng_total += (int)((ws[p]->N + 15) / 16);
@@ -286,15 +289,15 @@ int gemv_fused_quant(const xt_weights* const* ws, int n, const float* x, int64_t
     int waves = 16;
     if (xt::is_int_format(fmt)) {
         waves = xt::int_gemv_waves(fmt, (int)M, nch);
+    } else if (fmt == XT_PACK5 && !staged) {
+        return 1;  // measured: Pack5 fused 9.8 us vs 8.8 quantiser + GEMV (C2, M = 1)
     } else if (fmt != XT_PACK5 && ng_total * 16 >= 8192) {
         return 1;
     }
     // Ternary tiles take the staging-free GEMV (one chunk per wave, so
     // K <= 16 chunks); Int8 / Int4 the staged one (one piece per thread).
-    static const bool staged = getenv("XTERN_GEMV_STAGED") != nullptr;
-    const bool direct = !xt::is_int_format(fmt) && !staged;
     const int segs = xt::chunk_cols(fmt) / 16;
-    if (direct ? nch > 16
+    if (direct ? (nch > 16 || M * K > xt::gemv2_fused_max(nch))
                : (!xt::gemv_fits(fmt, (int)M, nch, waves, xt::gemv_ncw(waves)) ||
                   M * nch * segs > (int64_t)waves * 64))
         return 1;

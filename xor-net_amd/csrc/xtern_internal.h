@@ -64,8 +64,11 @@ struct MMArgs {
     int mode;
 };
 // GEMV with the quantiser fused when M * K is at most this (every workgroup
-// re-reads the f32 rows, so only for small inputs).
+// re-reads the f32 rows, so only for small inputs).  For the staging-free
+// GEMV (Pack4 / XorSparse) the measured break-even is lower: fused 4.2 vs
+// 6.2 us at M = 1, K = 2560, but 7.6 vs 6.5 us at M = 4.
 constexpr int kGemvFusedQuantMax = 8192;
+constexpr int kGemv2FusedQuantMax = 4096;
 
 struct MMConfig {
     int mb, nb, waves, pf;  // tokens per WG = 16*mb, rows per WG = 16*nb
@@ -94,6 +97,8 @@ hipError_t launch_gemm32(const MMArgs& a, int ntiles, int splitk, hipStream_t s)
 // Decode GEMV (M <= 16): 16 output rows per workgroup, activations in LDS.
 hipError_t launch_gemv(int fmt, const MMArgs& a, int ntiles, int waves, hipStream_t s);
 int gemv_ncw(int waves);
+// Largest M * K the staging-free GEMV quantises itself for nch chunks (0: none).
+int gemv2_fused_max(int nch);
 int int_gemv_waves(int fmt, int mb, int nch);
 bool gemv_fits(int fmt, int M, int nch, int waves, int ncw);
 // MLP middle stage (xtern_kernels.hip): per row of gate/up, activation,

@@ -866,14 +866,23 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
             }
         }
         __syncthreads();  // tmax cleared
+        // (non-negative floats order as their bit patterns; NaN is ignored)
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const int f = threadIdx.x + u * NT;
-            if (f < n4) {
-                const int m = (4 * f) / K;
-                const float mx = fmaxf(fmaxf(fabsf(xv[u].x), fabsf(xv[u].y)),
-                                       fmaxf(fabsf(xv[u].z), fabsf(xv[u].w)));  // NaN ignored
-                atomicMax(&tmax[0][m], __float_as_uint(mx));  // non-negative floats order as ints
+            const int f0 = wave * 64 + u * NT;  // first piece of this wave
+            if (f0 >= n4) continue;
+            const float mx = f < n4 ? fmaxf(fmaxf(fabsf(xv[u].x), fabsf(xv[u].y)),
+                                            fmaxf(fabsf(xv[u].z), fabsf(xv[u].w)))
+                                    : 0.0f;
+            const int m0 = (4 * f0) / K, m1 = (4 * min(f0 + 63, n4 - 1)) / K;
+            if (m0 == m1) {  // the wave's pieces lie in one row: one atomic per wave
+                const int wm = wave_reduce_bits(__float_as_int(mx), [](int x, int y) {
+                    return __float_as_int(fmaxf(__int_as_float(x), __int_as_float(y)));
+                });
+                if (lane == 0) atomicMax(&tmax[0][m0], (unsigned)wm);
+            } else if (f < n4) {
+                atomicMax(&tmax[0][(4 * f) / K], __float_as_uint(mx));
             }
         }
         __syncthreads();
@@ -964,7 +973,16 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
     }
 }
 
-// The staging-free GEMV applies to ternary tiles with caller-quantised rows.
+// Waves of the staging-free GEMV for nch chunks, and the most f32 elements
+// (M * K) its fused quantiser takes: 8 float4 per thread.
+static int gemv2_waves(int nch) {
+    for (int w : {4, 8, 10, 16})
+        if (nch <= w) return w;
+    return 16;
+}
+int gemv2_fused_max(int nch) { return nch > 16 ? 0 : gemv2_waves(nch) * 64 * 32; }
+
+// The staging-free GEMV applies to ternary tiles (given or fused-quantised rows).
 static hipError_t launch_gemv2(int fmt, const MMArgs& a, int ntiles, hipStream_t s) {
     const int nch = a.nch;
     // fused rows: at most 8 float4 per thread, A stage of 1 KiB per k-step
@@ -1725,24 +1743,16 @@ MMConfig choose_config(int fmt, int M, int ntiles_nb1, int nch, bool have_rowsum
         }
     }
     if (M <= 16) {
-        // Measured (MI355X, rotating weights, M = 1..16): Pack5 decodes
-        // faster with K split over 8 waves of 16-row workgroups; many rows
-        // (N >= 8192) make the GEMV's 16-row workgroups overhead-bound, 32
-        // rows x 4 waves win (C3 4096 -> 14336: 5.9 vs 8.4 us at M = 1);
-        // long K and M >= 4 favour the K-split kernel too.  Short K with few
-        // rows stays on the GEMV.
+        // Measured (MI355X, rotating weights, M = 1..16): the staging-free
+        // GEMV wins or ties everywhere except many rows of Pack4 / XorSparse
+        // at moderate K (C3 4096 -> 14336: 6.0 vs 7.2 us at M = 1 on the
+        // 32-row, 4-wave K-split kernel).
         const int nrows = ntiles_nb1 * 16;
         const int kc = nch * (fmt == XT_PACK5 ? 320 : 256);
-        if (ntiles_nb1 > 0) {
-            if (fmt == XT_PACK5) return MMConfig{1, 1, 8, 2, 1};
-            if (nrows >= 8192 && kc <= 8192) return MMConfig{1, 2, 4, 4, 1};
-            if (kc > 4096) return MMConfig{1, 1, 8, 2, 1};
-            if (nrows >= 4096 && M >= 8) return MMConfig{1, 2, 4, 4, 1};
-            if (nrows >= 4096 && M >= 4) return MMConfig{1, 1, 8, 2, 1};
-        }
-        const int w = 16;
-        if (gemv_fits(fmt, M, nch, w, gemv_ncw(w))) {
-            c = MMConfig{1, 1, w, 1, 1};
+        if (ntiles_nb1 > 0 && fmt != XT_PACK5 && nrows >= 8192 && kc <= 8192)
+            return MMConfig{1, 2, 4, 4, 1};
+        if (nch <= 64 || gemv_fits(fmt, M, nch, 16, gemv_ncw(16))) {
+            c = MMConfig{1, 1, 16, 1, 1};
             c.kind = 2;
             return c;
         }

@@ -656,11 +656,12 @@ def _multi(ws, ys):
     return harr, yarr
 
 
-def linear_multi_f32(ws, x, mode=XT_QUANT_AVX512, stream=None):
+def linear_multi_f32(ws, x, mode=XT_QUANT_AVX512, stream=None, outs=None):
     torch = _torch()
     x2 = x.reshape(-1, x.shape[-1])
     M = x2.shape[0]
-    ys = [torch.empty((M, w.out_dim), dtype=torch.float32, device=x.device) for w in ws]
+    ys = outs if outs is not None else [torch.empty((M, w.out_dim), dtype=torch.float32,
+                                                    device=x.device) for w in ws]
     harr, yarr = _multi(ws, ys)
     _check(_lib.xt_ternary_linear_multi_f32(harr, len(ws), _dev_ptr(x2, torch.float32, "x"), M,
                                             yarr, mode, _stream_ptr(stream)))
