@@ -64,11 +64,10 @@ struct MMArgs {
     int mode;
 };
 // GEMV with the quantiser fused when M * K is at most this (every workgroup
-// re-reads the f32 rows, so only for small inputs).  For the staging-free
-// GEMV (Pack4 / XorSparse) the measured break-even is lower: fused 4.2 vs
-// 6.2 us at M = 1, K = 2560, but 7.6 vs 6.5 us at M = 4.
+// re-reads the f32 rows, so only for small inputs).  The staging-free GEMV
+// (Pack4 / XorSparse) fuses one row of up to this many columns.
 constexpr int kGemvFusedQuantMax = 8192;
-constexpr int kGemv2FusedQuantMax = 4096;
+constexpr int kGemv2FusedQuantMax = 8192;
 
 struct MMConfig {
     int mb, nb, waves, pf;  // tokens per WG = 16*mb, rows per WG = 16*nb

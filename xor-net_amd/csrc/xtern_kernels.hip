@@ -980,7 +980,7 @@ static int gemv2_waves(int nch) {
         if (nch <= w) return w;
     return 16;
 }
-int gemv2_fused_max(int nch) { return nch > 16 ? 0 : gemv2_waves(nch) * 64 * 32; }
+int gemv2_fused_max(int nch) { return nch > 64 ? 0 : gemv2_waves(nch) * 64 * 32; }
 
 // The staging-free GEMV applies to ternary tiles (given or fused-quantised rows).
 static hipError_t launch_gemv2(int fmt, const MMArgs& a, int ntiles, hipStream_t s) {
@@ -990,8 +990,8 @@ static hipError_t launch_gemv2(int fmt, const MMArgs& a, int ntiles, hipStream_t
 #define XT_GV2(W_, NCW_)                                                                         \
     if (nch <= W_ * NCW_) {                                                                      \
         if (a.x) {                                                                               \
-            if (NCW_ != 1 || (size_t)a.M * a.K > (size_t)W_ * 64 * 32) {                       \
-                return hipErrorInvalidValue; /* fused rows: one chunk per wave */                \
+            if ((size_t)a.M * a.K > (size_t)W_ * 64 * 32) {                                   \
+                return hipErrorInvalidValue; /* fused rows: 8 float4 per thread */               \
             } else if (fmt == XT_PACK5) {                                                        \
                 hipLaunchKernelGGL((gemv2_kernel<XT_PACK5, W_, NCW_, true>), dim3(ntiles), dim3(W_ * 64), stage, s, a); \
             } else {                                                                             \
@@ -1013,7 +1013,7 @@ static hipError_t launch_gemv2(int fmt, const MMArgs& a, int ntiles, hipStream_t
 hipError_t launch_gemv(int fmt, const MMArgs& a, int ntiles, int waves, hipStream_t s) {
     static const bool staged = getenv("XTERN_GEMV_STAGED") != nullptr;
     if (!staged && (fmt == XT_PACK4 || fmt == XT_PACK5 || fmt == XT_XORSPARSE) &&
-        a.nch <= (a.x ? 16 : 64))
+        a.nch <= 64)
         return launch_gemv2(fmt == XT_PACK5 ? XT_PACK5 : XT_PACK4, a, ntiles, s);
     const int ch = fmt == XT_PACK5 ? 320 : 256;
     const size_t lds = (size_t)a.M * a.nch * ch;
