@@ -190,6 +190,7 @@ int run_product(const xt_weights* const* ws, int n, const int8_t* q, int ldq, co
     const int64_t gy = (M + 16 * cfg.mb - 1) / (16 * cfg.mb);
     if (gy > 65535) return fail(XT_ERR_UNSUPPORTED, "M too large for one launch");
     if (cfg.kind == 2) {
+        a.rg = cfg.nb;
         hipError_t e = xt::launch_gemv(fmt, a, tiles, cfg.waves, s);
         if (e != hipSuccess) return hip_fail(e, "ternary GEMV launch");
         return XT_OK;
@@ -307,19 +308,21 @@ int gemv_fused_quant(const xt_weights* const* ws, int n, const float* x, int64_t
     xt::MMArgs a;
     memset(&a, 0, sizeof a);
     int tiles = 0;
+    const int rg = xt::gemv_row_groups(fmt, nch, ng_total);
     for (int p = 0; p < n; ++p) {
         a.proj[p].tiles = ws[p]->tiles;
         a.proj[p].ws = ws[p]->ws;
         a.proj[p].y = ys[p];
         a.proj[p].N = (int)ws[p]->N;
         a.proj[p].tile0 = tiles;
-        tiles += (int)((ws[p]->N + 15) / 16);
+        tiles += (int)((ws[p]->N + 15) / 16 + rg - 1) / rg;
     }
     a.nproj = n;
     a.M = (int)M;
     a.nch = nch;
     a.cps = nch;
     a.x = x;
+    a.rg = rg;
     a.ldx = K;
     a.K = (int)K;
     a.mode = mode;

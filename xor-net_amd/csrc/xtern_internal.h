@@ -62,6 +62,7 @@ struct MMArgs {
     int64_t ldx;
     int K;
     int mode;
+    int rg;                 // decode GEMV: 16-row groups per workgroup (0 or 1: one)
 };
 // GEMV with the quantiser fused when M * K is at most this (every workgroup
 // re-reads the f32 rows, so only for small inputs).  The staging-free GEMV
@@ -98,6 +99,9 @@ hipError_t launch_gemv(int fmt, const MMArgs& a, int ntiles, int waves, hipStrea
 int gemv_ncw(int waves);
 // Largest M * K the staging-free GEMV quantises itself for nch chunks (0: none).
 int gemv2_fused_max(int nch);
+// 16-row groups per workgroup of the decode GEMV that launch_gemv runs for
+// this format and K (its ntiles count workgroups of that many groups).
+int gemv_row_groups(int fmt, int nch, int ngroups);
 int int_gemv_waves(int fmt, int mb, int nch);
 bool gemv_fits(int fmt, int M, int nch, int waves, int ncw);
 // MLP middle stage (xtern_kernels.hip): per row of gate/up, activation,

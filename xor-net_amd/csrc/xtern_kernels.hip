@@ -795,11 +795,11 @@ __device__ __forceinline__ int signed_codes(int c) {
 // as quantize_kernel): each lane reads its pieces as f32, the per-token
 // absmax goes through the waves' shuffles and LDS (one barrier), then each
 // lane quantises its own pieces.  No separate quantiser launch.
-template <int FMT, int WAVES, int NCW, bool FUSED>
+template <int FMT, int WAVES, int NCW, bool FUSED, int RG>
 __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
     constexpr int STEPS = (FMT == XT_PACK5) ? 5 : 4;
     constexpr int CH = STEPS * 64;
-    __shared__ v4i red[WAVES][64];
+    __shared__ v4i red[WAVES][RG][64];
     __shared__ unsigned tmax[WAVES][16];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -814,11 +814,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
     const ProjBounds pb = proj_bounds();
     __builtin_amdgcn_sched_barrier(0);  // one round of argument loads
     const ProjView pv = select_proj(pb, bx);
-    const int G = bx - pv.tile0;
     const int N = pv.N;
+    const int NG = (N + 15) >> 4;
+    const int G0 = (bx - pv.tile0) * RG;  // first row group of the workgroup
 
-    // epilogue operands (wave 0 finishes: tokens 4g + r, output row o)
-    const int o = G * 16 + j;
+    // epilogue operands (wave w < RG finishes row group G0 + w: tokens
+    // 4g + r, output row o)
+    const int o = (G0 + min(wave, RG - 1)) * 16 + j;
     const float wscale = pv.ws[min(o, N - 1)];
     float invr[4];
     if constexpr (!FUSED) {
@@ -826,15 +828,19 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
         for (int r = 0; r < 4; ++r) invr[r] = inv[min(4 * g + r, M - 1)];
     }
 
-    const uint8_t* wsrc = pv.tiles + ((size_t)G * nch * 64 + lane) * 16;
-    v4i wv[NCW];
+    const uint8_t* wsrc[RG];
+#pragma unroll
+    for (int r = 0; r < RG; ++r)
+        wsrc[r] = pv.tiles + ((size_t)min(G0 + r, NG - 1) * nch * 64 + lane) * 16;
+    v4i wv[NCW][RG];
     v4i av[NCW][STEPS];
     if constexpr (!FUSED) {
         const int8_t* arow = q + (size_t)min(j, M - 1) * ldq + 16 * g;
 #pragma unroll
         for (int t = 0; t < NCW; ++t) {
             const int c = min(wave + t * WAVES, nch - 1);
-            wv[t] = ld_stream(wsrc + (size_t)c * kTileBytes);
+#pragma unroll
+            for (int r = 0; r < RG; ++r) wv[t][r] = ld_stream(wsrc[r] + (size_t)c * kTileBytes);
 #pragma unroll
             for (int s = 0; s < STEPS; ++s) av[t][s] = ld_cached(arow + (size_t)c * CH + s * 64);
         }
@@ -854,7 +860,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
 #pragma unroll
         for (int t = 0; t < NCW; ++t) {
             const int c = min(wave + t * WAVES, nch - 1);
-            wv[t] = ld_stream(wsrc + (size_t)c * kTileBytes);
+#pragma unroll
+            for (int r = 0; r < RG; ++r) wv[t][r] = ld_stream(wsrc[r] + (size_t)c * kTileBytes);
         }
         float4 xv[8];
 #pragma unroll
@@ -918,51 +925,59 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
             invr[r] = (x2 > 0.0f) ? __fdiv_rn(x2, 127.0f) : 1.0f;
         }
     }
-    v4i acc[STEPS];
+    v4i acc[RG][STEPS];
 #pragma unroll
-    for (int s = 0; s < STEPS; ++s) acc[s] = v4i{0, 0, 0, 0};
+    for (int r = 0; r < RG; ++r)
+#pragma unroll
+        for (int s = 0; s < STEPS; ++s) acc[r][s] = v4i{0, 0, 0, 0};
 #pragma unroll
     for (int t = 0; t < NCW; ++t) {
         const bool live = wave + t * WAVES < nch;
-        if constexpr (FMT == XT_PACK5) {
-            int E[4], O[4];
 #pragma unroll
-            for (int d = 0; d < 4; ++d) {
-                E[d] = wv[t][d] & 0x00ff00ff;
-                O[d] = ((unsigned)wv[t][d] >> 8) & 0x00ff00ff;
-            }
-#pragma unroll
-            for (int s = 0; s < STEPS; ++s) {
-                v4i b;
+        for (int r = 0; r < RG; ++r) {
+            if constexpr (FMT == XT_PACK5) {
+                int E[4], O[4];
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
-                    const int pE = E[d] * 3, pO = O[d] * 3;
-                    b[d] = signed_codes((int)__builtin_amdgcn_perm((unsigned)pO, (unsigned)pE, 0x07030501u));
-                    E[d] = pE & 0x00ff00ff;
-                    O[d] = pO & 0x00ff00ff;
+                    E[d] = wv[t][r][d] & 0x00ff00ff;
+                    O[d] = ((unsigned)wv[t][r][d] >> 8) & 0x00ff00ff;
                 }
-                const v4i x = (live && j < M) ? av[t][s] : v4i{0, 0, 0, 0};
-                acc[s] = mfma(x, b, acc[s]);
-            }
-        } else {
 #pragma unroll
-            for (int s = 0; s < STEPS; ++s) {
-                v4i b = decode4(wv[t][s]);
+                for (int s = 0; s < STEPS; ++s) {
+                    v4i b;
 #pragma unroll
-                for (int d = 0; d < 4; ++d) b[d] = signed_codes(b[d]);
-                const v4i x = (live && j < M) ? av[t][s] : v4i{0, 0, 0, 0};
-                acc[s] = mfma(x, b, acc[s]);
+                    for (int d = 0; d < 4; ++d) {
+                        const int pE = E[d] * 3, pO = O[d] * 3;
+                        b[d] = signed_codes((int)__builtin_amdgcn_perm((unsigned)pO, (unsigned)pE, 0x07030501u));
+                        E[d] = pE & 0x00ff00ff;
+                        O[d] = pO & 0x00ff00ff;
+                    }
+                    const v4i x = (live && j < M) ? av[t][s] : v4i{0, 0, 0, 0};
+                    acc[r][s] = mfma(x, b, acc[r][s]);
+                }
+            } else {
+#pragma unroll
+                for (int s = 0; s < STEPS; ++s) {
+                    v4i b = decode4(wv[t][r][s]);
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) b[d] = signed_codes(b[d]);
+                    const v4i x = (live && j < M) ? av[t][s] : v4i{0, 0, 0, 0};
+                    acc[r][s] = mfma(x, b, acc[r][s]);
+                }
             }
         }
     }
 #pragma unroll
-    for (int s = 1; s < STEPS; ++s) acc[0] += acc[s];
-    red[wave][lane] = acc[0];
-    __syncthreads();
-    if (wave != 0 || o >= N) return;
-    v4i sum = red[0][lane];  // (tmax is not reused: no barrier needed before red)
+    for (int r = 0; r < RG; ++r) {
 #pragma unroll
-    for (int w = 1; w < WAVES; ++w) sum += red[w][lane];
+        for (int s = 1; s < STEPS; ++s) acc[r][0] += acc[r][s];
+        red[wave][r][lane] = acc[r][0];
+    }
+    __syncthreads();
+    if (wave >= RG || o >= N) return;
+    v4i sum = red[0][wave][lane];
+#pragma unroll
+    for (int w = 1; w < WAVES; ++w) sum += red[w][wave][lane];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int i = 4 * g + r;
@@ -973,6 +988,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
     }
 }
 
+// Row groups per workgroup of the staging-free GEMV.  Two groups (half the
+// workgroups, one activation load for both) win only when there are many
+// rows: C0 (6912 rows, K = 2560) 3.8 -> 3.5 us, but 2560 rows 2.9 -> 3.2 us
+// and K = 14336 6.7 -> 8.5 us; Pack5 (3200 -> 8640) 5.4 -> 6.1 us.
+static int gemv2_rg_for(int fmt, int nch, int ngroups) {
+    return (fmt != XT_PACK5 && ngroups >= 400 && nch <= 16) ? 2 : 1;
+}
+
 // Waves of the staging-free GEMV for nch chunks, and the most f32 elements
 // (M * K) its fused quantiser takes: 8 float4 per thread.
 static int gemv2_waves(int nch) {
@@ -980,27 +1003,40 @@ static int gemv2_waves(int nch) {
         if (nch <= w) return w;
     return 16;
 }
-int gemv2_fused_max(int nch) { return nch > 64 ? 0 : gemv2_waves(nch) * 64 * 32; }
+// LDS of the fused GEMV: the A stage (1 KiB per k-step) plus the static
+// cross-wave sums and maxima; it must fit the 160 KiB of a CU.
+static size_t gemv2_fused_lds(int nch, int steps, int rg) {
+    const int w = gemv2_waves(nch);
+    return (size_t)nch * steps * 1024 + (size_t)w * rg * 64 * 16 + (size_t)w * 16 * 4;
+}
+constexpr size_t kLdsBytes = 160 * 1024;
+int gemv2_fused_max(int nch) {
+    if (nch > 64 || gemv2_fused_lds(nch, 4, 2) > kLdsBytes) return 0;
+    return gemv2_waves(nch) * 64 * 32;
+}
 
 // The staging-free GEMV applies to ternary tiles (given or fused-quantised rows).
-static hipError_t launch_gemv2(int fmt, const MMArgs& a, int ntiles, hipStream_t s) {
+template <int RG>
+static hipError_t launch_gemv2_rg(int fmt, const MMArgs& a, int ntiles, hipStream_t s) {
     const int nch = a.nch;
     // fused rows: at most 8 float4 per thread, A stage of 1 KiB per k-step
-    const size_t stage = (size_t)nch * (fmt == XT_PACK5 ? 5 : 4) * 1024;
+    const int steps = fmt == XT_PACK5 ? 5 : 4;
+    const size_t stage = (size_t)nch * steps * 1024;
+    if (a.x && gemv2_fused_lds(nch, steps, RG) > kLdsBytes) return hipErrorInvalidValue;
 #define XT_GV2(W_, NCW_)                                                                         \
     if (nch <= W_ * NCW_) {                                                                      \
         if (a.x) {                                                                               \
             if ((size_t)a.M * a.K > (size_t)W_ * 64 * 32) {                                   \
                 return hipErrorInvalidValue; /* fused rows: 8 float4 per thread */               \
             } else if (fmt == XT_PACK5) {                                                        \
-                hipLaunchKernelGGL((gemv2_kernel<XT_PACK5, W_, NCW_, true>), dim3(ntiles), dim3(W_ * 64), stage, s, a); \
+                hipLaunchKernelGGL((gemv2_kernel<XT_PACK5, W_, NCW_, true, RG>), dim3(ntiles), dim3(W_ * 64), stage, s, a); \
             } else {                                                                             \
-                hipLaunchKernelGGL((gemv2_kernel<XT_PACK4, W_, NCW_, true>), dim3(ntiles), dim3(W_ * 64), stage, s, a); \
+                hipLaunchKernelGGL((gemv2_kernel<XT_PACK4, W_, NCW_, true, RG>), dim3(ntiles), dim3(W_ * 64), stage, s, a); \
             }                                                                                    \
         } else if (fmt == XT_PACK5) {                                                            \
-            hipLaunchKernelGGL((gemv2_kernel<XT_PACK5, W_, NCW_, false>), dim3(ntiles), dim3(W_ * 64), 0, s, a); \
+            hipLaunchKernelGGL((gemv2_kernel<XT_PACK5, W_, NCW_, false, RG>), dim3(ntiles), dim3(W_ * 64), 0, s, a); \
         } else {                                                                                 \
-            hipLaunchKernelGGL((gemv2_kernel<XT_PACK4, W_, NCW_, false>), dim3(ntiles), dim3(W_ * 64), 0, s, a); \
+            hipLaunchKernelGGL((gemv2_kernel<XT_PACK4, W_, NCW_, false, RG>), dim3(ntiles), dim3(W_ * 64), 0, s, a); \
         }                                                                                        \
         return hipGetLastError();                                                                \
     }
@@ -1010,10 +1046,20 @@ static hipError_t launch_gemv2(int fmt, const MMArgs& a, int ntiles, hipStream_t
     return hipErrorInvalidValue;
 }
 
-hipError_t launch_gemv(int fmt, const MMArgs& a, int ntiles, int waves, hipStream_t s) {
+static hipError_t launch_gemv2(int fmt, const MMArgs& a, int ntiles, hipStream_t s) {
+    return a.rg == 2 ? launch_gemv2_rg<2>(fmt, a, ntiles, s) : launch_gemv2_rg<1>(fmt, a, ntiles, s);
+}
+
+static bool use_gemv2(int fmt, int nch) {
     static const bool staged = getenv("XTERN_GEMV_STAGED") != nullptr;
-    if (!staged && (fmt == XT_PACK4 || fmt == XT_PACK5 || fmt == XT_XORSPARSE) &&
-        a.nch <= 64)
+    return !staged && (fmt == XT_PACK4 || fmt == XT_PACK5 || fmt == XT_XORSPARSE) && nch <= 64;
+}
+int gemv_row_groups(int fmt, int nch, int ngroups) {
+    return use_gemv2(fmt, nch) ? gemv2_rg_for(fmt, nch, ngroups) : 1;
+}
+
+hipError_t launch_gemv(int fmt, const MMArgs& a, int ntiles, int waves, hipStream_t s) {
+    if (use_gemv2(fmt, a.nch))
         return launch_gemv2(fmt == XT_PACK5 ? XT_PACK5 : XT_PACK4, a, ntiles, s);
     const int ch = fmt == XT_PACK5 ? 320 : 256;
     const size_t lds = (size_t)a.M * a.nch * ch;
@@ -1732,8 +1778,10 @@ int int_gemv_waves(int fmt, int mb, int nch) {
 MMConfig choose_config(int fmt, int M, int ntiles_nb1, int nch, bool have_rowsum) {
     MMConfig c;
     if (env_config(&c)) {
-        if (c.kind == 2 && M <= 16 && gemv_fits(fmt, M, nch, c.waves, gemv_ncw(c.waves)))
+        if (c.kind == 2 && M <= 16 && gemv_fits(fmt, M, nch, c.waves, gemv_ncw(c.waves))) {
+            c.nb = gemv_row_groups(fmt, nch, ntiles_nb1);
             return c;
+        }
         if (c.kind == 3 && M > 16 && have_rowsum && fmt == XT_PACK4 &&
             (nch + c.splitk - 1) / c.splitk <= gemm32_ncmax())
             return c;
@@ -1752,7 +1800,7 @@ MMConfig choose_config(int fmt, int M, int ntiles_nb1, int nch, bool have_rowsum
         if (ntiles_nb1 > 0 && fmt != XT_PACK5 && nrows >= 8192 && kc <= 8192)
             return MMConfig{1, 2, 4, 4, 1};
         if (nch <= 64 || gemv_fits(fmt, M, nch, 16, gemv_ncw(16))) {
-            c = MMConfig{1, 1, 16, 1, 1};
+            c = MMConfig{1, gemv_row_groups(fmt, nch, ntiles_nb1), 16, 1, 1};
             c.kind = 2;
             return c;
         }
