@@ -130,16 +130,16 @@ class Graph:
 
 
 def product_only(np, torch, xtern, wl, reps):
-    """Average duration of one product launch (mm_kernel) per matrix: a HIP
-    graph of back-to-back linear_q_rowsum launches over the rotating copies,
-    timed with events on the graph's stream."""
+    """Average duration of one product launch per matrix: a HIP graph of
+    back-to-back linear_q (forward_with_quantized) launches over the rotating
+    copies, timed with events on the graph's stream."""
     out = []
     for s in wl["sets"]:
-        q, inv, rs = xtern.quantize_i8_rowsum(s["x"])
+        q, inv = xtern.quantize_i8(s["x"])
         torch.cuda.synchronize()
         n = len(s["copies"])
-        g = Graph(torch, lambda i, s=s, q=q, inv=inv, rs=rs:
-                  xtern.linear_q_rowsum(s["copies"][i], q, inv, rs, out=s["y"]), n)
+        g = Graph(torch, lambda i, s=s, q=q, inv=inv:
+                  xtern.linear_q(s["copies"][i], q, inv, out=s["y"]), n)
         out.append(g.time_ms(max(1, reps // n)))
     return out
 

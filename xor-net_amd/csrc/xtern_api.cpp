@@ -227,6 +227,16 @@ int run_product(const xt_weights* const* ws, int n, const int8_t* q, int ldq, co
     return XT_OK;
 }
 
+// Whether the product for M rows needs the quantiser's activation row sums:
+// only the Pack5 prefill GEMM multiplies codes with a caller row sum; the
+// other kernels decode signed weights or sum the rows themselves (measured:
+// computing them for the long-K kernel costs more in the quantiser than the
+// kernel's own extra MFMA per k-step saves).
+bool wants_rowsum(const xt_weights* w, int64_t M) {
+    if (xt::is_int_format(w->fmt)) return false;
+    return xt::choose_config(w->fmt, (int)M, 0, (int)w->nch, true).kind == 1;
+}
+
 int check_group(const xt_weights* const* ws, int n, const void* in, int64_t M, float* const* ys) {
     if (!ws || n < 1 || n > 4) return fail(XT_ERR_INVALID, "need 1..4 weight handles");
     for (int p = 0; p < n; ++p) {
@@ -249,8 +259,7 @@ int linear_q(const xt_weights* const* ws, int n, const int8_t* q, const float* i
     if (M == 0) return XT_OK;
     const int64_t K = ws[0]->K;
     const int64_t kpad = ws[0]->nch * xt::chunk_cols(ws[0]->fmt);
-    const xt::MMConfig probe = xt::choose_config(ws[0]->fmt, (int)M, 0, 0, true);
-    const bool need_rowsum = (probe.kind == 1 || probe.kind == 3) && !xt::is_int_format(ws[0]->fmt);
+    const bool need_rowsum = wants_rowsum(ws[0], M);
     const bool direct = (kpad == K) && ((((uintptr_t)q) & 15) == 0);
     if (direct && user_rowsum)
         return run_product(ws, n, q, (int)K, inv, user_rowsum, M, ys, acc, s);
@@ -347,7 +356,9 @@ int linear_f32(const xt_weights* const* ws, int n, const float* x, int64_t M, fl
     if (int rc = workspace(s, qbytes + 2 * fbytes, &wsp)) return rc;
     int8_t* q = static_cast<int8_t*>(wsp);
     float* inv = reinterpret_cast<float*>(static_cast<char*>(wsp) + qbytes);
-    int32_t* rowsum = reinterpret_cast<int32_t*>(static_cast<char*>(wsp) + qbytes + fbytes);
+    int32_t* rowsum = wants_rowsum(ws[0], M)
+                          ? reinterpret_cast<int32_t*>(static_cast<char*>(wsp) + qbytes + fbytes)
+                          : nullptr;
     hipError_t e = xt::launch_quantize(x, K, (int)M, (int)K, q, (int)kpad, inv, rowsum, mode, s);
     if (e != hipSuccess) return hip_fail(e, "quantize launch");
     return run_product(ws, n, q, (int)kpad, inv, rowsum, M, ys, nullptr, s);

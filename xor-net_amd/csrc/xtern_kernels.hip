@@ -207,7 +207,7 @@ __global__ __launch_bounds__(NT) void quantize_reg_kernel(const float* __restric
                 ((uint32_t)(b[2] & 255) << 16) | ((uint32_t)(b[3] & 255) << 24);
     }
     for (int i = K4 + threadIdx.x; i < (ldq >> 2); i += NT) q4[i] = 0u;  // padding
-    sum = block_reduce(sum, AddOp(), sm_i);
+    if (rowsum) sum = block_reduce(sum, AddOp(), sm_i);  // uniform: skipped when unused
     if (threadIdx.x == 0) {
         inv[m] = invs;
         if (rowsum) rowsum[m] = sum;
@@ -1346,7 +1346,7 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const MMArgs a, int ns
     const size_t plane_sz = (size_t)a.M * a.ldp;
     int tot = 0;
     for (int z = 0; z < nsplit; ++z) tot += a.part[z * plane_sz + (size_t)i * a.ldp + col];
-    const int d = tot - a.rowsum[i];
+    const int d = tot - (a.rowsum ? a.rowsum[i] : 0);  // signed-decode kernels pass none
     pr.y[(size_t)i * pr.N + o] = __fmul_rn(__fmul_rn((float)d, a.inv[i]), pr.ws[o]);
     if (pr.acc) pr.acc[(size_t)i * pr.N + o] = d;
 }
@@ -1489,7 +1489,6 @@ __global__ __launch_bounds__(768) void gemm32s_kernel(const MMArgs a) {
     const int mbase = by * 32;
     const int cbeg = bz * cps;
     const int nc = min(nch - cbeg, cps);  // chunks of this slice, 1..NCMAX
-    const int gblk = (bx - pv.tile0) * 8;  // first row group of the block
 
     // The gy token blocks that share the weights start at different quarters
     // of the slice (different HBM lines in flight; integer sums do not depend
@@ -1547,13 +1546,8 @@ __global__ __launch_bounds__(768) void gemm32s_kernel(const MMArgs a) {
     const int sc4 = (threadIdx.x & 31) * 4;
     const int ob = (bx - pv.tile0) * 128;
     float sinv[2];
-    int srs[2];
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-        const int i = min(mbase + srow + 16 * u, M - 1);
-        sinv[u] = a.inv[i];
-        srs[u] = split ? 0 : a.rowsum[i];
-    }
+    for (int u = 0; u < 2; ++u) sinv[u] = a.inv[min(mbase + srow + 16 * u, M - 1)];
     float sws[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) sws[e] = pv.ws[min(ob + sc4 + e, N - 1)];
@@ -1592,9 +1586,15 @@ __global__ __launch_bounds__(768) void gemm32s_kernel(const MMArgs a) {
     for (int c = 0; c < NCMAX; ++c) {
         if (c + DW < NCMAX)
             wv[c + DW] = *reinterpret_cast<const v4i*>(wsrc + (size_t)chunk_at(c + DW) * kTileBytes);
-        const v4i bv = (c < nc) ? wv[c] : v4i{0, 0, 0, 0};
+        // chunks past the slice: code 1 everywhere, i.e. weight 0
+        const v4i bv = (c < nc) ? wv[c] : v4i{0x55555555, 0x55555555, 0x55555555, 0x55555555};
 #pragma unroll
-        for (int s = 0; s < 4; ++s) acc[s] = mfma32(acur[s], decode4(bv[s]), acc[s]);
+        for (int s = 0; s < 4; ++s) {
+            v4i b = decode4(bv[s]);
+#pragma unroll
+            for (int d = 0; d < 4; ++d) b[d] = signed_codes(b[d]);
+            acc[s] = mfma32(acur[s], b, acc[s]);
+        }
         if (c + 1 < NCMAX) {
             __syncthreads();  // chunk c + 1 has landed
             read_a(c + 1, acur);
@@ -1649,7 +1649,7 @@ __global__ __launch_bounds__(768) void gemm32s_kernel(const MMArgs a) {
         v4i dv;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-            dv[e] = d4[e] - srs[u];
+            dv[e] = d4[e];
             // layers.rs:294 — (dot as f32 * inv_scale) * w_scale.
             yv[e] = __fmul_rn(__fmul_rn((float)dv[e], sinv[u]), sws[e]);
         }
@@ -1782,7 +1782,7 @@ MMConfig choose_config(int fmt, int M, int ntiles_nb1, int nch, bool have_rowsum
             c.nb = gemv_row_groups(fmt, nch, ntiles_nb1);
             return c;
         }
-        if (c.kind == 3 && M > 16 && have_rowsum && fmt == XT_PACK4 &&
+        if (c.kind == 3 && M > 16 && fmt == XT_PACK4 &&
             (nch + c.splitk - 1) / c.splitk <= gemm32_ncmax())
             return c;
         if (c.kind == 0 && shape_known(c, !have_rowsum)) {
@@ -1810,7 +1810,7 @@ MMConfig choose_config(int fmt, int M, int ntiles_nb1, int nch, bool have_rowsum
     // fits its LDS stage (C1 up: 10.9 -> 7.8 us).  Longer K stays on the
     // K-split kernel below: splitting it over workgroups plus a reduction
     // launch measured slower (C1 down: 12.6 vs 8.5 us).
-    if (have_rowsum && fmt == XT_PACK4 && nch <= gemm32_ncmax()) {
+    if (fmt == XT_PACK4 && nch <= gemm32_ncmax()) {
         c = MMConfig{2, 8, 8, 1, 1};
         c.kind = 3;
         return c;
