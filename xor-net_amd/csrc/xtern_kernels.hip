@@ -857,12 +857,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
         constexpr int NT = WAVES * 64;
         const int n4 = (M * K) >> 2;
         if (threadIdx.x < 16) tmax[0][threadIdx.x] = 0u;
-#pragma unroll
-        for (int t = 0; t < NCW; ++t) {
-            const int c = min(wave + t * WAVES, nch - 1);
-#pragma unroll
-            for (int r = 0; r < RG; ++r) wv[t][r] = ld_stream(wsrc[r] + (size_t)c * kTileBytes);
-        }
+        // The f32 pieces are loaded before the weights: loads return in
+        // order, so the quantiser then waits for its own loads only and runs
+        // while the weights are in flight.
         float4 xv[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
@@ -872,6 +869,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
                 xv[u] = *reinterpret_cast<const float4*>(a.x + (size_t)m * a.ldx + col);
             }
         }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < NCW; ++t) {
+            const int c = min(wave + t * WAVES, nch - 1);
+#pragma unroll
+            for (int r = 0; r < RG; ++r) wv[t][r] = ld_stream(wsrc[r] + (size_t)c * kTileBytes);
+        }
+        __builtin_amdgcn_sched_barrier(0);
         __syncthreads();  // tmax cleared
         // (non-negative floats order as their bit patterns; NaN is ignored)
 #pragma unroll
