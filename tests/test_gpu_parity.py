@@ -455,3 +455,19 @@ def test_small_forward_quantiser_ties(fmt, mode, M, K):
     ys = xtern.linear_multi_f32([w, w2], torch.from_numpy(x).to(DEV), mode=mode)
     check_y(ys[0].cpu().numpy(), y)
     check_y(ys[1].cpu().numpy(), oracle_q(fmt, t, q, inv, ws * np.float32(2))[0])
+
+
+@pytest.mark.parametrize("K,N,M", [(2560, 3840, 32), (2560, 2560, 32), (2560, 6912, 24),
+                                   (2560, 13824, 32), (6912, 2560, 32)])
+def test_small_prefill_default_config(K, N, M):
+    """Short prefills of the BitNet-2B shapes (the decode-stack config at
+    M = 24 / 32), whichever kernel the default choice takes, are exact."""
+    log(f"small prefill K={K} N={N} M={M}")
+    rng = np.random.default_rng(K + N + M)
+    t = tern(rng, N, K)
+    w = xtern.DeviceWeights(xtern.XT_PACK4, K, N, make_bytes(t, xtern.XT_PACK4),
+                            np.ones(N, np.float32))
+    q = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    _, acc = xtern.linear_q(w, torch.from_numpy(q).to(DEV), torch.ones(M, device=DEV),
+                            acc=True)
+    assert np.array_equal(acc.cpu().numpy(), exact_acc(t, q))

@@ -290,8 +290,9 @@ int gemv_fused_quant(const xt_weights* const* ws, int n, const float* x, int64_t
     // staging-free GEMV: one row only (measured: K = 6912, 8.1 -> 6.6 us at
     // M = 1; already slower at M = 2 for N = 6912, where every workgroup
     // re-reads and re-quantises the rows)
-    if (direct && M > 1) return 1;
-    if (disabled || M > 16 || M * K > (direct ? xt::kGemv2FusedQuantMax : xt::kGemvFusedQuantMax) ||
+    const bool force = getenv("XTERN_FUSED_FORCE") != nullptr;  // TEMP
+    if (direct && M > 1 && !force) return 1;
+    if (disabled || M > 16 || M * K > (direct ? (force ? 65536 : xt::kGemv2FusedQuantMax) : xt::kGemvFusedQuantMax) ||
         (((uintptr_t)x) & 15) || (K & 3))
         return 1;
     int ng_total = 0;
@@ -302,9 +303,9 @@ int gemv_fused_quant(const xt_weights* const* ws, int n, const float* x, int64_t
     int waves = 16;
     if (xt::is_int_format(fmt)) {
         waves = xt::int_gemv_waves(fmt, (int)M, nch);
-    } else if (fmt == XT_PACK5 && !staged) {
+    } else if (fmt == XT_PACK5 && !staged && !force) {
         return 1;  // measured: Pack5 fused 9.8 us vs 8.8 quantiser + GEMV (C2, M = 1)
-    } else if (fmt != XT_PACK5 && ng_total * 16 >= 8192) {
+    } else if (fmt != XT_PACK5 && ng_total * 16 >= 8192 && !force) {
         return 1;
     }
     // Ternary tiles take the staging-free GEMV (one chunk per wave, so

@@ -1815,6 +1815,13 @@ MMConfig choose_config(int fmt, int M, int ntiles_nb1, int nch, bool have_rowsum
     // fits its LDS stage (C1 up: 10.9 -> 7.8 us).  Longer K stays on the
     // K-split kernel below: splitting it over workgroups plus a reduction
     // launch measured slower (C1 down: 12.6 vs 8.5 us).
+    // A grid of fewer than ~80 of its 32 x 128 tiles leaves most CUs idle
+    // while each tile takes the same ~7 us; 16 tokens x 32 rows with K over 4
+    // waves spreads such shapes over 4-8x the workgroups (M = 32: K 2560 ->
+    // N 2560 / 3840 7.2 -> 5.0 / 5.2 us; M = 24, N = 6912: 7.4 -> 6.2 us;
+    // 108 tiles, N = 13824 at M = 32: 7.8 vs 8.3 us, the GEMM stays).
+    const long g32_tiles = (long)((ntiles_nb1 * 16 + 127) / 128) * ((M + 31) / 32);
+    if (fmt == XT_PACK4 && ntiles_nb1 > 0 && g32_tiles < 80) return MMConfig{1, 2, 4, 4, 1};
     if (fmt == XT_PACK4 && nch <= gemm32_ncmax()) {
         c = MMConfig{2, 8, 8, 1, 1};
         c.kind = 3;
