@@ -290,9 +290,8 @@ int gemv_fused_quant(const xt_weights* const* ws, int n, const float* x, int64_t
     // staging-free GEMV: one row only (measured: K = 6912, 8.1 -> 6.6 us at
     // M = 1; already slower at M = 2 for N = 6912, where every workgroup
     // re-reads and re-quantises the rows)
-    const bool force = getenv("XTERN_FUSED_FORCE") != nullptr;  // TEMP
-    if (direct && M > 1 && !force) return 1;
-    if (disabled || M > 16 || M * K > (direct ? (force ? 65536 : xt::kGemv2FusedQuantMax) : xt::kGemvFusedQuantMax) ||
+    if (direct && M > 1) return 1;
+    if (disabled || M > 16 || M * K > (direct ? xt::kGemv2FusedQuantMax : xt::kGemvFusedQuantMax) ||
         (((uintptr_t)x) & 15) || (K & 3))
         return 1;
     int ng_total = 0;
@@ -303,15 +302,17 @@ int gemv_fused_quant(const xt_weights* const* ws, int n, const float* x, int64_t
     int waves = 16;
     if (xt::is_int_format(fmt)) {
         waves = xt::int_gemv_waves(fmt, (int)M, nch);
-    } else if (fmt == XT_PACK5 && !staged && !force) {
-        return 1;  // measured: Pack5 fused 9.8 us vs 8.8 quantiser + GEMV (C2, M = 1)
-    } else if (fmt != XT_PACK5 && ng_total * 16 >= 8192 && !force) {
+    } else if (fmt == XT_PACK5 && !staged && nch <= 16) {
+        // measured (C2, M = 1): K = 3200 fused 9.5 us vs 8.2 quantiser + GEMV,
+        // K = 8640 fused 8.1 vs 8.7
+        return 1;
+    } else if (fmt != XT_PACK5 && ng_total * 16 >= 8192) {
         return 1;
     }
     // Ternary tiles take the staging-free GEMV (one chunk per wave, so
     // K <= 16 chunks); Int8 / Int4 the staged one (one piece per thread).
     const int segs = xt::chunk_cols(fmt) / 16;
-    if (direct ? (M * K > xt::gemv2_fused_max(nch))
+    if (direct ? (M * K > xt::gemv2_fused_max(fmt, nch))
                : (!xt::gemv_fits(fmt, (int)M, nch, waves, xt::gemv_ncw(waves)) ||
                   M * nch * segs > (int64_t)waves * 64))
         return 1;

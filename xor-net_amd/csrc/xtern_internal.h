@@ -66,9 +66,10 @@ struct MMArgs {
 };
 // GEMV with the quantiser fused when M * K is at most this (every workgroup
 // re-reads the f32 rows, so only for small inputs).  The staging-free GEMV
-// (Pack4 / XorSparse) fuses one row of up to this many columns.
+// fuses one row of up to this many columns (its LDS stage bounds K further:
+// 31 Pack4 or 28 Pack5 chunks).
 constexpr int kGemvFusedQuantMax = 8192;
-constexpr int kGemv2FusedQuantMax = 8192;
+constexpr int kGemv2FusedQuantMax = 16384;
 
 struct MMConfig {
     int mb, nb, waves, pf;  // tokens per WG = 16*mb, rows per WG = 16*nb
@@ -98,7 +99,7 @@ hipError_t launch_gemm32(const MMArgs& a, int ntiles, int splitk, hipStream_t s)
 hipError_t launch_gemv(int fmt, const MMArgs& a, int ntiles, int waves, hipStream_t s);
 int gemv_ncw(int waves);
 // Largest M * K the staging-free GEMV quantises itself for nch chunks (0: none).
-int gemv2_fused_max(int nch);
+int gemv2_fused_max(int fmt, int nch);
 // 16-row groups per workgroup of the decode GEMV that launch_gemv runs for
 // this format and K (its ntiles count workgroups of that many groups).
 int gemv_row_groups(int fmt, int nch, int ngroups);

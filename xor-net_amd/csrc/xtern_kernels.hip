@@ -1015,8 +1015,10 @@ static size_t gemv2_fused_lds(int nch, int steps, int rg) {
     return (size_t)nch * steps * 1024 + (size_t)w * rg * 64 * 16 + (size_t)w * 16 * 4;
 }
 constexpr size_t kLdsBytes = 160 * 1024;
-int gemv2_fused_max(int nch) {
-    if (nch > 64 || gemv2_fused_lds(nch, 4, 2) > kLdsBytes) return 0;
+int gemv2_fused_max(int fmt, int nch) {
+    // Pack5 always runs one row group per workgroup; Pack4 may run two.
+    const bool p5 = fmt == XT_PACK5;
+    if (nch > 64 || gemv2_fused_lds(nch, p5 ? 5 : 4, p5 ? 1 : 2) > kLdsBytes) return 0;
     return gemv2_waves(nch) * 64 * 32;
 }
 
