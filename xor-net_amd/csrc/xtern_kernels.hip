@@ -2085,14 +2085,6 @@ __device__ __forceinline__ float apply_act(int act, float g, float u, bool main_
     }
 }
 
-// Binade of a running sum: floor(log2 s) clamped below at -126 (the grid
-// 2^-149 spans [0, 2^-125)); 128 for sums at or beyond 2^128.
-__device__ __forceinline__ int binade_d(double a) {
-    if (a == 0.0) return -126;
-    const int e = __builtin_amdgcn_frexp_exp(a) - 1;  // a = m * 2^(e+1), m in [0.5, 1)
-    return e < -126 ? -126 : (e > 128 ? 128 : e);
-}
-
 constexpr int kMidThreads = 1024;
 constexpr int kMidWaves = kMidThreads / 64;
 constexpr int kMidCmax = 16;                         // row length <= 16 * 1024
@@ -2114,19 +2106,8 @@ __device__ __forceinline__ uint64_t dpp64(uint64_t v) {
     const uint32_t hi = dpp32<CTRL, ROW_MASK>((uint32_t)(v >> 32));
     return ((uint64_t)hi << 32) | lo;
 }
-__device__ __forceinline__ double dpp_d(uint64_t bits) { return __longlong_as_double((long long)bits); }
-__device__ __forceinline__ uint64_t d_bits(double d) { return (uint64_t)__double_as_longlong(d); }
 
 // Inclusive wave scans (Hillis-Steele in rows of 16, then row broadcasts).
-__device__ __forceinline__ double wave_scan_add(double v) {
-    v = __dadd_rn(v, dpp_d(dpp64<0x111, 0xf>(d_bits(v))));
-    v = __dadd_rn(v, dpp_d(dpp64<0x112, 0xf>(d_bits(v))));
-    v = __dadd_rn(v, dpp_d(dpp64<0x114, 0xf>(d_bits(v))));
-    v = __dadd_rn(v, dpp_d(dpp64<0x118, 0xf>(d_bits(v))));
-    v = __dadd_rn(v, dpp_d(dpp64<0x142, 0xa>(d_bits(v))));
-    v = __dadd_rn(v, dpp_d(dpp64<0x143, 0xc>(d_bits(v))));
-    return v;
-}
 __device__ __forceinline__ uint64_t wave_scan_add(uint64_t v) {
     v += dpp64<0x111, 0xf>(v);
     v += dpp64<0x112, 0xf>(v);
@@ -2213,59 +2194,157 @@ __device__ __forceinline__ void grid_split(float t, int b, uint32_t* q, int* r) 
 // does.  `lt` holds t[0..n) (finite, >= 0) in LDS; thread j handles the
 // contiguous elements [j*E, j*E + E), E = ceil(n / 1024) <= kMidCmax.
 struct SeqSumLds {
-    double wtot[kMidWaves];
+    float wtot[kMidWaves];
     uint64_t wgp[kMidWaves];
     int wcnt[kMidWaves];
     float res;
 };
 
-__device__ __forceinline__ float exact_seq_sum(int n, const float* lt, SeqSumLds& sl,
-                                               int* rec_idx, uint64_t* rec_gp, int* rec_b) {
+__device__ __forceinline__ float wave_scan_addf(float v) {
+    v = __fadd_rn(v, __uint_as_float(dpp32<0x111, 0xf>(__float_as_uint(v))));
+    v = __fadd_rn(v, __uint_as_float(dpp32<0x112, 0xf>(__float_as_uint(v))));
+    v = __fadd_rn(v, __uint_as_float(dpp32<0x114, 0xf>(__float_as_uint(v))));
+    v = __fadd_rn(v, __uint_as_float(dpp32<0x118, 0xf>(__float_as_uint(v))));
+    v = __fadd_rn(v, __uint_as_float(dpp32<0x142, 0xa>(__float_as_uint(v))));
+    v = __fadd_rn(v, __uint_as_float(dpp32<0x143, 0xc>(__float_as_uint(v))));
+    return v;
+}
+// Binade of a float >= 0 (subnormals and 0 in -126, infinity 128).
+__device__ __forceinline__ int binade_f(float a) {
+    const int e = (int)(__float_as_uint(a) >> 23);
+    return e == 0 ? -126 : e - 127;
+}
+
+// Significand of s >= 0 on the grid of its binade (implicit bit included;
+// for binade -126 the subnormal or smallest-normal encoding), and the float
+// of significand T < 2^24 in binade b.
+__device__ __forceinline__ int sig_binade(float s, uint32_t* S) {
+    const uint32_t sbits = __float_as_uint(s);
+    const int se = (int)(sbits >> 23);
+    *S = (sbits & 0x7fffffu) | (se ? 0x800000u : 0u);
+    return se == 0 ? -126 : se - 127;
+}
+__device__ __forceinline__ float from_grid(uint64_t T, int b) {
+    return __uint_as_float(T >= 0x800000u ? ((uint32_t)(b + 127) << 23) | ((uint32_t)T & 0x7fffffu)
+                                          : (uint32_t)T);  // b = -126, subnormal
+}
+
+// s + lt[j] + ... + lt[end - 1], each partial sum rounded to f32, by one
+// whole wave (s is the same in every lane): 64 elements at a time are split
+// on the grid of the running sum's binade and prefix-summed; the leading
+// ones that are no tie and keep the sum inside the binade are added at once
+// (exact integer addition on the grid), the next one with a real f32 add.
+__device__ float seq_advance(float s, const float* lt, int j, int end) {
+    const int lane = threadIdx.x & 63;
+    s = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(s)));
+    while (j < end) {
+        uint32_t S;
+        const int bs = sig_binade(s, &S);
+        if (bs > 127) return s;  // infinity plus finite non-negative terms
+        const int e = j + lane;
+        uint32_t inc = 0;
+        bool stop = true;
+        if (e < end) {
+            uint32_t q;
+            int r;
+            grid_split(lt[e], bs, &q, &r);
+            inc = min(q + (r == 2 ? 1u : 0u), kGrid);
+            stop = r == 1;
+        }
+        const uint32_t pre = wave_scan_add(inc);  // <= 64 * 2^24
+        const bool ok = !stop && (uint64_t)S + pre < kGrid;
+        const uint64_t bad = __ballot(!ok);
+        const int m = bad ? (int)__builtin_ctzll(bad) : 64;
+        if (m > 0) {
+            s = from_grid((uint64_t)S + lane_read(pre, m - 1), bs);
+            j += m;
+        }
+        if (m < 64 && j < end) {
+            s = __fadd_rn(s, lt[j]);
+            ++j;
+        }
+        s = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(s)));
+    }
+    return s;
+}
+
+// Sequential float sum t[0] + t[1] + ... + t[n-1] (each partial sum rounded
+// to f32, in index order) -- the order of rms_norm's sum of squares --
+// computed by the whole workgroup.  Within one binade [2^b, 2^(b+1)) of the
+// running sum, every f32 add is an integer add on the grid u = 2^(b-23):
+// fl(s + t) = s + u * round(t / u), except when t / u is an exact half (a
+// tie, whose rounding depends on the parity of s) or when the sum leaves the
+// binade.  So:
+//  1. a float prefix sum predicts the binade of the running sum before each
+//     element;
+//  2. elements that are ties, or after which the predicted binade changes,
+//     end a "piece"; every other element contributes its integer increment,
+//     and the increments are prefix-summed;
+//  3. one wave walks the pieces in order with the running sum's bits on the
+//     scalar unit: if they lie in the piece's precomputed range (the sum is
+//     in the predicted binade and stays below its top after the piece), the
+//     piece is one integer add on the bits; otherwise seq_advance adds the
+//     piece; the piece's end element is always a real f32 add.
+// The result never depends on the prediction being right, only the speed
+// does.  `lt` holds t[0..n) (finite, >= 0) in LDS; thread j handles the
+// contiguous elements [j*E, j*E + E), E = ceil(n / 1024) <= kMidCmax.
+__device__ __forceinline__ float exact_seq_sum(int n, const float* lt, SeqSumLds& sl, int* rec_idx,
+                                               uint64_t* rec_gp, int* rec_b) {
     const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
     const int E = (n + kMidThreads - 1) / kMidThreads;
     const int i0 = tid * E;
-    const int i1 = min(i0 + E, n);  // this thread's elements: [i0, i1)
-    // 1. prefix sums in double: thread-local, then across lanes and waves
-    double acc = 0.0;
-#pragma unroll 1
-    for (int i = i0; i < i1; ++i) acc = __dadd_rn(acc, (double)lt[i]);
-    const double incl = wave_scan_add(acc);
-    const double excl = dpp_d(dpp64<0x138, 0xf>(d_bits(incl)));  // wave_shr:1, lane 0 gets 0
-    const double excl_next = dpp_d(dpp64<0x130, 0xf>(d_bits(excl)));  // wave_shl:1
+    const int cnt = max(0, min(E, n - i0));  // this thread's elements: [i0, i0 + cnt)
+    float t[kMidCmax];
+#pragma unroll
+    for (int e = 0; e < kMidCmax; ++e) t[e] = e < cnt ? lt[i0 + e] : 0.0f;
+    // 1. prefix sums: thread-local, then across lanes and waves
+    float acc = 0.0f;
+#pragma unroll
+    for (int e = 0; e < kMidCmax; ++e)
+        if (e < cnt) acc = __fadd_rn(acc, t[e]);
+    const float incl = wave_scan_addf(acc);
+    const float excl = __uint_as_float(dpp32<0x138, 0xf>(__float_as_uint(incl)));  // wave_shr:1
+    const float excl_next = __uint_as_float(dpp32<0x130, 0xf>(__float_as_uint(excl)));  // wave_shl:1
     if (lane == 63) sl.wtot[w] = incl;
     __syncthreads();
     XT_STAMP(3);
-    double woff = 0.0;
-    for (int j = 0; j < w; ++j) woff = __dadd_rn(woff, sl.wtot[j]);
-    const double woff_next = __dadd_rn(woff, sl.wtot[w]);
+    float woff = 0.0f;
+    for (int j = 0; j < w; ++j) woff = __fadd_rn(woff, sl.wtot[j]);
+    const float woff_next = __fadd_rn(woff, sl.wtot[w]);
     // Prefix before this thread's first element, and before the next
     // thread's first element, computed exactly as that thread computes it.
-    const double off = __dadd_rn(woff, excl);
-    const double off_next = lane < 63 ? __dadd_rn(woff, excl_next) : __dadd_rn(woff_next, 0.0);
+    const float off = __fadd_rn(woff, excl);
+    const float off_next = lane < 63 ? __fadd_rn(woff, excl_next) : __fadd_rn(woff_next, 0.0f);
 
     // 2. The binade before element i is that of off + (local prefix before
     // i) -- the next thread's `off` after the last element.  Piece ends and
-    // integer increments; run twice (count, then write), recomputing rather
-    // than holding per-element state.
+    // integer increments, kept in registers.
+    uint32_t inc[kMidCmax];
+    int bb[kMidCmax];
+    uint32_t endbits = 0;
     uint64_t dsum = 0;
-    uint32_t ends = 0;
     {
-        double lp = 0.0;
-        int b = binade_d(off);
-#pragma unroll 1
-        for (int i = i0; i < i1; ++i) {
-            const float t = lt[i];
-            lp = __dadd_rn(lp, (double)t);
-            const int bn = (i + 1 < i0 + E) ? binade_d(__dadd_rn(off, lp)) : binade_d(off_next);
-            uint32_t q;
-            int r;
-            grid_split(t, b, &q, &r);
-            const bool end = r == 1 || bn != b || i == n - 1;
-            dsum += end ? 0u : min(q + (r == 2 ? 1u : 0u), kGrid);
-            ends += end ? 1u : 0u;
-            b = bn;
+        float lp = 0.0f;
+        int b = binade_f(off);
+#pragma unroll
+        for (int e = 0; e < kMidCmax; ++e) {
+            inc[e] = 0;
+            bb[e] = b;
+            if (e < cnt) {
+                lp = __fadd_rn(lp, t[e]);
+                const int bn = (e + 1 < E) ? binade_f(__fadd_rn(off, lp)) : binade_f(off_next);
+                uint32_t q;
+                int r;
+                grid_split(t[e], b, &q, &r);
+                const bool end = r == 1 || bn != b || i0 + e == n - 1;
+                inc[e] = end ? 0u : min(q + (r == 2 ? 1u : 0u), kGrid);
+                endbits |= (end ? 1u : 0u) << e;
+                dsum += inc[e];
+                b = bn;
+            }
         }
     }
+    const uint32_t ends = __builtin_popcount(endbits);
     const uint64_t gincl = wave_scan_add(dsum);
     const uint32_t cincl = wave_scan_add(ends);
     if (lane == 63) {
@@ -2274,106 +2353,99 @@ __device__ __forceinline__ float exact_seq_sum(int n, const float* lt, SeqSumLds
     }
     __syncthreads();
     XT_STAMP(4);
-    uint64_t goff = gincl - dsum;
-    int coff = (int)(cincl - ends);
+    uint64_t gp = gincl - dsum;
+    int rank = (int)(cincl - ends);
     int total_ends = 0;
     for (int j = 0; j < kMidWaves; ++j) {
         if (j < w) {
-            goff += sl.wgp[j];
-            coff += sl.wcnt[j];
+            gp += sl.wgp[j];
+            rank += sl.wcnt[j];
         }
         total_ends += sl.wcnt[j];
     }
     const bool overflow = total_ends > kMidRecMax;
-    if (!overflow && ends) {
-        double lp = 0.0;
-        int b = binade_d(off);
-        int rank = coff;
-        uint64_t gp = goff;
-#pragma unroll 1
-        for (int i = i0; i < i1; ++i) {
-            const float t = lt[i];
-            lp = __dadd_rn(lp, (double)t);
-            const int bn = (i + 1 < i0 + E) ? binade_d(__dadd_rn(off, lp)) : binade_d(off_next);
-            uint32_t q;
-            int r;
-            grid_split(t, b, &q, &r);
-            const bool end = r == 1 || bn != b || i == n - 1;
-            if (end) {
-                rec_idx[rank] = i;
-                rec_gp[rank] = gp;  // own increment is 0
-                rec_b[rank] = b;
-                ++rank;
-            } else {
-                gp += min(q + (r == 2 ? 1u : 0u), kGrid);
+    if (!overflow && endbits) {
+#pragma unroll
+        for (int e = 0; e < kMidCmax; ++e) {
+            if (e < cnt) {
+                if ((endbits >> e) & 1u) {
+                    rec_idx[rank] = i0 + e;
+                    rec_gp[rank] = gp;  // own increment is 0
+                    rec_b[rank] = bb[e];
+                    ++rank;
+                }
+                gp += inc[e];
             }
-            b = bn;
         }
     }
     __syncthreads();
     XT_STAMP(5);
 
     // 3. walk the pieces (wave 0).  Records are loaded 64 at a time, one per
-    // lane, with everything that does not depend on the running sum; the
-    // sequential part reads them with readlane.
+    // lane, with everything that does not depend on the running sum: the
+    // range [lo, lim) of running-sum bits for which the piece's P increments
+    // are one integer add on the bits (in binade b the bits are
+    // ((b + 127) << 23) + significand - 2^23, or the significand itself for
+    // b = -126, so "sum in binade b and sum + P below 2^(b+1)" is
+    // lo <= bits < hi - P).  The sequential part reads them with readlane.
     if (w == 0) {
 #if XT_MID_STATS
-        int n_fb = 0, n_fb_el = 0;
+        int n_fb = 0;
 #endif
+        // (uniform values read from LDS are made scalar, so that the walk
+        // runs on the scalar unit instead of under exec masks)
+        total_ends = __builtin_amdgcn_readfirstlane(total_ends);
         float s = 0.0f;
         if (overflow) {
-            for (int j = 0; j < n; ++j) s = __fadd_rn(s, lt[j]);
+            s = seq_advance(0.0f, lt, 0, n);
         } else {
+            uint32_t sbits = 0;
             for (int k0 = 0; k0 < total_ends; k0 += 64) {
                 const int k = k0 + lane;
-                int idx = 0, start = 0, rb = 0;
-                uint64_t P = 0;
+                int idx = 0, start = 0;
+                uint32_t lo = 0, lim = 0xffffffffu, P32 = 0;
                 float tend = 0.0f;
                 if (k < total_ends) {
                     idx = rec_idx[k];
-                    rb = rec_b[k];
-                    const uint64_t gp = rec_gp[k];
+                    const int rb = rec_b[k];
                     start = k > 0 ? rec_idx[k - 1] + 1 : 0;
-                    P = gp - (k > 0 ? rec_gp[k - 1] : 0ull);
+                    const uint64_t P = rec_gp[k] - (k > 0 ? rec_gp[k - 1] : 0ull);
                     tend = lt[idx];
+                    if (start < idx) {
+                        const uint32_t hi = (uint32_t)(rb + 128) << 23;
+                        lo = rb == -126 ? 0u : (uint32_t)(rb + 127) << 23;
+                        if (rb > 127 || P >= (uint64_t)(hi - lo)) {
+                            lo = 1u;  // empty range
+                            lim = 0u;
+                        } else {
+                            lim = hi - (uint32_t)P;
+                            P32 = (uint32_t)P;
+                        }
+                    }
                 }
                 const int kn = min(64, total_ends - k0);
                 for (int kk = 0; kk < kn; ++kk) {
-                    const int sidx = lane_read(idx, kk), sstart = lane_read(start, kk);
-                    const int sb = lane_read(rb, kk);
-                    const uint64_t sP = lane_read(P, kk);
-                    const float st = lane_read(tend, kk);
-                    if (sstart < sidx) {
-                        // Inside binade b the running sum is S * 2^(b-23) with
-                        // S its significand (implicit bit included; for b =
-                        // -126 the subnormal or smallest-normal encoding).
-                        const uint32_t sbits = __float_as_uint(s);
-                        const int se = (int)(sbits >> 23);  // s >= 0
-                        const int bs = se == 0 ? -126 : se - 127;
-                        const uint32_t S = (sbits & 0x7fffffu) | (se ? 0x800000u : 0u);
-                        const uint64_t T = (uint64_t)S + sP;
-                        if (bs == sb && sb <= 127 && T < kGrid) {
-                            const uint32_t nb = (T >= 0x800000u)
-                                                    ? ((uint32_t)(sb + 127) << 23) | ((uint32_t)T & 0x7fffffu)
-                                                    : (uint32_t)T;  // b = -126, subnormal
-                            s = __uint_as_float(nb);
-                        } else {
+                    const uint32_t klo = lane_read(lo, kk), klim = lane_read(lim, kk);
+                    if (sbits >= klo && sbits < klim) {
+                        sbits += lane_read(P32, kk);
+                    } else {
 #if XT_MID_STATS
-                            ++n_fb;
-                            n_fb_el += sidx - sstart;
+                        ++n_fb;
 #endif
-                            for (int j = sstart; j < sidx; ++j) s = __fadd_rn(s, lt[j]);
-                        }
+                        const float sa = seq_advance(__uint_as_float(sbits), lt, lane_read(start, kk),
+                                                     lane_read(idx, kk));
+                        sbits = __builtin_amdgcn_readfirstlane(__float_as_uint(sa));
                     }
-                    s = __fadd_rn(s, st);
+                    sbits = __builtin_amdgcn_readfirstlane(
+                        __float_as_uint(__fadd_rn(__uint_as_float(sbits), lane_read(tend, kk))));
                 }
             }
+            s = __uint_as_float(sbits);
         }
         if (lane == 0) sl.res = s;
 #if XT_MID_STATS
         XT_COUNT(8, total_ends);
         XT_COUNT(9, n_fb);
-        XT_COUNT(10, n_fb_el);
 #endif
     }
     XT_STAMP(6);
@@ -2396,12 +2468,13 @@ __global__ __launch_bounds__(kMidThreads) void mlp_mid_kernel(MidArgs a) {
     const float* gr = a.gate + (size_t)m * a.ldg;
     const float* ur = a.up + (size_t)m * a.ldg;
     XT_STAMP(0);
-    float v[kMidCmax];
+    float v[kMidCmax], nwv[kMidCmax];
 #pragma unroll
     for (int c = 0; c < kMidCmax; ++c) {
         const int i = (w * C + c) * 64 + lane;
         v[c] = (c < C && i < n) ? apply_act(ACT, gr[i], ACT == kActIdentity ? 0.0f : ur[i], i < nmain)
                                 : 0.0f;
+        nwv[c] = (a.norm_w && c < C && i < n) ? a.norm_w[i] : 0.0f;  // fetched early
     }
     XT_STAMP(1);
     if (a.norm_w) {
@@ -2440,7 +2513,7 @@ __global__ __launch_bounds__(kMidThreads) void mlp_mid_kernel(MidArgs a) {
 #pragma unroll
         for (int c = 0; c < kMidCmax; ++c) {
             const int i = (w * C + c) * 64 + lane;
-            if (c < C && i < n) v[c] = __fmul_rn(__fmul_rn(v[c], invr), a.norm_w[i]);
+            if (c < C && i < n) v[c] = __fmul_rn(__fmul_rn(v[c], invr), nwv[c]);
         }
     }
     XT_STAMP(11);
