@@ -279,6 +279,10 @@ int linear_q(const xt_weights* const* ws, int n, const int8_t* q, const float* i
 
 // Small inputs on the GEMV: the kernel quantises the f32 rows itself (no
 // separate quantiser launch).  Returns 1 when the case does not apply.
+// Largest workgroups x K for which the decode GEMV quantises its f32 row in
+// every workgroup rather than after a separate quantiser launch.
+constexpr int64_t kFusedRowReads = 1200 * 1024;
+
 int gemv_fused_quant(const xt_weights* const* ws, int n, const float* x, int64_t M,
                      float* const* ys, int mode, hipStream_t s) {
     const bool disabled = getenv("XTERN_NO_FUSED_QUANT") != nullptr;
@@ -296,9 +300,11 @@ int gemv_fused_quant(const xt_weights* const* ws, int n, const float* x, int64_t
         return 1;
     int ng_total = 0;
     for (int p = 0; p < n; ++p) ng_total += (int)((ws[p]->N + 15) / 16);
-    // The fused GEMV saves the quantiser launch (~4 us), which outweighs the
-    // K-split kernel's edge on every measured shape except many rows of
-    // Pack4 / XorSparse (N >= 8192), where that kernel is ~2.5 us faster.
+    // The fused GEMV saves the quantiser launch, but every workgroup reads
+    // and quantises the whole f32 row: worth it while workgroups x K stays
+    // small (measured, Pack4 at M = 1: gate+up 2 x 6912 rows at K = 2560,
+    // 432 workgroups, 6.6 us fused vs 7.2 quantiser + GEMV; K = 4096 ->
+    // 14336, 448 workgroups, 10.1 vs 8.6).
     int waves = 16;
     if (xt::is_int_format(fmt)) {
         waves = xt::int_gemv_waves(fmt, (int)M, nch);
@@ -306,8 +312,9 @@ int gemv_fused_quant(const xt_weights* const* ws, int n, const float* x, int64_t
         // measured (C2, M = 1): K = 3200 fused 9.5 us vs 8.2 quantiser + GEMV,
         // K = 8640 fused 8.1 vs 8.7
         return 1;
-    } else if (fmt != XT_PACK5 && ng_total * 16 >= 8192) {
-        return 1;
+    } else if (fmt != XT_PACK5 && !staged) {
+        const int rg = xt::gemv_row_groups(fmt, nch, ng_total);
+        if ((int64_t)((ng_total + rg - 1) / rg) * K > kFusedRowReads) return 1;
     }
     // Ternary tiles take the staging-free GEMV (one chunk per wave, so
     // K <= 16 chunks); Int8 / Int4 the staged one (one piece per thread).

@@ -1799,13 +1799,9 @@ MMConfig choose_config(int fmt, int M, int ntiles_nb1, int nch, bool have_rowsum
     }
     if (M <= 16) {
         // Measured (MI355X, rotating weights, M = 1..16): the staging-free
-        // GEMV wins or ties everywhere except many rows of Pack4 / XorSparse
-        // at moderate K (C3 4096 -> 14336: 6.0 vs 7.2 us at M = 1 on the
-        // 32-row, 4-wave K-split kernel).
-        const int nrows = ntiles_nb1 * 16;
-        const int kc = nch * (fmt == XT_PACK5 ? 320 : 256);
-        if (ntiles_nb1 > 0 && fmt != XT_PACK5 && nrows >= 8192 && kc <= 8192)
-            return MMConfig{1, 2, 4, 4, 1};
+        // GEMV wins or ties everywhere, also for many rows (K 2560 -> 8192,
+        // M = 4: 3.9 vs 4.7 us on the 32-row, 4-wave K-split kernel;
+        // 4096 -> 14336, M = 16: 7.9 vs 8.7).
         if (nch <= 64 || gemv_fits(fmt, M, nch, 16, gemv_ncw(16))) {
             c = MMConfig{1, gemv_row_groups(fmt, nch, ntiles_nb1), 16, 1, 1};
             c.kind = 2;
