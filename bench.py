@@ -275,6 +275,40 @@ def stack_c4(np, torch, xtern, rng, Ms=(1, 8, 32), layers=30):
     return res
 
 
+def mlp_block_c4(np, torch, xtern, rng, Ms=(1, 8), layers=30):
+    """The BitNet-2B MLP block of the decode step as the reference's
+    fused_mlp_all runs it (layers.rs:497-645): gate+up on one quantised input,
+    ReLU^2(gate) * up, ffn_sub_norm (RMSNorm, exact sequential sum of
+    squares), requantisation, down -- 30 layers of distinct weights (398 MB,
+    > the MALL), independent inputs per layer, one HIP graph per pass.  Not a
+    BASELINE config (configs[4] times the linear layers alone); reported so
+    the middle stage is measured too."""
+    proto = {n: tern_bytes(np, rng, N, K, xtern.XT_PACK4)[0]
+             for n, (K, N) in (("gate", (2560, 6912)), ("up", (2560, 6912)), ("down", (6912, 2560)))}
+    L = []
+    for _ in range(layers):
+        L.append({n: xtern.DeviceWeights(xtern.XT_PACK4, K, N, proto[n], np.full(N, 0.05, np.float32))
+                  for n, (K, N) in (("gate", (2560, 6912)), ("up", (2560, 6912)), ("down", (6912, 2560)))})
+    nw = torch.from_numpy(rng.uniform(0.5, 1.5, 6912).astype(np.float32)).cuda()
+    wbytes = layers * 3 * 6912 * 2560 // 4
+    res = []
+    for M in Ms:
+        x = torch.from_numpy(rng.standard_normal((M, 2560)).astype(np.float32)).cuda()
+        y = torch.empty((M, 2560), dtype=torch.float32, device="cuda")
+
+        def run(_i):
+            for w in L:
+                xtern.mlp_f32(w["gate"], w["up"], w["down"], x, norm_w=nw, out=y)
+        g = Graph(torch, run, 1)
+        us = g.time_ms(10) * 1e3
+        res.append({"workload": "c4_mlp_block_subnorm", "M": M, "layers": layers,
+                    "us_per_mlp": round(us / layers, 2),
+                    "weight_GBs": round(wbytes / (us * 1e-6) / 1e9, 1)})
+    del L
+    torch.cuda.empty_cache()
+    return res
+
+
 def cpu_baseline(np, wl, budget_s=12.0):
     """The oracle's restatement of the reference CPU path (TernaryLinear::forward
     with the VNNI dot when the host has it) on the first `rows` tokens of each
@@ -409,6 +443,8 @@ def main():
         out["configs"] = gemv_configs(np, torch, xtern, rng)
         log("c4 stack ...")
         out["configs"] += stack_c4(np, torch, xtern, rng)
+        log("c4 mlp block ...")
+        out["configs"] += mlp_block_c4(np, torch, xtern, rng)
     if not args.no_cpu:
         log("cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline(np, wl)

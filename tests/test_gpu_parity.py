@@ -231,6 +231,10 @@ def test_c4_stack_layer_shapes():
         g, u = xtern.linear_multi_f32([W["gate"], W["up"]], x)
         assert torch.equal(g, xtern.linear_f32(W["gate"], x))
         assert torch.equal(u, xtern.linear_f32(W["up"], x))
+        # the f32 entry points (quantiser fused into the GEMV at M = 1) equal
+        # the separate quantiser plus the product
+        assert torch.equal(g, xtern.linear_q(W["gate"], q, inv))
+        assert torch.equal(u, xtern.linear_q(W["up"], q, inv))
         xd = torch.from_numpy(rng.standard_normal((M, 6912)).astype(np.float32)).to(DEV)
         qd, invd = xtern.quantize_i8(xd)
         _, acc = xtern.linear_q(W["down"], qd, invd, acc=True)
