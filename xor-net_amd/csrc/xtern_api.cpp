@@ -439,11 +439,12 @@ int mlp_run(const xt_weights* gate, const xt_weights* up, const xt_weights* down
     a.q = qm;
     a.ldq = (int)kpad;
     a.inv = invm;
-    a.rowsum = rsm;
+    // row sums of the requantised rows only for a down product that uses them
+    a.rowsum = wants_rowsum(down, M) ? rsm : nullptr;
     if ((rc = launch_mid(a, M, s))) return rc;
     float* ys[1] = {y};
     const xt_weights* dw[1] = {down};
-    return run_product(dw, 1, qm, (int)kpad, invm, rsm, M, ys, nullptr, s);
+    return run_product(dw, 1, qm, (int)kpad, invm, a.rowsum, M, ys, nullptr, s);
 }
 
 }  // namespace

@@ -2545,6 +2545,11 @@ __global__ __launch_bounds__(kMidThreads) void mlp_mid_kernel(MidArgs a) {
         }
     }
     for (int i = n + tid; i < a.ldq; i += kMidThreads) qr[i] = 0;
+    if (!a.rowsum) {  // the product decodes signed weights or sums the row itself
+        if (tid == 0) a.inv[m] = invs;
+        XT_STAMP(7);
+        return;
+    }
     sum = wave_sum_int(sum);
     __syncthreads();  // sm_i reuse after the flag reads
     if (lane == 0) sm_i[w] = sum;
