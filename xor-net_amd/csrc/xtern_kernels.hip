@@ -2169,26 +2169,6 @@ __device__ __forceinline__ void grid_split(float t, int b, uint32_t* q, int* r) 
     *r = shift <= 0 ? 0 : rdn;
 }
 
-// Sequential float sum t[0] + t[1] + ... + t[n-1] (each partial sum rounded
-// to f32, in index order) -- the order of rms_norm's sum of squares --
-// computed by the whole workgroup.  Within one binade [2^b, 2^(b+1)) of the
-// running sum, every f32 add is an integer add on the grid u = 2^(b-23):
-// fl(s + t) = s + u * round(t / u), except when t / u is an exact half (a
-// tie, whose rounding depends on the parity of s) or when the sum leaves the
-// binade.  So:
-//  1. a double prefix sum predicts the binade of the running sum before each
-//     element;
-//  2. elements that are ties, or after which the predicted binade changes,
-//     end a "piece"; every other element contributes its integer increment,
-//     and the increments are prefix-summed;
-//  3. one wave walks the pieces in order: if the actual running sum is in the
-//     piece's predicted binade and stays below its top, the piece's
-//     increments are added at once (exact), otherwise the piece's elements
-//     are added one by one; the piece's end element is always added with a
-//     real f32 add.
-// The result never depends on the prediction being right, only the speed
-// does.  `lt` holds t[0..n) (finite, >= 0) in LDS; thread j handles the
-// contiguous elements [j*E, j*E + E), E = ceil(n / 1024) <= kMidCmax.
 struct SeqSumLds {
     float wtot[kMidWaves];
     uint64_t wgp[kMidWaves];
