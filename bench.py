@@ -362,6 +362,32 @@ def copy_calibration(torch):
     print(json.dumps({"copy_bytes": n, "launches": 3}))
 
 
+def vendor_int8(np, torch, xtern, rng):
+    """Reference point, not the product: the ROCm library's dense int8 GEMM
+    (torch._int_mm, i8 weights -- 4x the bytes of Pack4) on the C1 and short
+    prefill shapes, beside this library's Pack4 product on the same shapes;
+    both over rotating weight copies (> 2x the MALL) in HIP graphs."""
+    rows = []
+    for M, K, N in ((128, 2560, 6912), (128, 6912, 2560), (32, 2560, 2560), (32, 2560, 6912)):
+        a = torch.randint(-127, 128, (M, K), dtype=torch.int8, device="cuda")
+        n = max(2, -(-2 * MALL_BYTES // (K * N)))
+        bs = [torch.randint(-1, 2, (N, K), dtype=torch.int8, device="cuda").t() for _ in range(n)]
+        g = Graph(torch, lambda i: torch._int_mm(a, bs[i]), n)
+        us_lib = g.time_ms(max(1, 100 // n)) * 1e3
+        del g, bs
+        torch.cuda.empty_cache()
+        wb, _ = tern_bytes(np, rng, N, K, xtern.XT_PACK4)
+        copies = make_copies(np, xtern, xtern.XT_PACK4, K, N, wb, np.ones(N, np.float32), 2 * MALL_BYTES)
+        us_q, _ = time_product(np, torch, xtern, copies, K, N, M, rng, reps=100)
+        del copies
+        torch.cuda.empty_cache()
+        rows.append({"M": M, "K": K, "N": N, "us_int_mm_i8": round(us_lib, 2),
+                     "us_xtern_pack4": round(us_q, 2),
+                     "TOPS_int_mm": round(2 * M * K * N / us_lib / 1e6, 1),
+                     "TOPS_xtern": round(2 * M * K * N / us_q / 1e6, 1)})
+    print(json.dumps({"vendor_int8_gemm": rows}))
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -371,6 +397,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--vendor-int8", action="store_true",
+                    help="time the ROCm dense int8 GEMM beside the Pack4 product and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); "
@@ -385,6 +413,9 @@ def main():
         copy_calibration(torch)
         return
     rng = np.random.default_rng(1234)
+    if args.vendor_int8:
+        vendor_int8(np, torch, xtern, rng)
+        return
     if args.workload != "c1":
         raise SystemExit("only the c1 workload is wired as the headline step")
     log("setting up c1 weights (rotating copies) ...")
