@@ -275,6 +275,29 @@ def stack_c4(np, torch, xtern, rng, Ms=(1, 8, 32), layers=30):
     return res
 
 
+def lm_head(np, torch, xtern, rng, Ms=(1, 16)):
+    """The BitNet-2B LM head (128256 x 2560) as the reference's Int8Linear /
+    Int4Linear (dynamic_linear.rs:180-535): µs per call given i8 rows
+    (product) and f32 rows (forward), HBM GB/s of the weight bytes; weights
+    rotate over > 2x the MALL.  Not a BASELINE config."""
+    N, K = 128256, 2560
+    res = []
+    for fmt, name, nb in ((xtern.XT_INT8, "lm_head_int8", N * K), (xtern.XT_INT4, "lm_head_int4", N * K // 2)):
+        hb = rng.integers(0, 256, nb, dtype=np.uint8)
+        ws = rng.uniform(0.5, 1.5, N).astype(np.float32)
+        copies = make_copies(np, xtern, fmt, K, N, hb, ws, 2 * MALL_BYTES)
+        for M in Ms:
+            us_q, us_f = time_product(np, torch, xtern, copies, K, N, M, rng, reps=40)
+            alg = nb + 4 * N + M * K + 4 * M + 4 * M * N
+            gbs = alg / (us_q * 1e-6) / 1e9
+            res.append({"workload": name, "K": K, "N": N, "M": M, "us_product": round(us_q, 2),
+                        "us_forward_f32": round(us_f, 2), "GBs": round(gbs, 1),
+                        "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)})
+        del copies
+        torch.cuda.empty_cache()
+    return res
+
+
 def mlp_block_c4(np, torch, xtern, rng, Ms=(1, 8), layers=30):
     """The BitNet-2B MLP block of the decode step as the reference's
     fused_mlp_all runs it (layers.rs:497-645): gate+up on one quantised input,
@@ -476,6 +499,8 @@ def main():
         out["configs"] += stack_c4(np, torch, xtern, rng)
         log("c4 mlp block ...")
         out["configs"] += mlp_block_c4(np, torch, xtern, rng)
+        log("lm head ...")
+        out["configs"] += lm_head(np, torch, xtern, rng)
     if not args.no_cpu:
         log("cpu baseline ...")
         out["cpu_baseline"] = cpu_baseline(np, wl)

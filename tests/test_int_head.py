@@ -131,7 +131,8 @@ def test_tile_layout(bits, N, K):
 @pytest.mark.gpu
 @pytest.mark.parametrize("bits", [8, 4])
 @pytest.mark.parametrize("K,N,M", [(2560, 1000, 1), (2560, 1000, 3), (333, 77, 5), (3200, 4096, 16),
-                                   (2560, 4096, 40), (7000, 300, 20)])
+                                   (2560, 4096, 40), (7000, 300, 20), (9000, 200, 2),
+                                   (2560, 6416, 2)])
 @pytest.mark.parametrize("mode", [xtern.XT_QUANT_AVX512, xtern.XT_QUANT_SCALAR])
 def test_int_linear_matches_oracle(bits, K, N, M, mode):
     import torch

@@ -122,11 +122,17 @@ int run_product_int(const xt_weights* const* ws, int n, const int8_t* q, int ldq
                     int64_t M, float* const* ys, int32_t* acc, hipStream_t s) {
     const int fmt = ws[0]->fmt;
     const int nch = (int)ws[0]->nch;
+    // The staging-free GEMV takes 16 rows per launch at any K it accepts;
+    // the staged one as many as its LDS stage holds.
+    const bool direct = xt::gemv2_takes(fmt, nch);
     int mb = 16;
-    while (mb > 1 && !xt::gemv_fits(fmt, mb, nch, 16, xt::gemv_ncw(16))) mb >>= 1;
-    if (!xt::gemv_fits(fmt, mb, nch, 16, xt::gemv_ncw(16)))
+    while (!direct && mb > 1 && !xt::gemv_fits(fmt, mb, nch, 16, xt::gemv_ncw(16))) mb >>= 1;
+    if (!direct && !xt::gemv_fits(fmt, mb, nch, 16, xt::gemv_ncw(16)))
         return fail(XT_ERR_UNSUPPORTED, "in_dim too large for the Int8/Int4 product");
-    const int waves = xt::int_gemv_waves(fmt, mb, nch);
+    const int waves = direct ? 16 : xt::int_gemv_waves(fmt, mb, nch);
+    int ng_total = 0;
+    for (int p = 0; p < n; ++p) ng_total += (int)((ws[p]->N + 15) / 16);
+    const int rg = xt::gemv_row_groups(fmt, nch, ng_total);
     for (int64_t m0 = 0; m0 < M; m0 += mb) {
         const int mr = (int)std::min<int64_t>(mb, M - m0);
         xt::MMArgs a;
@@ -140,8 +146,9 @@ int run_product_int(const xt_weights* const* ws, int n, const int8_t* q, int ldq
             a.proj[p].acc = (n == 1 && acc) ? acc + m0 * ws[p]->N : nullptr;
             a.proj[p].N = (int)ws[p]->N;
             a.proj[p].tile0 = tiles;
-            tiles += ng;
+            tiles += (ng + rg - 1) / rg;
         }
+        a.rg = rg;
         a.nproj = n;
         a.q = q + m0 * ldq;
         a.inv = inv + m0;
@@ -295,6 +302,10 @@ int gemv_fused_quant(const xt_weights* const* ws, int n, const float* x, int64_t
     // M = 1; already slower at M = 2 for N = 6912, where every workgroup
     // re-reads and re-quantises the rows)
     if (direct && M > 1) return 1;
+    // Int8 / Int4 on the staging-free GEMV: the separate quantiser costs a
+    // few us against the ~50 us of a 128256-row head (measured: Int8 head
+    // forward 158 us fused on the staged GEMV, 50 us product on this one)
+    if (xt::is_int_format(fmt) && xt::gemv2_takes(fmt, nch)) return 1;
     if (disabled || M > 16 || M * K > (direct ? xt::kGemv2FusedQuantMax : xt::kGemvFusedQuantMax) ||
         (((uintptr_t)x) & 15) || (K & 3))
         return 1;
@@ -326,7 +337,8 @@ int gemv_fused_quant(const xt_weights* const* ws, int n, const float* x, int64_t
     xt::MMArgs a;
     memset(&a, 0, sizeof a);
     int tiles = 0;
-    const int rg = xt::gemv_row_groups(fmt, nch, ng_total);
+    // (Int8 / Int4 rows quantised in the kernel run on the staged GEMV)
+    const int rg = direct ? xt::gemv_row_groups(fmt, nch, ng_total) : 1;
     for (int p = 0; p < n; ++p) {
         a.proj[p].tiles = ws[p]->tiles;
         a.proj[p].ws = ws[p]->ws;

@@ -103,6 +103,9 @@ int gemv2_fused_max(int fmt, int nch);
 // 16-row groups per workgroup of the decode GEMV that launch_gemv runs for
 // this format and K (its ntiles count workgroups of that many groups).
 int gemv_row_groups(int fmt, int nch, int ngroups);
+// Whether launch_gemv runs the staging-free GEMV for this format and K
+// (i8 rows given).
+bool gemv2_takes(int fmt, int nch);
 int int_gemv_waves(int fmt, int mb, int nch);
 bool gemv_fits(int fmt, int M, int nch, int waves, int ncw);
 // MLP middle stage (xtern_kernels.hip): per row of gate/up, activation,

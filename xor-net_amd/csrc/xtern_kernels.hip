@@ -799,6 +799,8 @@ template <int FMT, int WAVES, int NCW, bool FUSED, int RG>
 __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
     constexpr int STEPS = (FMT == XT_PACK5) ? 5 : 4;
     constexpr int CH = STEPS * 64;
+    // 1 KiB tiles per chunk: Int8 one per k-step, Int4 one per two k-steps
+    constexpr int TPC = (FMT == XT_INT8) ? 4 : (FMT == XT_INT4 ? 2 : 1);
     __shared__ v4i red[WAVES][RG][64];
     __shared__ unsigned tmax[WAVES][16];
     const int lane = threadIdx.x & 63;
@@ -831,8 +833,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
     const uint8_t* wsrc[RG];
 #pragma unroll
     for (int r = 0; r < RG; ++r)
-        wsrc[r] = pv.tiles + ((size_t)min(G0 + r, NG - 1) * nch * 64 + lane) * 16;
-    v4i wv[NCW][RG];
+        wsrc[r] = pv.tiles + ((size_t)min(G0 + r, NG - 1) * nch * TPC * 64 + lane) * 16;
+    v4i wv[NCW][RG][TPC];
     v4i av[NCW][STEPS];
     if constexpr (!FUSED) {
         const int8_t* arow = q + (size_t)min(j, M - 1) * ldq + 16 * g;
@@ -840,7 +842,10 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
         for (int t = 0; t < NCW; ++t) {
             const int c = min(wave + t * WAVES, nch - 1);
 #pragma unroll
-            for (int r = 0; r < RG; ++r) wv[t][r] = ld_stream(wsrc[r] + (size_t)c * kTileBytes);
+            for (int r = 0; r < RG; ++r)
+#pragma unroll
+                for (int u = 0; u < TPC; ++u)
+                    wv[t][r][u] = ld_stream(wsrc[r] + ((size_t)c * TPC + u) * kTileBytes);
 #pragma unroll
             for (int s = 0; s < STEPS; ++s) av[t][s] = ld_cached(arow + (size_t)c * CH + s * 64);
         }
@@ -874,7 +879,10 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
         for (int t = 0; t < NCW; ++t) {
             const int c = min(wave + t * WAVES, nch - 1);
 #pragma unroll
-            for (int r = 0; r < RG; ++r) wv[t][r] = ld_stream(wsrc[r] + (size_t)c * kTileBytes);
+            for (int r = 0; r < RG; ++r)
+#pragma unroll
+                for (int u = 0; u < TPC; ++u)
+                    wv[t][r][u] = ld_stream(wsrc[r] + ((size_t)c * TPC + u) * kTileBytes);
         }
         __builtin_amdgcn_sched_barrier(0);
         __syncthreads();  // tmax cleared
@@ -944,8 +952,8 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
                 int E[4], O[4];
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
-                    E[d] = wv[t][r][d] & 0x00ff00ff;
-                    O[d] = ((unsigned)wv[t][r][d] >> 8) & 0x00ff00ff;
+                    E[d] = wv[t][r][0][d] & 0x00ff00ff;
+                    O[d] = ((unsigned)wv[t][r][0][d] >> 8) & 0x00ff00ff;
                 }
 #pragma unroll
                 for (int s = 0; s < STEPS; ++s) {
@@ -963,9 +971,22 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
             } else {
 #pragma unroll
                 for (int s = 0; s < STEPS; ++s) {
-                    v4i b = decode4(wv[t][r][s]);
+                    v4i b;
+                    if constexpr (FMT == XT_INT8) {
+                        b = wv[t][r][s];
+                    } else if constexpr (FMT == XT_INT4) {
+                        // code c = q + 8 -> (c ^ 8) in the high nibble is the
+                        // signed byte 16 q; the sum is divided by 16 at the end
 #pragma unroll
-                    for (int d = 0; d < 4; ++d) b[d] = signed_codes(b[d]);
+                        for (int d = 0; d < 4; ++d) {
+                            const unsigned w = (unsigned)wv[t][r][s >> 1][d] ^ 0x88888888u;
+                            b[d] = (int)(((s & 1) ? w : (w << 4)) & 0xf0f0f0f0u);
+                        }
+                    } else {
+                        b = decode4(wv[t][r][0][s]);
+#pragma unroll
+                        for (int d = 0; d < 4; ++d) b[d] = signed_codes(b[d]);
+                    }
                     const v4i x = (live && j < M) ? av[t][s] : v4i{0, 0, 0, 0};
                     acc[r][s] = mfma(x, b, acc[r][s]);
                 }
@@ -983,6 +1004,10 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
     v4i sum = red[0][wave][lane];
 #pragma unroll
     for (int w = 1; w < WAVES; ++w) sum += red[w][wave][lane];
+    if constexpr (FMT == XT_INT4) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) sum[r] >>= 4;  // exact: every term is a multiple of 16
+    }
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         const int i = 4 * g + r;
@@ -1042,6 +1067,16 @@ static hipError_t launch_gemv2_rg(int fmt, const MMArgs& a, int ntiles, hipStrea
             }                                                                                    \
         } else if (fmt == XT_PACK5) {                                                            \
             hipLaunchKernelGGL((gemv2_kernel<XT_PACK5, W_, NCW_, false, RG>), dim3(ntiles), dim3(W_ * 64), 0, s, a); \
+        } else if (fmt == XT_INT8) {                                                             \
+            if constexpr (NCW_ <= 2)                                                             \
+                hipLaunchKernelGGL((gemv2_kernel<XT_INT8, W_, NCW_, false, RG>), dim3(ntiles), dim3(W_ * 64), 0, s, a); \
+            else                                                                                 \
+                return hipErrorInvalidValue;                                                     \
+        } else if (fmt == XT_INT4) {                                                             \
+            if constexpr (NCW_ <= 2)                                                             \
+                hipLaunchKernelGGL((gemv2_kernel<XT_INT4, W_, NCW_, false, RG>), dim3(ntiles), dim3(W_ * 64), 0, s, a); \
+            else                                                                                 \
+                return hipErrorInvalidValue;                                                     \
         } else {                                                                                 \
             hipLaunchKernelGGL((gemv2_kernel<XT_PACK4, W_, NCW_, false, RG>), dim3(ntiles), dim3(W_ * 64), 0, s, a); \
         }                                                                                        \
@@ -1059,15 +1094,19 @@ static hipError_t launch_gemv2(int fmt, const MMArgs& a, int ntiles, hipStream_t
 
 static bool use_gemv2(int fmt, int nch) {
     static const bool staged = getenv("XTERN_GEMV_STAGED") != nullptr;
-    return !staged && (fmt == XT_PACK4 || fmt == XT_PACK5 || fmt == XT_XORSPARSE) && nch <= 64;
+    if (staged) return false;
+    if (fmt == XT_INT8 || fmt == XT_INT4) return nch <= 32;  // weight registers: 4 / 2 tiles a chunk
+    return (fmt == XT_PACK4 || fmt == XT_PACK5 || fmt == XT_XORSPARSE) && nch <= 64;
 }
+bool gemv2_takes(int fmt, int nch) { return use_gemv2(fmt, nch); }
 int gemv_row_groups(int fmt, int nch, int ngroups) {
     return use_gemv2(fmt, nch) ? gemv2_rg_for(fmt, nch, ngroups) : 1;
 }
 
 hipError_t launch_gemv(int fmt, const MMArgs& a, int ntiles, int waves, hipStream_t s) {
-    if (use_gemv2(fmt, a.nch))
-        return launch_gemv2(fmt == XT_PACK5 ? XT_PACK5 : XT_PACK4, a, ntiles, s);
+    // (Int8 / Int4 rows quantised in the kernel stay on the staged GEMV)
+    if (use_gemv2(fmt, a.nch) && !(a.x && is_int_format(fmt)))
+        return launch_gemv2(fmt == XT_XORSPARSE ? XT_PACK4 : fmt, a, ntiles, s);
     const int ch = fmt == XT_PACK5 ? 320 : 256;
     const size_t lds = (size_t)a.M * a.nch * ch;
 #define XT_GEMV(W_, NCW_)                                                                        \
