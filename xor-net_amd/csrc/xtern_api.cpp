@@ -324,13 +324,14 @@ int gemv_fused_quant(const xt_weights* const* ws, int n, const float* x, int64_t
         // K = 8640 fused 8.1 vs 8.7
         return 1;
     } else if (fmt != XT_PACK5 && !staged) {
-        const int rg = xt::gemv_row_groups(fmt, nch, ng_total);
-        if ((int64_t)((ng_total + rg - 1) / rg) * K > kFusedRowReads) return 1;
+        const int g = xt::gemv_row_groups(fmt, nch, ng_total);
+        if ((int64_t)((ng_total + g - 1) / g) * K > kFusedRowReads) return 1;
     }
     // Ternary tiles take the staging-free GEMV (one chunk per wave, so
     // K <= 16 chunks); Int8 / Int4 the staged one (one piece per thread).
     const int segs = xt::chunk_cols(fmt) / 16;
-    if (direct ? (M * K > xt::gemv2_fused_max(fmt, nch))
+    const int rg = direct ? xt::gemv_row_groups(fmt, nch, ng_total) : 1;
+    if (direct ? (M * K > xt::gemv2_fused_max(fmt, nch, rg))
                : (!xt::gemv_fits(fmt, (int)M, nch, waves, xt::gemv_ncw(waves)) ||
                   M * nch * segs > (int64_t)waves * 64))
         return 1;
@@ -338,7 +339,6 @@ int gemv_fused_quant(const xt_weights* const* ws, int n, const float* x, int64_t
     memset(&a, 0, sizeof a);
     int tiles = 0;
     // (Int8 / Int4 rows quantised in the kernel run on the staged GEMV)
-    const int rg = direct ? xt::gemv_row_groups(fmt, nch, ng_total) : 1;
     for (int p = 0; p < n; ++p) {
         a.proj[p].tiles = ws[p]->tiles;
         a.proj[p].ws = ws[p]->ws;

@@ -98,8 +98,9 @@ hipError_t launch_gemm32(const MMArgs& a, int ntiles, int splitk, hipStream_t s)
 // Decode GEMV (M <= 16): 16 output rows per workgroup, activations in LDS.
 hipError_t launch_gemv(int fmt, const MMArgs& a, int ntiles, int waves, hipStream_t s);
 int gemv_ncw(int waves);
-// Largest M * K the staging-free GEMV quantises itself for nch chunks (0: none).
-int gemv2_fused_max(int fmt, int nch);
+// Largest M * K the staging-free GEMV quantises itself for nch chunks and rg
+// row groups per workgroup (0: none).
+int gemv2_fused_max(int fmt, int nch, int rg);
 // 16-row groups per workgroup of the decode GEMV that launch_gemv runs for
 // this format and K (its ntiles count workgroups of that many groups).
 int gemv_row_groups(int fmt, int nch, int ngroups);

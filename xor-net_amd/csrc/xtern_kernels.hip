@@ -1018,12 +1018,20 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
     }
 }
 
-// Row groups per workgroup of the staging-free GEMV.  Two groups (half the
-// workgroups, one activation load for both) win only when there are many
-// rows: C0 (6912 rows, K = 2560) 3.8 -> 3.5 us, but 2560 rows 2.9 -> 3.2 us
-// and K = 14336 6.7 -> 8.5 us; Pack5 (3200 -> 8640) 5.4 -> 6.1 us.
+// Row groups per workgroup of the staging-free GEMV: the most (4, 2, 1)
+// that leave at least 200 workgroups and at most 80 KiB of weights per
+// workgroup.  Measured (MI355X, rotating weights, µs at M = 1 / 16 for 1, 2,
+// 4 groups): C0 2560 -> 6912 3.7 / 3.5 / 4.1 at M = 1; 4096 -> 14336 7.5 /
+// 5.9 / 5.3 and 11.8 / 7.9 / 6.4; 2560 -> 32768 at M = 16 14.3 / 11.1 / 7.8;
+// Int4 head 128256 rows 33.3 / 29.7 / 27.9; Int8 head 48.9 / 49.9 / 52.1 at
+// M = 1 and 72.6 / 61.9 / 61.1 at M = 16.  Pack5 stays at one (3200 -> 8640:
+// 5.4 vs 6.1 us with two).
 static int gemv2_rg_for(int fmt, int nch, int ngroups) {
-    return (fmt != XT_PACK5 && ngroups >= 400 && nch <= 16) ? 2 : 1;
+    if (fmt == XT_PACK5) return 1;
+    const int tpc = fmt == XT_INT8 ? 4 : (fmt == XT_INT4 ? 2 : 1);
+    for (int rg : {4, 2})
+        if (ngroups / rg >= 200 && rg * nch * tpc * kTileBytes <= 80 * 1024) return rg;
+    return 1;
 }
 
 // Waves of the staging-free GEMV for nch chunks, and the most f32 elements
@@ -1040,10 +1048,8 @@ static size_t gemv2_fused_lds(int nch, int steps, int rg) {
     return (size_t)nch * steps * 1024 + (size_t)w * rg * 64 * 16 + (size_t)w * 16 * 4;
 }
 constexpr size_t kLdsBytes = 160 * 1024;
-int gemv2_fused_max(int fmt, int nch) {
-    // Pack5 always runs one row group per workgroup; Pack4 may run two.
-    const bool p5 = fmt == XT_PACK5;
-    if (nch > 64 || gemv2_fused_lds(nch, p5 ? 5 : 4, p5 ? 1 : 2) > kLdsBytes) return 0;
+int gemv2_fused_max(int fmt, int nch, int rg) {
+    if (nch > 64 || gemv2_fused_lds(nch, fmt == XT_PACK5 ? 5 : 4, rg) > kLdsBytes) return 0;
     return gemv2_waves(nch) * 64 * 32;
 }
 
@@ -1089,6 +1095,7 @@ static hipError_t launch_gemv2_rg(int fmt, const MMArgs& a, int ntiles, hipStrea
 }
 
 static hipError_t launch_gemv2(int fmt, const MMArgs& a, int ntiles, hipStream_t s) {
+    if (a.rg == 4) return launch_gemv2_rg<4>(fmt, a, ntiles, s);
     return a.rg == 2 ? launch_gemv2_rg<2>(fmt, a, ntiles, s) : launch_gemv2_rg<1>(fmt, a, ntiles, s);
 }
 
