@@ -1024,13 +1024,14 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
 // 4 groups): C0 2560 -> 6912 3.7 / 3.5 / 4.1 at M = 1; 4096 -> 14336 7.5 /
 // 5.9 / 5.3 and 11.8 / 7.9 / 6.4; 2560 -> 32768 at M = 16 14.3 / 11.1 / 7.8;
 // Int4 head 128256 rows 33.3 / 29.7 / 27.9; Int8 head 48.9 / 49.9 / 52.1 at
-// M = 1 and 72.6 / 61.9 / 61.1 at M = 16.  Pack5 stays at one (3200 -> 8640:
-// 5.4 vs 6.1 us with two).
+// M = 1 and 72.6 / 61.9 / 61.1 at M = 16.  Pack5 never takes two (3200 ->
+// 8640: 5.3 / 6.1 / 6.1; 3200 -> 32000: 11.0 / 12.1 / 9.3).
 static int gemv2_rg_for(int fmt, int nch, int ngroups) {
-    if (fmt == XT_PACK5) return 1;
     const int tpc = fmt == XT_INT8 ? 4 : (fmt == XT_INT4 ? 2 : 1);
     for (int rg : {4, 2})
-        if (ngroups / rg >= 200 && rg * nch * tpc * kTileBytes <= 80 * 1024) return rg;
+        if (ngroups / rg >= 200 && rg * nch * tpc * kTileBytes <= 80 * 1024 &&
+            !(fmt == XT_PACK5 && rg == 2))
+            return rg;
     return 1;
 }
 
