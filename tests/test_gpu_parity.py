@@ -475,3 +475,18 @@ def test_small_prefill_default_config(K, N, M):
     _, acc = xtern.linear_q(w, torch.from_numpy(q).to(DEV), torch.ones(M, device=DEV),
                             acc=True)
     assert np.array_equal(acc.cpu().numpy(), exact_acc(t, q))
+
+
+@pytest.mark.parametrize("fmt,K,N", [(xtern.XT_PACK5, 3200, 16016), (xtern.XT_PACK4, 2560, 32784),
+                                     (xtern.XT_PACK4, 4096, 14352)])
+@pytest.mark.parametrize("M", [1, 3, 16])
+def test_tall_decode_row_groups(fmt, K, N, M):
+    """Tall matrices, where the decode GEMV runs several 16-row groups per
+    workgroup (including a last workgroup with fewer groups), are exact."""
+    log(f"tall decode fmt={FMT_ID[fmt]} K={K} N={N} M={M}")
+    rng = np.random.default_rng(K + N + M)
+    t = tern(rng, N, K)
+    w = xtern.DeviceWeights(fmt, K, N, make_bytes(t, fmt), np.ones(N, np.float32))
+    q = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    _, acc = xtern.linear_q(w, torch.from_numpy(q).to(DEV), torch.ones(M, device=DEV), acc=True)
+    assert np.array_equal(acc.cpu().numpy(), exact_acc(t, q))
