@@ -2262,10 +2262,11 @@ __device__ __forceinline__ float from_grid(uint64_t T, int b) {
 }
 
 // s + lt[j] + ... + lt[end - 1], each partial sum rounded to f32, by one
-// whole wave (s is the same in every lane): 64 elements at a time are split
-// on the grid of the running sum's binade and prefix-summed; the leading
-// ones that are no tie and keep the sum inside the binade are added at once
-// (exact integer addition on the grid), the next one with a real f32 add.
+// whole wave (s is the same in every lane): 256 elements at a time (4
+// consecutive ones per lane) are split on the grid of the running sum's
+// binade and prefix-summed; the leading ones that are no tie and keep the sum
+// inside the binade are added at once (exact integer addition on the grid),
+// the next one with a real f32 add.
 __device__ float seq_advance(float s, const float* lt, int j, int end) {
     const int lane = threadIdx.x & 63;
     s = __uint_as_float(__builtin_amdgcn_readfirstlane(__float_as_uint(s)));
@@ -2273,25 +2274,51 @@ __device__ float seq_advance(float s, const float* lt, int j, int end) {
         uint32_t S;
         const int bs = sig_binade(s, &S);
         if (bs > 127) return s;  // infinity plus finite non-negative terms
-        const int e = j + lane;
-        uint32_t inc = 0;
-        bool stop = true;
-        if (e < end) {
-            uint32_t q;
-            int r;
-            grid_split(lt[e], bs, &q, &r);
-            inc = min(q + (r == 2 ? 1u : 0u), kGrid);
-            stop = r == 1;
+        // lane l: elements j + 4 l .. j + 4 l + 3; local inclusive prefixes
+        uint32_t pre[4];
+        int kbad = 4;  // first element of the lane that is a tie or past `end`
+        uint32_t acc = 0;
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const int e = j + 4 * lane + k;
+            uint32_t q = 0;
+            int r = 1;  // past the end: treated as a stop
+            if (e < end) grid_split(lt[e], bs, &q, &r);
+            if (r == 1 && kbad == 4) kbad = k;
+            acc += min(q + (r == 2 ? 1u : 0u), kGrid);
+            pre[k] = acc;  // <= 4 * 2^24 per lane
         }
-        const uint32_t pre = wave_scan_add(inc);  // <= 64 * 2^24
-        const bool ok = !stop && (uint64_t)S + pre < kGrid;
-        const uint64_t bad = __ballot(!ok);
-        const int m = bad ? (int)__builtin_ctzll(bad) : 64;
+        const uint32_t lincl = wave_scan_add(acc);  // <= 256 * 2^24 < 2^32
+        const uint32_t lexcl = lincl - acc;
+        // first element (in order) that is a stop or leaves the binade
+        int kfirst = kbad;
+#pragma unroll
+        for (int k = 3; k >= 0; --k)
+            if ((uint64_t)S + lexcl + pre[k] >= kGrid) kfirst = min(kfirst, k);
+        const uint64_t bad = __ballot(kfirst < 4);
+        int m;  // elements added on the grid
+        uint32_t pm = 0;
+        if (bad) {
+            const int L = (int)__builtin_ctzll(bad);
+            const int kL = lane_read(kfirst, L);
+            m = 4 * L + kL;
+            if (m > 0) {
+                // prefix through element m - 1
+                uint32_t mine = 0;
+#pragma unroll
+                for (int k = 0; k < 4; ++k)
+                    if (k == kL - 1) mine = lexcl + pre[k];
+                pm = kL > 0 ? lane_read(mine, L) : lane_read(lincl, L - 1);
+            }
+        } else {
+            m = 256;
+            pm = lane_read(lincl, 63);
+        }
         if (m > 0) {
-            s = from_grid((uint64_t)S + lane_read(pre, m - 1), bs);
+            s = from_grid((uint64_t)S + pm, bs);
             j += m;
         }
-        if (m < 64 && j < end) {
+        if (m < 256 && j < end) {
             s = __fadd_rn(s, lt[j]);
             ++j;
         }
@@ -2457,20 +2484,22 @@ __device__ __forceinline__ float exact_seq_sum(int n, const float* lt, SeqSumLds
                     }
                 }
                 const int kn = min(64, total_ends - k0);
+                // The dependency chain per piece is two compares, a select
+                // and one f32 add; the fallback is a branch not taken.
                 for (int kk = 0; kk < kn; ++kk) {
                     const uint32_t klo = lane_read(lo, kk), klim = lane_read(lim, kk);
-                    if (sbits >= klo && sbits < klim) {
-                        sbits += lane_read(P32, kk);
-                    } else {
+                    const uint32_t kp = lane_read(P32, kk);
+                    const float kt = lane_read(tend, kk);
+                    const bool inr = sbits >= klo && sbits < klim;
+                    sbits = inr ? sbits + kp : sbits;
+                    if (__builtin_expect(!inr, 0)) {
 #if XT_MID_STATS
                         ++n_fb;
 #endif
-                        const float sa = seq_advance(__uint_as_float(sbits), lt, lane_read(start, kk),
-                                                     lane_read(idx, kk));
-                        sbits = __builtin_amdgcn_readfirstlane(__float_as_uint(sa));
+                        sbits = __float_as_uint(seq_advance(__uint_as_float(sbits), lt,
+                                                            lane_read(start, kk), lane_read(idx, kk)));
                     }
-                    sbits = __builtin_amdgcn_readfirstlane(
-                        __float_as_uint(__fadd_rn(__uint_as_float(sbits), lane_read(tend, kk))));
+                    sbits = __float_as_uint(__fadd_rn(__uint_as_float(sbits), kt));
                 }
             }
             s = __uint_as_float(sbits);
