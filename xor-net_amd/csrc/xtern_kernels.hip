@@ -1049,7 +1049,9 @@ static int gemv2_rg_for(int fmt, int nch, int ngroups) {
 static int gemv2_waves(int nch) {
     for (int w : {4, 8, 10, 16})
         if (nch <= w) return w;
-    return 16;
+    // (as the launcher's list: 14 waves where they cover K at 2, 3 or 4
+    // chunks per wave)
+    return (nch <= 28 || (nch > 32 && nch <= 42) || (nch > 48 && nch <= 56)) ? 14 : 16;
 }
 // LDS of the fused GEMV: the A stage (1 KiB per k-step) plus the static
 // cross-wave sums and maxima; it must fit the 160 KiB of a CU.
@@ -1105,8 +1107,12 @@ static hipError_t launch_gemv2_rg(int fmt, const MMArgs& a, int ntiles, hipStrea
         hipLaunchKernelGGL((gemv2_kernel<XT_PACK5, 5, 2, false, RG>), dim3(ntiles), dim3(5 * 64), 0, s, a);
         return hipGetLastError();
     }
-    XT_GV2(4, 1) XT_GV2(8, 1) XT_GV2(10, 1) XT_GV2(16, 1) XT_GV2(16, 2) XT_GV2(16, 3)
-    XT_GV2(16, 4)
+    // Above 16 chunks, 14 waves where they cover K with the same chunks per
+    // wave (27 or 28 chunks, 42, 56): fewer idle waves (measured at M = 1 /
+    // 8: 6912 -> 2560 4.3 -> 4.1 / 5.3 -> 5.0 us; 14336 -> 4096 6.7 -> 6.3 /
+    // 8.3 -> 7.7; Pack5 8640 -> 3200 5.1 -> 5.0 / 5.6 -> 5.5)
+    XT_GV2(4, 1) XT_GV2(8, 1) XT_GV2(10, 1) XT_GV2(16, 1) XT_GV2(14, 2) XT_GV2(16, 2)
+    XT_GV2(14, 3) XT_GV2(16, 3) XT_GV2(14, 4) XT_GV2(16, 4)
 #undef XT_GV2
     return hipErrorInvalidValue;
 }
