@@ -490,3 +490,24 @@ def test_tall_decode_row_groups(fmt, K, N, M):
     q = rng.integers(-127, 128, (M, K)).astype(np.int8)
     _, acc = xtern.linear_q(w, torch.from_numpy(q).to(DEV), torch.ones(M, device=DEV), acc=True)
     assert np.array_equal(acc.cpu().numpy(), exact_acc(t, q))
+
+
+@pytest.mark.parametrize("K,N", [(6912, 2560), (8192, 300), (2600, 700), (2560, 6912), (100, 40)])
+@pytest.mark.parametrize("mode", [xtern.XT_QUANT_AVX512, xtern.XT_QUANT_SCALAR])
+def test_one_row_forward_equals_quantiser_plus_product(K, N, mode):
+    """f32 forward of one row (the quantiser fused into the decode GEMV,
+    several chunks per wave, K not a multiple of the chunk) gives exactly the
+    separate quantiser followed by the product."""
+    log(f"one-row forward K={K} N={N} mode={mode}")
+    rng = np.random.default_rng(K + N + mode)
+    t = tern(rng, N, K)
+    w = xtern.DeviceWeights(xtern.XT_PACK4, K, N, make_bytes(t, xtern.XT_PACK4),
+                            rng.uniform(0.2, 2.0, N).astype(np.float32))
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    x[0, rng.integers(0, K, 3)] *= 40
+    xd = torch.from_numpy(x).to(DEV)
+    y = xtern.linear_f32(w, xd, mode=mode)
+    q, inv = xtern.quantize_i8(xd, mode=mode)
+    y2, acc = xtern.linear_q(w, q, inv, acc=True)
+    assert torch.equal(y, y2)
+    assert np.array_equal(acc.cpu().numpy(), exact_acc(t, q.cpu().numpy()))

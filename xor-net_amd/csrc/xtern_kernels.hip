@@ -863,27 +863,38 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
         const int K = a.K;
         constexpr int NT = WAVES * 64;
         const int n4 = (M * K) >> 2;
-        // One row of at most one float4 per thread (Pack4 tiles, one chunk
-        // per wave): thread t holds piece t, so wave w holds exactly chunk
-        // w's 64 pieces and every lane finds its A fragment in the packed
-        // bytes of four lanes of its own wave (ds_bpermute, no LDS stage);
-        // the row maximum comes from per-wave maxima (no atomics, so no
-        // clearing barrier).  One barrier in all.
+        // One row on Pack4 tiles: thread t holds pieces t + u NT (u < NCW),
+        // so lane l of wave w holds piece l of chunks w + u WAVES -- exactly
+        // the chunks the wave multiplies -- and every lane finds its A
+        // fragment in the packed bytes of four lanes of its own wave
+        // (ds_bpermute, no LDS stage); the row maximum comes from per-wave
+        // maxima (no atomics, so no clearing barrier).  One barrier in all.
         bool one_pass = false;
-        if constexpr (FMT == XT_PACK4 && NCW == 1) one_pass = M == 1 && n4 <= NT;
+        if constexpr (FMT == XT_PACK4) one_pass = M == 1 && n4 <= NCW * NT;
         if (one_pass) {
-            const int f = threadIdx.x;
-            float4 x0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-            if (f < n4) x0 = *reinterpret_cast<const float4*>(a.x + 4 * f);
+            float4 x0[NCW];
+#pragma unroll
+            for (int t = 0; t < NCW; ++t) {
+                const int f = threadIdx.x + t * NT;
+                x0[t] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                if (f < n4) x0[t] = *reinterpret_cast<const float4*>(a.x + 4 * f);
+            }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-            for (int r = 0; r < RG; ++r)
+            for (int t = 0; t < NCW; ++t) {
+                const int c = min(wave + t * WAVES, nch - 1);
 #pragma unroll
-                for (int u = 0; u < TPC; ++u)
-                    wv[0][r][u] = ld_stream(wsrc[r] + ((size_t)min(wave, nch - 1) * TPC + u) * kTileBytes);
+                for (int r = 0; r < RG; ++r)
+#pragma unroll
+                    for (int u = 0; u < TPC; ++u)
+                        wv[t][r][u] = ld_stream(wsrc[r] + ((size_t)c * TPC + u) * kTileBytes);
+            }
             __builtin_amdgcn_sched_barrier(0);
             // (non-negative floats order as their bit patterns; NaN is ignored)
-            const float mx = fmaxf(fmaxf(fabsf(x0.x), fabsf(x0.y)), fmaxf(fabsf(x0.z), fabsf(x0.w)));
+            float mx = 0.0f;
+#pragma unroll
+            for (int t = 0; t < NCW; ++t)
+                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(x0[t].x), fabsf(x0[t].y)), fmaxf(fabsf(x0[t].z), fabsf(x0[t].w))));
             const int wm = wave_reduce_bits(__float_as_int(mx), [](int p, int q) {
                 return __float_as_int(fmaxf(__int_as_float(p), __int_as_float(q)));
             });
@@ -897,24 +908,31 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
             const float iv = (rmx > 0.0f) ? __fdiv_rn(rmx, 127.0f) : 1.0f;
 #pragma unroll
             for (int r = 0; r < 4; ++r) invr[r] = iv;
-            const int kmain = (K / 16) * 16, col = 4 * f;
-            const float e4[4] = {x0.x, x0.y, x0.z, x0.w};
-            unsigned w4 = 0;
+            const int kmain = (K / 16) * 16;
+            unsigned w4[NCW];
             auto pack = [&](auto mode_c) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    w4 |= (unsigned)(quant_one(e4[e], scale, decltype(mode_c)::value, col + e < kmain) & 255)
-                          << (8 * e);
+                for (int t = 0; t < NCW; ++t) {
+                    const int f = threadIdx.x + t * NT, col = 4 * f;
+                    const float e4[4] = {x0[t].x, x0[t].y, x0[t].z, x0[t].w};
+                    unsigned v = 0;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        v |= (unsigned)(quant_one(e4[e], scale, decltype(mode_c)::value, col + e < kmain) & 255)
+                             << (8 * e);
+                    w4[t] = f < n4 ? v : 0u;  // columns past K: zero activations
+                }
             };
             if (a.mode == XT_QUANT_AVX512) pack(std::integral_constant<int, XT_QUANT_AVX512>{});
             else pack(std::integral_constant<int, XT_QUANT_SCALAR>{});
-            if (f >= n4) w4 = 0u;  // columns past K: zero activations
             // lane (g, j) of step s takes the pieces of lanes 16 s + 4 g + d
 #pragma unroll
-            for (int st = 0; st < STEPS; ++st)
+            for (int t = 0; t < NCW; ++t)
 #pragma unroll
-                for (int d = 0; d < 4; ++d)
-                    av[0][st][d] = __builtin_amdgcn_ds_bpermute((16 * st + 4 * g + d) << 2, (int)w4);
+                for (int st = 0; st < STEPS; ++st)
+#pragma unroll
+                    for (int d = 0; d < 4; ++d)
+                        av[t][st][d] = __builtin_amdgcn_ds_bpermute((16 * st + 4 * g + d) << 2, (int)w4[t]);
         } else {
         if (threadIdx.x < 16) tmax[0][threadIdx.x] = 0u;
         // The f32 pieces are loaded before the weights: loads return in
@@ -1136,7 +1154,7 @@ static hipError_t launch_gemv2_rg(int fmt, const MMArgs& a, int ntiles, hipStrea
                 hipLaunchKernelGGL((gemv2_kernel<XT_PACK5, W_, NCW_, true, RG>), dim3(ntiles), dim3(W_ * 64), stage, s, a); \
             } else {                                                                             \
                 /* one row in one pass: no LDS stage */                                          \
-                const size_t st_ = (NCW_ == 1 && a.M == 1 && (size_t)a.K <= (size_t)W_ * 256) ? 0 : stage; \
+                const size_t st_ = a.M == 1 ? 0 : stage;                                    \
                 hipLaunchKernelGGL((gemv2_kernel<XT_PACK4, W_, NCW_, true, RG>), dim3(ntiles), dim3(W_ * 64), st_, s, a); \
             }                                                                                    \
         } else if (fmt == XT_PACK5) {                                                            \
