@@ -492,16 +492,18 @@ def test_tall_decode_row_groups(fmt, K, N, M):
     assert np.array_equal(acc.cpu().numpy(), exact_acc(t, q))
 
 
-@pytest.mark.parametrize("K,N", [(6912, 2560), (8192, 300), (2600, 700), (2560, 6912), (100, 40)])
+@pytest.mark.parametrize("fmt", [xtern.XT_PACK4, xtern.XT_PACK5], ids=FMT_ID.get)
+@pytest.mark.parametrize("K,N", [(6912, 2560), (8192, 300), (2600, 700), (2560, 6912), (100, 40),
+                                 (8640, 3200)])
 @pytest.mark.parametrize("mode", [xtern.XT_QUANT_AVX512, xtern.XT_QUANT_SCALAR])
-def test_one_row_forward_equals_quantiser_plus_product(K, N, mode):
+def test_one_row_forward_equals_quantiser_plus_product(fmt, K, N, mode):
     """f32 forward of one row (the quantiser fused into the decode GEMV,
     several chunks per wave, K not a multiple of the chunk) gives exactly the
     separate quantiser followed by the product."""
-    log(f"one-row forward K={K} N={N} mode={mode}")
+    log(f"one-row forward fmt={FMT_ID[fmt]} K={K} N={N} mode={mode}")
     rng = np.random.default_rng(K + N + mode)
     t = tern(rng, N, K)
-    w = xtern.DeviceWeights(xtern.XT_PACK4, K, N, make_bytes(t, xtern.XT_PACK4),
+    w = xtern.DeviceWeights(fmt, K, N, make_bytes(t, fmt),
                             rng.uniform(0.2, 2.0, N).astype(np.float32))
     x = rng.standard_normal((1, K)).astype(np.float32)
     x[0, rng.integers(0, K, 3)] *= 40

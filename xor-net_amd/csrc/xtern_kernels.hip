@@ -863,21 +863,24 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
         const int K = a.K;
         constexpr int NT = WAVES * 64;
         const int n4 = (M * K) >> 2;
-        // One row on Pack4 tiles: thread t holds pieces t + u NT (u < NCW),
-        // so lane l of wave w holds piece l of chunks w + u WAVES -- exactly
-        // the chunks the wave multiplies -- and every lane finds its A
+        // One row: lane l of wave w loads float4 piece l of each chunk the
+        // wave multiplies (chunks w + t WAVES), and for Pack5's 80-piece
+        // chunks also piece 64 + l (l < 16), so every lane finds its A
         // fragment in the packed bytes of four lanes of its own wave
         // (ds_bpermute, no LDS stage); the row maximum comes from per-wave
         // maxima (no atomics, so no clearing barrier).  One barrier in all.
+        constexpr int PPC = CH / 4;  // float4 pieces per chunk: 64 or 80
         bool one_pass = false;
-        if constexpr (FMT == XT_PACK4) one_pass = M == 1 && n4 <= NCW * NT;
+        if constexpr (FMT == XT_PACK4 || FMT == XT_PACK5) one_pass = M == 1;
         if (one_pass) {
-            float4 x0[NCW];
+            float4 x0[NCW], x1[NCW];
 #pragma unroll
             for (int t = 0; t < NCW; ++t) {
-                const int f = threadIdx.x + t * NT;
-                x0[t] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+                const int f = (wave + t * WAVES) * PPC + lane;
+                x0[t] = x1[t] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
                 if (f < n4) x0[t] = *reinterpret_cast<const float4*>(a.x + 4 * f);
+                if constexpr (PPC > 64)
+                    if (lane < PPC - 64 && f + 64 < n4) x1[t] = *reinterpret_cast<const float4*>(a.x + 4 * (f + 64));
             }
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -891,10 +894,10 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
             }
             __builtin_amdgcn_sched_barrier(0);
             // (non-negative floats order as their bit patterns; NaN is ignored)
+            auto amax = [](float4 v) { return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w))); };
             float mx = 0.0f;
 #pragma unroll
-            for (int t = 0; t < NCW; ++t)
-                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(x0[t].x), fabsf(x0[t].y)), fmaxf(fabsf(x0[t].z), fabsf(x0[t].w))));
+            for (int t = 0; t < NCW; ++t) mx = fmaxf(mx, fmaxf(amax(x0[t]), amax(x1[t])));
             const int wm = wave_reduce_bits(__float_as_int(mx), [](int p, int q) {
                 return __float_as_int(fmaxf(__int_as_float(p), __int_as_float(q)));
             });
@@ -909,30 +912,39 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) invr[r] = iv;
             const int kmain = (K / 16) * 16;
-            unsigned w4[NCW];
+            unsigned w4[NCW], w5[NCW];
             auto pack = [&](auto mode_c) {
-#pragma unroll
-                for (int t = 0; t < NCW; ++t) {
-                    const int f = threadIdx.x + t * NT, col = 4 * f;
-                    const float e4[4] = {x0[t].x, x0[t].y, x0[t].z, x0[t].w};
-                    unsigned v = 0;
+                auto q4 = [&](float4 v, int f) {
+                    const int col = 4 * f;
+                    const float e4[4] = {v.x, v.y, v.z, v.w};
+                    unsigned r = 0;
 #pragma unroll
                     for (int e = 0; e < 4; ++e)
-                        v |= (unsigned)(quant_one(e4[e], scale, decltype(mode_c)::value, col + e < kmain) & 255)
+                        r |= (unsigned)(quant_one(e4[e], scale, decltype(mode_c)::value, col + e < kmain) & 255)
                              << (8 * e);
-                    w4[t] = f < n4 ? v : 0u;  // columns past K: zero activations
+                    return f < n4 ? r : 0u;  // columns past K: zero activations
+                };
+#pragma unroll
+                for (int t = 0; t < NCW; ++t) {
+                    const int f = (wave + t * WAVES) * PPC + lane;
+                    w4[t] = q4(x0[t], f);
+                    w5[t] = PPC > 64 ? q4(x1[t], f + 64) : 0u;
                 }
             };
             if (a.mode == XT_QUANT_AVX512) pack(std::integral_constant<int, XT_QUANT_AVX512>{});
             else pack(std::integral_constant<int, XT_QUANT_SCALAR>{});
-            // lane (g, j) of step s takes the pieces of lanes 16 s + 4 g + d
+            // lane (g, j) of step s takes chunk pieces 16 s + 4 g + d: lanes
+            // 0..63 of the first packed value, then lanes 0..15 of the second
 #pragma unroll
             for (int t = 0; t < NCW; ++t)
 #pragma unroll
                 for (int st = 0; st < STEPS; ++st)
 #pragma unroll
-                    for (int d = 0; d < 4; ++d)
-                        av[t][st][d] = __builtin_amdgcn_ds_bpermute((16 * st + 4 * g + d) << 2, (int)w4[t]);
+                    for (int d = 0; d < 4; ++d) {
+                        const int idx = 16 * st + 4 * g + d;
+                        av[t][st][d] = st < 4 ? __builtin_amdgcn_ds_bpermute(idx << 2, (int)w4[t])
+                                              : __builtin_amdgcn_ds_bpermute((idx - 64) << 2, (int)w5[t]);
+                    }
         } else {
         if (threadIdx.x < 16) tmax[0][threadIdx.x] = 0u;
         // The f32 pieces are loaded before the weights: loads return in
@@ -1151,7 +1163,7 @@ static hipError_t launch_gemv2_rg(int fmt, const MMArgs& a, int ntiles, hipStrea
             if ((size_t)a.M * a.K > (size_t)W_ * 64 * 32) {                                   \
                 return hipErrorInvalidValue; /* fused rows: 8 float4 per thread */               \
             } else if (fmt == XT_PACK5) {                                                        \
-                hipLaunchKernelGGL((gemv2_kernel<XT_PACK5, W_, NCW_, true, RG>), dim3(ntiles), dim3(W_ * 64), stage, s, a); \
+                hipLaunchKernelGGL((gemv2_kernel<XT_PACK5, W_, NCW_, true, RG>), dim3(ntiles), dim3(W_ * 64), a.M == 1 ? 0 : stage, s, a); \
             } else {                                                                             \
                 /* one row in one pass: no LDS stage */                                          \
                 const size_t st_ = a.M == 1 ? 0 : stage;                                    \
