@@ -302,15 +302,21 @@ struct ProjView {
 };
 typedef const __attribute__((address_space(4))) MMArgs* KArgPtr;
 struct ProjBounds {
-    int np, t1, t2, t3;
+    int np, t0, t1, t2, t3;
 };
 // Read at kernel entry, in the same round of scalar loads as the grid size.
+// proj[0].tile0 (always 0) is read in this round too: it shares the first
+// argument line with proj[0]'s pointers, so that line is fetched beside the
+// bounds and the selected projection's load (proj[0] in a single-projection
+// launch) hits the scalar cache instead of waiting on a second cold line.
 __device__ __forceinline__ ProjBounds proj_bounds() {
     KArgPtr ka = (KArgPtr)__builtin_amdgcn_kernarg_segment_ptr();
-    return ProjBounds{ka->nproj, ka->proj[1].tile0, ka->proj[2].tile0, ka->proj[3].tile0};
+    return ProjBounds{ka->nproj, ka->proj[0].tile0, ka->proj[1].tile0, ka->proj[2].tile0,
+                      ka->proj[3].tile0};
 }
 __device__ __forceinline__ ProjView select_proj(const ProjBounds& pb, int bx) {
     KArgPtr ka = (KArgPtr)__builtin_amdgcn_kernarg_segment_ptr();
+    bx -= pb.t0;  // (tile0 of the first projection is 0)
     const int sel = ((pb.np > 1) & (bx >= pb.t1)) + ((pb.np > 2) & (bx >= pb.t2)) +
                     ((pb.np > 3) & (bx >= pb.t3));
     ProjView v;
