@@ -1645,6 +1645,9 @@ __global__ __launch_bounds__(768) void gemm32s_kernel(const MMArgs a) {
     const int M = a.M;
     const int nch = a.nch;
     const int cps = a.cps;
+    // (the bounds are consumed here, so their loads join the grid-size round
+    // instead of being sunk to their first use after it)
+    asm volatile("" ::"s"(pb.np), "s"(pb.t0), "s"(pb.t1), "s"(pb.t2), "s"(pb.t3), "s"(gx), "s"(gy), "s"(gz));
     __builtin_amdgcn_sched_barrier(0);  // one round of argument loads
     const int lin = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
     const int t = xcd_remap(lin, gx * gy * gz);
