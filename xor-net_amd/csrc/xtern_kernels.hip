@@ -388,6 +388,10 @@ __global__ __launch_bounds__(WAVES * 64) void mm_kernel(const MMArgs a) {
     const int ldq = a.ldq;
     const int cbeg = blockIdx.z * a.cps;
     const int cend = min(nch, cbeg + a.cps);
+    const int8_t* const qbase = a.q;
+    // (consumed here, so the activation pointer and strides are loaded with
+    // the projection's fields rather than in a third round inside the loop)
+    asm volatile("" ::"s"(qbase), "s"(ldq), "s"(nch), "s"(M), "s"(cend), "s"(tiles));
 
     v4i acc[MB][NB];
 #pragma unroll
@@ -417,7 +421,7 @@ __global__ __launch_bounds__(WAVES * 64) void mm_kernel(const MMArgs a) {
 #pragma unroll
                 for (int s = 0; s < STEPS; ++s)
                     av[pp][mb][s] = (c < cend && row < M)
-                                        ? ld_cached(a.q + (size_t)row * ldq + c * CH + s * 64 + g * 16)
+                                        ? ld_cached(qbase + (size_t)row * ldq + c * CH + s * 64 + g * 16)
                                         : zero;
             }
         }
