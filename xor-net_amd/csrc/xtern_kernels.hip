@@ -88,7 +88,9 @@ struct AddOp {
 
 // Workgroup reduction: DPP inside each wave, then the per-wave values
 // through LDS.  MaxOp is only used on non-negative values (absmax).
-template <typename T, typename Op>
+// NW: waves of the workgroup when known at compile time (0: from blockDim,
+// an extra kernel-argument load).
+template <int NW = 0, typename T, typename Op>
 __device__ __forceinline__ T block_reduce(T v, Op op, T* smem) {
     int bits;
     if constexpr (sizeof(T) == 4 && __is_same(T, float)) {
@@ -99,7 +101,7 @@ __device__ __forceinline__ T block_reduce(T v, Op op, T* smem) {
     } else {
         v = (T)wave_reduce_bits((int)v, [op](int x, int y) { return (int)op((T)x, (T)y); });
     }
-    const int wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    const int wave = threadIdx.x >> 6, nw = NW > 0 ? NW : (int)(blockDim.x >> 6);
     if ((threadIdx.x & 63) == 0) smem[wave] = v;
     __syncthreads();
     T r = smem[0];
@@ -182,16 +184,22 @@ __global__ __launch_bounds__(NT) void quantize_reg_kernel(const float* __restric
     const int m = blockIdx.x;
     const float4* x4 = reinterpret_cast<const float4*>(x + (size_t)m * ldx);
     uint32_t* q4 = reinterpret_cast<uint32_t*>(q + (size_t)m * ldq);
-    const int K4 = K >> 2;
+    const int K4 = K >> 2;  // >= 1 (the launcher sends K < 4 elsewhere)
+    // (every argument is consumed here, so all of them arrive in one round of
+    // scalar loads ahead of the row load)
+    asm volatile("" ::"s"(x), "s"(ldx), "s"(K), "s"(q), "s"(ldq), "s"(inv), "s"(rowsum), "s"(mode));
     float4 v[NV];
     float mx = 0.0f;
+    // unconditional loads at clamped pieces, zeroed afterwards
+#pragma unroll
+    for (int u = 0; u < NV; ++u) v[u] = x4[min((int)threadIdx.x + u * NT, K4 - 1)];
 #pragma unroll
     for (int u = 0; u < NV; ++u) {
         const int i = threadIdx.x + u * NT;
-        v[u] = i < K4 ? x4[i] : make_float4(0.f, 0.f, 0.f, 0.f);
+        if (i >= K4) v[u] = make_float4(0.f, 0.f, 0.f, 0.f);
         mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
     }
-    mx = block_reduce(mx, MaxOp(), sm_f);
+    mx = block_reduce<NT / 64>(mx, MaxOp(), sm_f);
     const float scale = (mx > 0.0f) ? __fdiv_rn(127.0f, mx) : 1.0f;
     const float invs = (mx > 0.0f) ? __fdiv_rn(mx, 127.0f) : 1.0f;
     const int kmain = (K / 16) * 16;
@@ -209,7 +217,7 @@ __global__ __launch_bounds__(NT) void quantize_reg_kernel(const float* __restric
                 ((uint32_t)(b[2] & 255) << 16) | ((uint32_t)(b[3] & 255) << 24);
     }
     for (int i = K4 + threadIdx.x; i < (ldq >> 2); i += NT) q4[i] = 0u;  // padding
-    if (rowsum) sum = block_reduce(sum, AddOp(), sm_i);  // uniform: skipped when unused
+    if (rowsum) sum = block_reduce<NT / 64>(sum, AddOp(), sm_i);  // uniform: skipped when unused
     if (threadIdx.x == 0) {
         inv[m] = invs;
         if (rowsum) rowsum[m] = sum;
@@ -240,7 +248,7 @@ hipError_t launch_quantize(const float* x, int64_t ldx, int M, int K, int8_t* q,
     if (M <= 0) return hipSuccess;
     const bool aligned = (K % 4 == 0) && (ldx % 4 == 0) && (ldq % 4 == 0) &&
                          ((uintptr_t)x % 16 == 0) && ((uintptr_t)q % 4 == 0);
-    if (aligned && K <= 16384) {
+    if (aligned && K >= 4 && K <= 16384) {
 #define XT_QREG(NV_, NT_)                                                                        \
     if (K <= 4 * NT_ * NV_) {                                                                    \
         hipLaunchKernelGGL((quantize_reg_kernel<NV_, NT_>), dim3(M), dim3(NT_), 0, s, x, ldx, K, q, \
