@@ -66,7 +66,7 @@ FMT_ID = {xtern.XT_PACK4: "pack4", xtern.XT_PACK5: "pack5", xtern.XT_XORSPARSE: 
 # ---------------------------------------------------------------- quantiser ---
 
 @pytest.mark.parametrize("mode", [xtern.XT_QUANT_AVX512, xtern.XT_QUANT_SCALAR])
-@pytest.mark.parametrize("M,K", [(1, 1), (1, 15), (2, 16), (3, 17), (1, 2560), (5, 6912),
+@pytest.mark.parametrize("M,K", [(1, 1), (2, 4), (1, 8), (1, 15), (2, 16), (3, 17), (1, 2560), (5, 6912),
                                  (128, 2560), (4, 14336), (2, 3203)])
 def test_quantize_exact(M, K, mode):
     log(f"quantize M={M} K={K} mode={mode}")
