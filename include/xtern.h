@@ -9,8 +9,24 @@
  * Device pointers are HIP device pointers on the current device; `stream` is a
  * hipStream_t passed as void* (NULL = the default stream).  All compute calls
  * are asynchronous on `stream`; the library only synchronises inside
- * xt_weights_create / xt_weights_destroy and when a workspace has to grow.
- * Calls are thread-safe; calls on different streams may run concurrently.
+ * xt_weights_create / xt_weights_destroy / xt_workspace_release.
+ *
+ * Threads: every call may be made from several host threads at once, also
+ * on one shared stream and with one shared weight handle (the reference's
+ * forward(&self) is shared across threads through Arc).  The device
+ * workspaces of the f32 entry points belong to one (device, stream, host
+ * thread) each, so concurrent callers never share one; a workspace that has
+ * to grow is replaced, and the old one is kept (not freed) until
+ * xt_workspace_release, because queued launches or a captured HIP graph may
+ * still use it.
+ *
+ * HIP graphs: the compute calls can be captured.  No call allocates,
+ * synchronises or clears memory while its stream is being captured: a call
+ * whose workspace would have to grow fails with XT_ERR_UNSUPPORTED instead.
+ * Make one eager call of the largest shape on the capturing stream and
+ * thread first.  A graph uses the workspace of the thread and stream it was
+ * captured on; replay it on that stream, or order it against eager calls of
+ * that thread on that stream.
  *
  * Reference paths below are relative to the xor-net source tree.
  */
@@ -186,6 +202,12 @@ int xt_weights_read_tiles(const xt_weights* w, void* host_out, size_t nbytes);
  * layout, `scales` out_dim floats. */
 int xt_int_quantize_host(int bits, const float* w, int64_t out_dim, int64_t in_dim, void* out,
                          float* scales);
+
+/* Free every device workspace the library holds (live and retired), after
+ * waiting for the current device.  No reference counterpart.  The caller
+ * guarantees that no captured graph using them is replayed afterwards; later
+ * calls allocate new workspaces. */
+int xt_workspace_release(void);
 
 /* Free a handle (NULL is a no-op).  Waits for the device first. */
 int xt_weights_destroy(xt_weights* w);

@@ -207,6 +207,54 @@ static void test_hf_prepacked_layer() {
     CHECK(hf.forward(x).data.download() == direct.forward(x).data.download(), "hf layer");
 }
 
+// No allocation inside graph capture: a call whose workspace would have to
+// grow while its stream is captured fails with XT_ERR_UNSUPPORTED; after one
+// eager call of that shape on the stream and thread the same call captures,
+// and replays of the graph equal the eager output.
+static void test_capture_never_allocates() {
+    std::vector<float> w(640 * 2560);
+    for (size_t i = 0; i < w.size(); ++i) w[i] = (float)((int)((i * 2654435761u) >> 7) % 3 - 1);
+    auto l = TernaryLinear::new_(2560, 640, w, TernaryPackType::Pack4);
+    std::vector<float> xin(8 * 2560);
+    for (size_t i = 0; i < xin.size(); ++i) xin[i] = std::sin(0.37f * (float)i);
+    FastTensor x(xin, {8, 2560});
+    DeviceBuffer<float> y1(8 * 640), y2(8 * 640);
+    hipStream_t s = nullptr;
+    CHECK(hipStreamCreate(&s) == hipSuccess, "stream");
+    hipGraph_t g = nullptr;
+    CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed) == hipSuccess, "begin capture");
+    const int rc = xt_ternary_linear_f32(l.handle(), x.data.data(), 8, y1.data(), XT_QUANT_AVX512, s);
+    CHECK(hipStreamEndCapture(s, &g) == hipSuccess, "end capture");
+    CHECK(rc == XT_ERR_UNSUPPORTED, "first call under capture: rc %d", rc);
+    CHECK(std::string(xt_last_error()).find("capture") != std::string::npos, "message: %s",
+          xt_last_error());
+    if (g) (void)hipGraphDestroy(g);
+    g = nullptr;
+    // eager call on the stream, then capture and replay
+    CHECK(xt_ternary_linear_f32(l.handle(), x.data.data(), 8, y1.data(), XT_QUANT_AVX512, s) == XT_OK,
+          "eager: %s", xt_last_error());
+    CHECK(hipStreamSynchronize(s) == hipSuccess, "sync");
+    CHECK(hipStreamBeginCapture(s, hipStreamCaptureModeRelaxed) == hipSuccess, "begin capture 2");
+    const int rc2 = xt_ternary_linear_f32(l.handle(), x.data.data(), 8, y2.data(), XT_QUANT_AVX512, s);
+    CHECK(hipStreamEndCapture(s, &g) == hipSuccess, "end capture 2");
+    CHECK(rc2 == XT_OK, "captured call: %s", xt_last_error());
+    hipGraphExec_t ge = nullptr;
+    if (g && hipGraphInstantiate(&ge, g, nullptr, nullptr, 0) == hipSuccess) {
+        const auto want = y1.download();
+        for (int r = 0; r < 3; ++r) {
+            CHECK(hipMemset(y2.data(), 0, y2.size() * sizeof(float)) == hipSuccess, "clear");
+            CHECK(hipGraphLaunch(ge, s) == hipSuccess, "launch");
+            CHECK(hipStreamSynchronize(s) == hipSuccess, "sync");
+            CHECK(y2.download() == want, "replay %d", r);
+        }
+        (void)hipGraphExecDestroy(ge);
+    } else {
+        CHECK(false, "instantiate");
+    }
+    if (g) (void)hipGraphDestroy(g);
+    (void)hipStreamDestroy(s);
+}
+
 int main(int argc, char** argv) {
     const bool cpu_only = argc > 1 && std::strcmp(argv[1], "--cpu") == 0;
     test_ternary_pack_unpack_roundtrip();
@@ -220,6 +268,7 @@ int main(int argc, char** argv) {
         test_linear_parity_and_zero_input();
         test_dense_and_sparse_match();
         test_errors_and_fused();
+        test_capture_never_allocates();
     }
     std::printf("%s: %d failure(s)\n", cpu_only ? "cpu tests" : "all tests", g_fail);
     return g_fail ? 1 : 0;

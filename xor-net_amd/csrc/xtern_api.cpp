@@ -20,6 +20,7 @@
 #include "../../include/xtern.h"
 #include "xtern_internal.h"
 #include "xtern_layout.h"
+#include "xtern_workspace.h"
 
 struct xt_weights {
     int fmt;
@@ -50,63 +51,91 @@ int hip_fail(hipError_t e, const char* what) {
         if (e_ != hipSuccess) return hip_fail(e_, #call); \
     } while (0)
 
-// Device workspaces, one per (device, stream, kind).  Work on one stream is
-// ordered, so reusing a buffer across calls on it is race-free; growing one
-// waits for the stream first.
+// Device workspaces (xtern_workspace.h): one buffer per (device, stream,
+// host thread, kind), never freed while queued work or a captured graph may
+// use it, never allocated during graph capture.
 //   kind 0: quantised activations, inv scales and row sums of the f32 entry
 //           points, padded copies of caller activations;
 //   kind 1: split-K partial-sum planes and arrival counters.  Zeroed when
 //           allocated; every product launch leaves the counters zero again
-//           (the last workgroup of a tile resets its counter).
-struct Workspace {
-    void* ptr = nullptr;
-    size_t cap = 0;
-};
-std::mutex g_ws_mu;
-std::map<std::tuple<int, hipStream_t, int>, Workspace> g_ws;
+//           (the last workgroup of a tile resets its counter);
+//   kind 2: the MLP's gate / up rows and requantised intermediate.
+int hipb_device(int* d) { return (int)hipGetDevice(d); }
+int hipb_alloc(void** p, size_t n) { return (int)hipMalloc(p, n); }
+int hipb_free(void* p) { return (int)hipFree(p); }
+int hipb_capturing(void* s, bool* c) {
+    hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+    hipError_t e = hipStreamIsCapturing(static_cast<hipStream_t>(s), &st);
+    *c = st != hipStreamCaptureStatusNone;
+    return (int)e;
+}
+int hipb_zero(void* p, size_t n, void* s) {
+    return (int)hipMemsetAsync(p, 0, n, static_cast<hipStream_t>(s));
+}
+int hipb_sync() { return (int)hipDeviceSynchronize(); }
+const char* hipb_str(int e) { return hipGetErrorString((hipError_t)e); }
 
-int workspace(hipStream_t s, size_t bytes, void** out, int kind = 0) {
-    int dev = 0;
-    XT_HIP(hipGetDevice(&dev));
-    std::lock_guard<std::mutex> lk(g_ws_mu);
-    Workspace& w = g_ws[std::make_tuple(dev, s, kind)];
-    if (w.cap < bytes) {
-        if (w.ptr) {
-            XT_HIP(hipStreamSynchronize(s));
-            XT_HIP(hipFree(w.ptr));
-            w.ptr = nullptr;
-            w.cap = 0;
-        }
-        size_t cap = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
-        hipError_t e = hipMalloc(&w.ptr, cap);
-        if (e != hipSuccess) return fail(XT_ERR_NOMEM, std::string("workspace hipMalloc: ") + hipGetErrorString(e));
-        w.cap = cap;
-        if (kind == 1) {
-            e = hipMemsetAsync(w.ptr, 0, cap, s);
-            if (e != hipSuccess) return hip_fail(e, "workspace clear");
-        }
+xt::WorkspaceTable& ws_table() {
+    static xt::WorkspaceTable* t = new xt::WorkspaceTable(xt::WsBackend{
+        hipb_device, hipb_alloc, hipb_free, hipb_capturing, hipb_zero, hipb_sync, hipb_str});
+    return *t;  // (left to process teardown: HIP may be gone by static destruction)
+}
+
+int ws_status(int st, const std::string& err) {
+    switch (st) {
+        case xt::WorkspaceTable::kOk: return XT_OK;
+        case xt::WorkspaceTable::kNoMem: return fail(XT_ERR_NOMEM, err);
+        case xt::WorkspaceTable::kCapture: return fail(XT_ERR_UNSUPPORTED, err);
+        default: return fail(XT_ERR_HIP, err);
     }
-    *out = w.ptr;
-    return XT_OK;
+}
+
+// Caller-provided scratch (the allocation-free entry point): requests of
+// kind 0 are carved from it in order; other kinds are refused.
+struct Scratch {
+    char* base;
+    size_t cap;
+    size_t used;
+};
+
+int workspace(hipStream_t s, size_t bytes, void** out, int kind = 0, Scratch* sc = nullptr) {
+    if (sc) {
+        if (kind != 0)
+            return fail(XT_ERR_UNSUPPORTED,
+                        "this product configuration needs a split-K workspace, which the "
+                        "allocation-free entry point does not provide");
+        const size_t need = (bytes + 255) / 256 * 256;
+        if (sc->used + need > sc->cap)
+            return fail(XT_ERR_INVALID, "needs " + std::to_string(sc->used + need) +
+                                            " bytes of scratch, the static scratch holds " +
+                                            std::to_string(sc->cap));
+        *out = sc->base + sc->used;
+        sc->used += need;
+        return XT_OK;
+    }
+    std::string err;
+    const int st = ws_table().get(s, bytes, kind, kind == 1, out, &err);
+    return ws_status(st, err);
 }
 
 inline size_t align_up(size_t v, size_t a) { return (v + a - 1) / a * a; }
 
 // Split-K workspace of a stream: [counters: g_cnt_region bytes][planes].  The
-// counter region only grows by reallocating the whole buffer (zeroed).
+// counter region only grows by replacing every split-K buffer (zeroed).
+std::mutex g_cnt_mu;
 size_t g_cnt_region = 1 << 16;
 
-int splitk_workspace(hipStream_t s, size_t cbytes, size_t pbytes, void** out, size_t* region) {
+int splitk_workspace(hipStream_t s, size_t cbytes, size_t pbytes, void** out, size_t* region,
+                     Scratch* sc) {
     {
-        std::lock_guard<std::mutex> lk(g_ws_mu);
+        std::lock_guard<std::mutex> lk(g_cnt_mu);
         if (cbytes > g_cnt_region) {
             g_cnt_region = cbytes;
-            for (auto& kv : g_ws)
-                if (std::get<2>(kv.first) == 1) kv.second.cap = 0;  // force regrowth
+            ws_table().mark_stale(1);
         }
         *region = g_cnt_region;
     }
-    return workspace(s, *region + pbytes, out, 1);
+    return workspace(s, *region + pbytes, out, 1, sc);
 }
 
 int check_weights(const xt_weights* w) {
@@ -164,7 +193,7 @@ int run_product_int(const xt_weights* const* ws, int n, const int8_t* q, int ldq
 
 int run_product(const xt_weights* const* ws, int n, const int8_t* q, int ldq, const float* inv,
                 const int32_t* rowsum, int64_t M, float* const* ys, int32_t* acc,
-                hipStream_t s) {
+                hipStream_t s, Scratch* sc = nullptr) {
     const int fmt = ws[0]->fmt;
     if (xt::is_int_format(fmt)) return run_product_int(ws, n, q, ldq, inv, M, ys, acc, s);
     int ng_total = 0;
@@ -207,7 +236,7 @@ int run_product(const xt_weights* const* ws, int n, const int8_t* q, int ldq, co
             void* wsp = nullptr;
             size_t region = 0;
             const size_t pbytes = align_up((size_t)cfg.splitk * M * cols * sizeof(int32_t), 256);
-            if (int rc = splitk_workspace(s, 0, pbytes, &wsp, &region)) return rc;
+            if (int rc = splitk_workspace(s, 0, pbytes, &wsp, &region, sc)) return rc;
             a.part = reinterpret_cast<int32_t*>(static_cast<char*>(wsp) + region);
         }
         a.ldp = cols;
@@ -224,7 +253,7 @@ int run_product(const xt_weights* const* ws, int n, const int8_t* q, int ldq, co
         const size_t pbytes = align_up((size_t)cfg.splitk * M * cols * sizeof(int32_t), 256);
         void* wsp = nullptr;
         size_t region = 0;
-        if (int rc = splitk_workspace(s, cbytes, pbytes, &wsp, &region)) return rc;
+        if (int rc = splitk_workspace(s, cbytes, pbytes, &wsp, &region, sc)) return rc;
         a.cnt = static_cast<unsigned*>(wsp);
         a.part = reinterpret_cast<int32_t*>(static_cast<char*>(wsp) + region);
         a.ldp = cols;
@@ -361,7 +390,7 @@ int gemv_fused_quant(const xt_weights* const* ws, int n, const float* x, int64_t
 }
 
 int linear_f32(const xt_weights* const* ws, int n, const float* x, int64_t M, float* const* ys,
-               int mode, hipStream_t s) {
+               int mode, hipStream_t s, Scratch* sc = nullptr) {
     if (int rc = check_group(ws, n, x, M, ys)) return rc;
     if (mode != XT_QUANT_AVX512 && mode != XT_QUANT_SCALAR)
         return fail(XT_ERR_INVALID, "unknown quantisation mode");
@@ -373,7 +402,7 @@ int linear_f32(const xt_weights* const* ws, int n, const float* x, int64_t M, fl
     const size_t qbytes = align_up((size_t)M * kpad, 256);
     const size_t fbytes = align_up((size_t)M * 4, 256);
     void* wsp = nullptr;
-    if (int rc = workspace(s, qbytes + 2 * fbytes, &wsp)) return rc;
+    if (int rc = workspace(s, qbytes + 2 * fbytes, &wsp, 0, sc)) return rc;
     int8_t* q = static_cast<int8_t*>(wsp);
     float* inv = reinterpret_cast<float*>(static_cast<char*>(wsp) + qbytes);
     int32_t* rowsum = wants_rowsum(ws[0], M)
@@ -381,7 +410,7 @@ int linear_f32(const xt_weights* const* ws, int n, const float* x, int64_t M, fl
                           : nullptr;
     hipError_t e = xt::launch_quantize(x, K, (int)M, (int)K, q, (int)kpad, inv, rowsum, mode, s);
     if (e != hipSuccess) return hip_fail(e, "quantize launch");
-    return run_product(ws, n, q, (int)kpad, inv, rowsum, M, ys, nullptr, s);
+    return run_product(ws, n, q, (int)kpad, inv, rowsum, M, ys, nullptr, s, sc);
 }
 
 int launch_mid(const xt::MidArgs& a, int64_t M, hipStream_t s) {
@@ -753,6 +782,11 @@ int xt_ternary_mlp_f32(const xt_weights* gate, const xt_weights* up, const xt_we
                     : XT_ACT_SILU_MUL;
     return mlp_run(gate, up, down, norm_weight, eps, act, mode, M, y,
                    static_cast<hipStream_t>(stream), x, true, nullptr);
+}
+
+int xt_workspace_release(void) {
+    std::string err;
+    return ws_status(ws_table().release_all(&err), err);
 }
 
 int xt_int_quantize_host(int bits, const float* w, int64_t out_dim, int64_t in_dim, void* out,

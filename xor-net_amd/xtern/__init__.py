@@ -103,6 +103,7 @@ _lib.xt_ternary_linear_q.argtypes = [_vp, _vp, _vp, _i64, _vp, _vp, _vp]
 _lib.xt_ternary_linear_q_rowsum.argtypes = [_vp, _vp, _vp, _vp, _i64, _vp, _vp, _vp]
 _lib.xt_ternary_linear_f32.argtypes = [_vp, _vp, _i64, _vp, ctypes.c_int, _vp]
 _lib.xt_ternary_linear_multi_q.argtypes = [_vp, ctypes.c_int, _vp, _vp, _i64, _vp, _vp]
+_lib.xt_workspace_release.argtypes = []
 _lib.xt_ternary_linear_multi_f32.argtypes = [_vp, ctypes.c_int, _vp, _i64, _vp, ctypes.c_int, _vp]
 
 
@@ -563,6 +564,11 @@ def linear_q(w, q, inv, acc=False, out=None, stream=None):
                                     _dev_ptr(a, torch.int32, "acc") if acc else None,
                                     _stream_ptr(stream)))
     return (y, a) if acc else y
+
+
+def workspace_release():
+    """Free the library's device workspaces (waits for the device)."""
+    _check(_lib.xt_workspace_release())
 
 
 def linear_f32(w, x, mode=XT_QUANT_AVX512, out=None, stream=None):
