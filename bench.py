@@ -129,6 +129,49 @@ class Graph:
         return a.elapsed_time(b) / (replays * self.n)
 
 
+def flush_mall(torch):
+    """Write 1 GiB (4x the 256 MB MALL) so no weights stay cached in it."""
+    t = torch.empty(1 << 30, dtype=torch.uint8, device="cuda")
+    t.fill_(1)
+    torch.cuda.synchronize()
+    del t
+
+
+def time_exact_steps(torch, xtern, wl, steps, warmup):
+    """`warmup` untimed steps, then exactly `steps` timed steps: one HIP graph
+    holding `steps` steps (step i on weight copy i mod ncopy), replayed once
+    between HIP events on its stream.  The warm-up steps run through their
+    own graph on other copies; then the MALL is flushed, so the timed steps
+    stream their weights from HBM even when `steps` is below the number of
+    copies.  A sleep kernel queued ahead of the start event keeps the GPU
+    busy while the host submits the graph, so the events bracket device
+    time.  Checks the last timed step's outputs against an eager run."""
+    ncopy = len(wl["sets"][0]["copies"])
+    g = Graph(torch, lambda i: run_steps(xtern, wl, 1, start_idx=i), steps)
+    if warmup > 0:
+        gw = Graph(torch, lambda i: run_steps(xtern, wl, 1, start_idx=(steps + i) % ncopy), warmup)
+        gw.g.replay()
+        gw.stream.synchronize()
+        del gw
+    flush_mall(torch)
+    with torch.cuda.stream(g.stream):
+        a = torch.cuda.Event(enable_timing=True)
+        b = torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(2_000_000)
+        a.record()
+        g.g.replay()
+        b.record()
+    b.synchronize()
+    ms = a.elapsed_time(b) / steps
+    got = [s["y"].clone() for s in wl["sets"]]
+    run_steps(xtern, wl, 1, start_idx=steps - 1)
+    torch.cuda.synchronize()
+    for s, y in zip(wl["sets"], got):
+        if not torch.equal(s["y"], y):
+            raise SystemExit("graph replay output differs from eager output")
+    return ms, steps
+
+
 def product_only(np, torch, xtern, wl, reps):
     """Average duration of one product launch per matrix: a HIP graph of
     back-to-back linear_q (forward_with_quantized) launches over the rotating
@@ -332,32 +375,98 @@ def mlp_block_c4(np, torch, xtern, rng, Ms=(1, 8), layers=30):
     return res
 
 
-def cpu_baseline(np, wl, budget_s=12.0):
+def host_cpu_info():
+    """CPU model, logical CPUs usable by this process, physical cores (unique
+    (package, core id) pairs of /proc/cpuinfo)."""
+    model, cores = "unknown", set()
+    phys = core = None
+    try:
+        for line in open("/proc/cpuinfo"):
+            k, _, v = line.partition(":")
+            k, v = k.strip(), v.strip()
+            if k == "model name" and model == "unknown":
+                model = v
+            elif k == "physical id":
+                phys = v
+            elif k == "core id":
+                core = v
+            elif not k and phys is not None and core is not None:
+                cores.add((phys, core))
+                phys = core = None
+        if phys is not None and core is not None:
+            cores.add((phys, core))
+    except OSError:
+        pass
+    try:
+        logical = len(os.sched_getaffinity(0))
+    except AttributeError:
+        logical = os.cpu_count() or 1
+    return {"model": model, "logical": logical, "physical_cores_host": len(cores) or None}
+
+
+def cpu_baseline(np, wl, rng, budget_s=6.0):
     """The oracle's restatement of the reference CPU path (TernaryLinear::forward
-    with the VNNI dot when the host has it) on the first `rows` tokens of each
-    matrix of the step, repeated until ~budget_s of CPU time."""
+    with the AVX-512 VNNI dot when the host has it, else the scalar dot) on
+    the host cores of the GPU box, in the same run:
+      c1  16-token samples of each C1 matrix, one task per token
+          (layers.rs:298-310), repeated for ~budget_s;
+      c0  the M = 1 GEMV (K=2560, N=6912) with the reference's row chunks of
+          max(ceil(N/T), 128) rows (layers.rs:284-296), repeated for ~budget_s/2;
+    each at T = min(nproc, 8) (the reference default, lib.rs:32-42) and at
+    every usable logical CPU (capped by OMP_NUM_THREADS when set)."""
     sys.path.insert(0, os.path.join(ROOT, "oracle"))
     import oracle
-    threads = min(os.cpu_count() or 1, 8)
+    info = host_cpu_info()
+    default_t = min(info["logical"], 8)
+    all_t = info["logical"]
+    if os.environ.get("OMP_NUM_THREADS", "").isdigit():
+        all_t = min(all_t, int(os.environ["OMP_NUM_THREADS"]))
     kernel = 1 if oracle.has_vnni() else 0
-    rows = 16  # tokens per sample: one per-token task each, as layers.rs:298-310
-    ops = 0
-    t_total = 0.0
-    reps = 0
-    while t_total < budget_s:
-        for s in wl["sets"]:
-            x = s["xh"][:rows]
+    isa = "avx512-vnni" if kernel else "scalar"
+
+    def c1(threads):
+        rows, ops, t_total, reps = 16, 0, 0.0, 0
+        while t_total < budget_s:
+            for s in wl["sets"]:
+                t0 = time.perf_counter()
+                oracle.linear_forward(0, s["K"], s["N"], s["xh"][:rows], s["ws"], wbytes=s["wb"],
+                                      threads=threads, kernel=kernel)
+                t_total += time.perf_counter() - t0
+                ops += 2 * rows * s["N"] * s["K"]
+            reps += 1
+        return ops / t_total / 1e12, reps, t_total
+
+    K, N = 2560, 6912
+    wb0, _ = tern_bytes(np, rng, N, K, 0)
+    ws0 = np.full(N, 0.8, np.float32)
+    x0 = rng.standard_normal((1, K)).astype(np.float32)
+    alg0 = N * K // 4 + 4 * K + 4 * N + 4 * N
+
+    def c0(threads):
+        times = []
+        t_total = 0.0
+        while t_total < budget_s / 2 or len(times) < 50:
             t0 = time.perf_counter()
-            oracle.linear_forward(0, s["K"], s["N"], x, s["ws"], wbytes=s["wb"],
-                                  threads=threads, kernel=kernel)
-            t_total += time.perf_counter() - t0
-            ops += 2 * rows * s["N"] * s["K"]
-        reps += 1
-    tops = ops / t_total / 1e12
-    return {"value": round(tops, 5), "unit": "TOPS (int8)", "cores": threads,
-            "kind": "port",
-            "sample": f"{reps} passes x {rows} tokens of each c1 matrix "
-                      f"({t_total:.1f} s), isa={'avx512-vnni' if kernel else 'scalar'}"}
+            oracle.linear_forward(0, K, N, x0, ws0, wbytes=wb0, threads=threads, kernel=kernel)
+            dt = time.perf_counter() - t0
+            times.append(dt)
+            t_total += dt
+        med = float(np.median(times))
+        return med * 1e6, alg0 / med / 1e9, len(times)
+
+    variants = []
+    for T in sorted({default_t, all_t}):
+        tops, reps, tt = c1(T)
+        us0, gbs0, n0 = c0(T)
+        variants.append({"threads": T, "c1_TOPS": round(tops, 5),
+                         "c1_sample": f"{reps} passes x 16 tokens of each c1 matrix ({tt:.1f} s)",
+                         "c0_us_per_call_median": round(us0, 1), "c0_GBs": round(gbs0, 2),
+                         "c0_calls": n0})
+    head = next(v for v in variants if v["threads"] == default_t)
+    return {"value": head["c1_TOPS"], "unit": "TOPS (int8)", "cores": default_t, "kind": "port",
+            "sample": head["c1_sample"] + f", isa={isa}", "isa": isa,
+            "cpu_model": info["model"], "logical_cpus": info["logical"],
+            "physical_cores_host": info["physical_cores_host"], "variants": variants}
 
 
 def recorded_traffic():
@@ -383,6 +492,57 @@ def copy_calibration(torch):
         b.copy_(a)
     torch.cuda.synchronize()
     print(json.dumps({"copy_bytes": n, "launches": 3}))
+
+
+def peaks(torch):
+    """On-box ceilings (libxtern_diag.so): a streaming read of 1 GiB (HBM
+    bound, 4x the MALL), single-launch reads of 4.4 MB (the C0 weight bytes)
+    over rotating buffers > 2x the MALL, launch to launch in a HIP graph, the
+    i8 MFMA rate of back-to-back 32x32x32 and 16x16x64 instructions, and the
+    launch-to-launch floor of an empty kernel.  HIP events on the launch
+    stream; one JSON line."""
+    import ctypes
+    lib = ctypes.CDLL(os.path.join(ROOT, "xor-net_amd", "xtern", "libxtern_diag.so"))
+    vp = ctypes.c_void_p
+    lib.xtd_read.argtypes = [vp, ctypes.c_size_t, ctypes.c_int, vp, vp]
+    lib.xtd_mfma_i8.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, vp, vp]
+    lib.xtd_empty.argtypes = [ctypes.c_int, ctypes.c_int, vp]
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
+    res = {}
+
+    def graph_ms(fn, n, replays=3):
+        g = Graph(torch, fn, n)
+        return g.time_ms(replays)
+
+    def sp():
+        return vp(torch.cuda.current_stream().cuda_stream)
+
+    big = torch.empty(1 << 30, dtype=torch.uint8, device="cuda").fill_(3)
+    for blocks in (1024, 2048, 4096):
+        ms = graph_ms(lambda i: lib.xtd_read(vp(big.data_ptr()), big.numel(), blocks,
+                                             vp(sink.data_ptr()), sp()), 4)
+        res[f"read_1GiB_blocks{blocks}_GBs"] = round(big.numel() / (ms * 1e-3) / 1e9, 1)
+    del big
+    torch.cuda.empty_cache()
+    nb = 4481536  # C0's weight bytes rounded to 16
+    copies = [torch.empty(nb, dtype=torch.uint8, device="cuda").fill_(i & 255)
+              for i in range(-(-2 * MALL_BYTES // nb))]
+    for blocks in (256, 512, 1088):
+        ms = graph_ms(lambda i: lib.xtd_read(vp(copies[i].data_ptr()), nb, blocks,
+                                             vp(sink.data_ptr()), sp()), len(copies))
+        res[f"read_4.4MB_blocks{blocks}_us"] = round(ms * 1e3, 3)
+        res[f"read_4.4MB_blocks{blocks}_GBs"] = round(nb / (ms * 1e-3) / 1e9, 1)
+    del copies
+    torch.cuda.empty_cache()
+    for shape, ops_per in ((32, 65536), (16, 32768)):
+        blocks, iters = 2048, 1000
+        ms = graph_ms(lambda i: lib.xtd_mfma_i8(shape, blocks, iters, vp(sink.data_ptr()), sp()), 2)
+        tops = blocks * 4 * 4 * iters * ops_per / (ms * 1e-3) / 1e12
+        res[f"mfma_i8_{shape}_TOPS"] = round(tops, 1)
+    for blocks in (1, 256, 1024):
+        ms = graph_ms(lambda i: lib.xtd_empty(blocks, 256, sp()), 200)
+        res[f"empty_kernel_grid{blocks}_us"] = round(ms * 1e3, 3)
+    print(json.dumps({"peaks": res}))
 
 
 def vendor_int8(np, torch, xtern, rng):
@@ -414,12 +574,14 @@ def vendor_int8(np, torch, xtern, rng):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=600)
+    ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="c1")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--copy-calibration", action="store_true")
+    ap.add_argument("--peaks", action="store_true",
+                    help="measure the on-box read / MFMA / launch ceilings and exit")
     ap.add_argument("--vendor-int8", action="store_true",
                     help="time the ROCm dense int8 GEMM beside the Pack4 product and exit")
     args = ap.parse_args()
@@ -435,6 +597,9 @@ def main():
     if args.copy_calibration:
         copy_calibration(torch)
         return
+    if args.peaks:
+        peaks(torch)
+        return
     rng = np.random.default_rng(1234)
     if args.vendor_int8:
         vendor_int8(np, torch, xtern, rng)
@@ -444,33 +609,12 @@ def main():
     log("setting up c1 weights (rotating copies) ...")
     wl = workload_c1(np, torch, xtern, rng)
 
-    # eager reference outputs, then the step graph (one step per weight copy)
+    # eager reference outputs, then the timed graph of exactly `steps` steps
     run_steps(xtern, wl, 1)
     torch.cuda.synchronize()
-    eager = [s["y"].clone() for s in wl["sets"]]
-    ncopy = len(wl["sets"][0]["copies"])
-    step_graph = Graph(torch, lambda i: run_steps(xtern, wl, 1, start_idx=i), ncopy)
-    replays = max(1, -(-args.steps // ncopy))
-    warm = max(1, -(-args.warmup // ncopy))
-    for _ in range(warm):
-        step_graph.g.replay()
-    step_graph.stream.synchronize()
-    # the last captured step used copy ncopy-1; recompute it eagerly to compare
-    run_steps(xtern, wl, 1, start_idx=ncopy - 1)
-    torch.cuda.synchronize()
-    check = [s["y"].clone() for s in wl["sets"]]
-    step_graph.g.replay()
-    step_graph.stream.synchronize()
-    for s, c in zip(wl["sets"], check):
-        if not torch.equal(s["y"], c):
-            raise SystemExit("graph replay output differs from eager output")
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    ms_step = step_graph.time_ms(replays)
-    wall = time.perf_counter() - t0
-    steps_timed = replays * ncopy
+    ms_step, steps_timed = time_exact_steps(torch, xtern, wl, args.steps, args.warmup)
     tops = wl["ops"] / (ms_step * 1e-3) / 1e12
-    log(f"step {ms_step * 1e3:.2f} us over {steps_timed} steps (wall {wall:.3f} s)")
+    log(f"step {ms_step * 1e3:.2f} us over {steps_timed} steps")
 
     prod_ms = product_only(np, torch, xtern, wl, reps=max(args.steps, 50))
     prod_ops = [2 * wl["M"] * s["N"] * s["K"] for s in wl["sets"]]
@@ -478,9 +622,12 @@ def main():
     tr = recorded_traffic()
     prod_tr = {k: v for k, v in (tr or {}).items() if k in ("gemm32s_up", "mm_down")}
     roof = {"bound": "mfma", "achieved": round(ach, 2), "peak": INT8_PEAK_TOPS,
-            "unit": "TFLOP/s", "frac": round(ach / INT8_PEAK_TOPS, 4),
+            "unit": "TOPS", "frac": round(ach / INT8_PEAK_TOPS, 4),
             "traffic": (sum(prod_tr.values()) // len(prod_tr)) if prod_tr else None,
             "traffic_per_launch": prod_tr or None,
+            "traffic_source": "profiles/pmc_traffic_c1.md (rocprofv3 --pmc FETCH_SIZE, "
+                              "WRITE_SIZE of the same kernels, copy-calibrated; not measured "
+                              "in this run)",
             "kernel": "product launches (gemm32s_kernel up, mm_kernel down)",
             "us_per_launch": {s["name"]: round(m * 1e3, 3) for s, m in zip(wl["sets"], prod_ms)}}
 
@@ -503,7 +650,7 @@ def main():
         out["configs"] += lm_head(np, torch, xtern, rng)
     if not args.no_cpu:
         log("cpu baseline ...")
-        out["cpu_baseline"] = cpu_baseline(np, wl)
+        out["cpu_baseline"] = cpu_baseline(np, wl, rng)
     print(json.dumps(out), flush=True)
 
 

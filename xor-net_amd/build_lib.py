@@ -51,6 +51,22 @@ def build_cpp_tests(verbose=False):
     return CPP_TEST_BIN
 
 
+DIAG_SRC = os.path.join(CSRC, "xtern_diag.hip")
+DIAG_OUT = os.path.join(HERE, "xtern", "libxtern_diag.so")
+
+
+def build_diag(verbose=False):
+    """libxtern_diag.so: the measurement kernels of bench.py --peaks (streaming
+    read, MFMA loop, empty launch); not part of the product ABI."""
+    cmd = [hipcc()] + HIPCC_FLAGS + [DIAG_SRC, "-o", DIAG_OUT]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError("hipcc (diag) failed:\n" + res.stderr)
+    return DIAG_OUT
+
+
 def build(verbose=False):
     cmd = [hipcc()] + HIPCC_FLAGS + [os.path.join(CSRC, s) for s in SOURCES] + ["-o", OUT]
     if verbose:
@@ -68,3 +84,4 @@ def build(verbose=False):
 if __name__ == "__main__":
     print(build(verbose="-q" not in sys.argv))
     print(build_cpp_tests(verbose="-q" not in sys.argv))
+    print(build_diag(verbose="-q" not in sys.argv))
