@@ -604,8 +604,11 @@ def main():
     if args.vendor_int8:
         vendor_int8(np, torch, xtern, rng)
         return
+    if args.workload == "c0":
+        print(json.dumps({"gemv_m1": gemv_m1(np, torch, xtern, rng)}))
+        return
     if args.workload != "c1":
-        raise SystemExit("only the c1 workload is wired as the headline step")
+        raise SystemExit("workloads: c1 (the headline step), c0 (the M=1 GEMV alone)")
     log("setting up c1 weights (rotating copies) ...")
     wl = workload_c1(np, torch, xtern, rng)
 
