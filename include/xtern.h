@@ -257,6 +257,20 @@ int xt_ternary_linear_q_rowsum(const xt_weights* w, const int8_t* q, const float
 int xt_ternary_linear_f32(const xt_weights* w, const float* x, int64_t M, float* y,
                           int mode, void* stream);
 
+/* xt_ternary_linear_f32 without any device allocation: no reference
+ * counterpart.  For callers that cannot allocate (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  The
+ * quantised rows go to a static device scratch of 8 MiB per GPU (held until
+ * the process ends) instead of a workspace: A + 2 * B bytes must fit, with
+ * A = M * ceil(in_dim / chunk) * chunk (chunk = 256, Pack5 320) and B = 4 * M,
+ * each rounded up to a multiple of 256, or the call fails with
+ * XT_ERR_INVALID.  A forced split-K configuration (XTERN_CONFIG) fails with
+ * XT_ERR_UNSUPPORTED.  Every call on one GPU shares that
+ * scratch: calls that overlap on one GPU (other streams, other threads) race;
+ * the caller serialises them.  Results equal xt_ternary_linear_f32's. */
+int xt_ternary_linear_f32_noalloc(const xt_weights* w, const float* x, int64_t M, float* y,
+                                  int mode, void* stream);
+
 /* Several projections that share one input (same in_dim and format) in one
  * launch: ys[p] [M][out_dim(p)] for p < n (n <= 4).  The input is quantised
  * once.  Replaces TernaryLinear::fused_forward_qkv (src/bit1_58/layers.rs:347-424)

@@ -709,6 +709,19 @@ int xt_ternary_linear_f32(const xt_weights* w, const float* x, int64_t M, float*
     return linear_f32(ws, 1, x, M, ys, mode, static_cast<hipStream_t>(stream));
 }
 
+int xt_ternary_linear_f32_noalloc(const xt_weights* w, const float* x, int64_t M, float* y,
+                                  int mode, void* stream) {
+    if (check_weights(w)) return XT_ERR_INVALID;
+    void* base = nullptr;
+    size_t cap = 0;
+    hipError_t e = xt::scratch_region(&base, &cap);
+    if (e != hipSuccess) return hip_fail(e, "static scratch address");
+    Scratch sc{static_cast<char*>(base), cap, 0};
+    const xt_weights* ws[1] = {w};
+    float* ys[1] = {y};
+    return linear_f32(ws, 1, x, M, ys, mode, static_cast<hipStream_t>(stream), &sc);
+}
+
 int xt_ternary_linear_multi_q(const xt_weights* const* ws, int n, const int8_t* q,
                               const float* inv_scale, int64_t M, float* const* ys, void* stream) {
     return linear_q(ws, n, q, inv_scale, nullptr, M, ys, nullptr, static_cast<hipStream_t>(stream));

@@ -131,6 +131,9 @@ struct MidArgs {
 constexpr int kActIdentity = 100;  // MidArgs::act: no activation (up unused)
 int mid_max_cols();
 hipError_t launch_mlp_mid(const MidArgs& a, int M, hipStream_t s);
+// Address (on the current device) and size of the static device scratch used
+// by the allocation-free entry point; resolved once per device.
+hipError_t scratch_region(void** ptr, size_t* bytes);
 // HF prepacked striped bytes [N/f][K] (device) -> tiles (device).
 hipError_t launch_hf_tiles(int fmt, const uint8_t* stored, int64_t K, int64_t N, uint8_t* tiles,
                            hipStream_t s);

@@ -11,6 +11,7 @@
 #include <stdio.h>
 #include <stdlib.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "../../include/xtern.h"
@@ -265,6 +266,33 @@ hipError_t launch_quantize(const float* x, int64_t ldx, int M, int K, int8_t* q,
     hipLaunchKernelGGL(quantize_kernel, dim3(M), dim3(256), 0, s, x, ldx, K, q, ldq, inv, rowsum,
                        mode);
     return hipGetLastError();
+}
+
+// Static scratch of the allocation-free entry point: device memory that the
+// library never allocates at run time.  Each GPU holds its own copy; host
+// code reaches it only through the address hipGetSymbolAddress returns for
+// the current device (the array's name is a host-side stand-in).  Every call
+// on one GPU shares it: calls that overlap on one GPU race.
+constexpr size_t kScratchBytes = (size_t)8 << 20;
+static __device__ __align__(256) uint8_t scratch[kScratchBytes];
+
+hipError_t scratch_region(void** ptr, size_t* bytes) {
+    static std::mutex mu;
+    static void* addr[64] = {};
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    if (dev < 0 || dev >= 64) return hipErrorInvalidDevice;
+    std::lock_guard<std::mutex> lk(mu);
+    if (!addr[dev]) {
+        void* p = nullptr;
+        e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return e;
+        addr[dev] = p;
+    }
+    *ptr = addr[dev];
+    *bytes = kScratchBytes;
+    return hipSuccess;
 }
 
 hipError_t launch_rowsum(const int8_t* qin, int64_t ldin, int M, int K, int8_t* qout, int ldout,

@@ -104,6 +104,7 @@ _lib.xt_ternary_linear_q_rowsum.argtypes = [_vp, _vp, _vp, _vp, _i64, _vp, _vp, 
 _lib.xt_ternary_linear_f32.argtypes = [_vp, _vp, _i64, _vp, ctypes.c_int, _vp]
 _lib.xt_ternary_linear_multi_q.argtypes = [_vp, ctypes.c_int, _vp, _vp, _i64, _vp, _vp]
 _lib.xt_workspace_release.argtypes = []
+_lib.xt_ternary_linear_f32_noalloc.argtypes = [_vp, _vp, _i64, _vp, ctypes.c_int, _vp]
 _lib.xt_ternary_linear_multi_f32.argtypes = [_vp, ctypes.c_int, _vp, _i64, _vp, ctypes.c_int, _vp]
 
 
@@ -564,6 +565,19 @@ def linear_q(w, q, inv, acc=False, out=None, stream=None):
                                     _dev_ptr(a, torch.int32, "acc") if acc else None,
                                     _stream_ptr(stream)))
     return (y, a) if acc else y
+
+
+def linear_f32_noalloc(w, x, mode=XT_QUANT_AVX512, out=None, stream=None):
+    """linear_f32 through xt_ternary_linear_f32_noalloc (static device scratch,
+    no allocation in the library; calls overlapping on one GPU race)."""
+    torch = _torch()
+    x2 = x.reshape(-1, x.shape[-1])
+    M = x2.shape[0]
+    y = out if out is not None else torch.empty((M, w.out_dim), dtype=torch.float32, device=x.device)
+    _check(_lib.xt_ternary_linear_f32_noalloc(w.handle, _dev_ptr(x2, torch.float32, "x"), M,
+                                              _dev_ptr(y, torch.float32, "y"), mode,
+                                              _stream_ptr(stream)))
+    return y
 
 
 def workspace_release():
