@@ -1,0 +1,174 @@
+"""The decode stack (xt_stack_*: every projection of several layers in one
+persistent launch) against the oracle, bit for bit.  Layers follow the
+BitNet-2B decode step (q/k/v fused, o, gate/up fused, down; reference
+src/models/llama/mod.rs:420-470) with the real dependency of the residual
+stream: layer L's q/k/v and gate/up read layer L-1's down output, written
+inside the same launch.  Each op's expected output is the oracle's
+TernaryLinear::forward (layers.rs:262-313) of the oracle's own input chain."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+import xtern
+
+pytestmark = pytest.mark.gpu
+
+BITNET = {"q": (2560, 2560), "k": (2560, 640), "v": (2560, 640), "o": (2560, 2560),
+          "gate": (2560, 6912), "up": (2560, 6912), "down": (6912, 2560)}
+SMALL = {"q": (256, 96), "k": (256, 32), "v": (256, 48), "o": (256, 256),
+         "gate": (256, 300), "up": (256, 300), "down": (300 + 4, 256)}
+
+
+def log(msg):
+    print(f"[case] {msg}", flush=True)
+
+
+def pack4(t):
+    c = (t + 1).astype(np.uint8)
+    pad = (-t.shape[1]) % 4
+    if pad:
+        c = np.concatenate([c, np.ones((t.shape[0], pad), np.uint8)], axis=1)
+    g = c.reshape(t.shape[0], -1, 4)
+    return (g[..., 0] | (g[..., 1] << 2) | (g[..., 2] << 4) | (g[..., 3] << 6)).astype(np.uint8).ravel()
+
+
+class Mat:
+    def __init__(self, rng, K, N, sparse=False):
+        p0 = rng.uniform(0.3, 0.7)
+        u = rng.random((N, K))
+        t = np.where(u < p0, 0, np.where(rng.random((N, K)) < 0.5, -1, 1)).astype(np.int8)
+        self.K, self.N, self.t = K, N, t
+        self.wb = pack4(t)
+        self.ws = rng.uniform(0.02, 0.1, N).astype(np.float32)
+        if sparse:
+            blob = np.frombuffer(xtern.encode_sparse_tensor(t, K, N)[0], np.uint8)
+            self.w = xtern.DeviceWeights(xtern.XT_XORSPARSE, K, N, blob, self.ws)
+        else:
+            self.w = xtern.DeviceWeights(xtern.XT_PACK4, K, N, self.wb, self.ws)
+
+    def ref(self, x, mode):
+        return oracle.linear_forward(0, self.K, self.N, x, self.ws, wbytes=self.wb, quant_mode=mode)[0]
+
+
+def build(rng, shapes, layers, M, order, sparse_down=False):
+    """Returns (ops for xtern.Stack, list of (op index, [outputs], [expected]))."""
+    dev = "cuda"
+    f32 = torch.float32
+    mats = [{n: Mat(rng, K, N, sparse=(sparse_down and n == "down")) for n, (K, N) in shapes.items()}
+            for _ in range(layers)]
+    Kd = shapes["down"][0]
+    Ka = shapes["q"][0]
+    ops, checks = [], []
+    x0 = torch.from_numpy(rng.standard_normal((M, Ka)).astype(np.float32)).to(dev)
+    h_prev, dep_prev = x0, None
+    for L, m in enumerate(mats):
+        xa = torch.from_numpy(rng.standard_normal((M, Ka)).astype(np.float32) * 2).to(dev)
+        xd = torch.from_numpy(rng.standard_normal((M, Kd)).astype(np.float32)).to(dev)
+        outs = {n: torch.full((M, m[n].N), float("nan"), dtype=f32, device=dev) for n in m}
+        down_op = ([m["down"].w], xd, [outs["down"]], None, ["down"], xd)
+        qkv_op = ([m["q"].w, m["k"].w, m["v"].w], h_prev, [outs["q"], outs["k"], outs["v"]], "prev",
+                  ["q", "k", "v"], h_prev)
+        o_op = ([m["o"].w], xa, [outs["o"]], None, ["o"], xa)
+        gu_op = ([m["gate"].w, m["up"].w], h_prev, [outs["gate"], outs["up"]], "prev", ["gate", "up"],
+                 h_prev)
+        seq = [down_op, qkv_op, o_op, gu_op] if order == "down_first" else [qkv_op, o_op, gu_op, down_op]
+        for ws, x, ys, dep, names, xin in seq:
+            d = dep_prev if dep == "prev" else None
+            ops.append((ws, x, ys, d))
+            checks.append((len(ops) - 1, names, ys, xin, m))
+            if names == ["down"]:
+                down_idx = len(ops) - 1
+        h_prev, dep_prev = outs["down"], down_idx
+    return ops, checks
+
+
+def expected(checks, mode):
+    """Oracle outputs in op order (inputs of dependent ops are the oracle's
+    own outputs of the op they depend on)."""
+    got = {}
+    exp = []
+    for idx, names, ys, xin, m in checks:
+        key = xin.data_ptr()
+        x = got.get(key)
+        if x is None:
+            x = xin.cpu().numpy()
+        e = [m[n].ref(x, mode) for n in names]
+        for y, v in zip(ys, e):
+            got[y.data_ptr()] = v
+        exp.append(e)
+    return exp
+
+
+def compare(checks, exp, tag):
+    for (idx, names, ys, _, _), e in zip(checks, exp):
+        for n, y, v in zip(names, ys, e):
+            g = y.cpu().numpy()
+            assert np.array_equal(g.view(np.int32), v.view(np.int32)), \
+                f"{tag}: op {idx} {n}: {int((g != v).sum())} of {g.size} outputs differ"
+
+
+CASES = [("bitnet_m1_down_first", BITNET, 2, 1, "down_first", xtern.XT_QUANT_AVX512),
+         ("bitnet_m1_chain", BITNET, 2, 1, "chain", xtern.XT_QUANT_AVX512),
+         ("bitnet_m8_chain", BITNET, 2, 8, "chain", xtern.XT_QUANT_SCALAR),
+         ("bitnet_m32_down_first", BITNET, 1, 32, "down_first", xtern.XT_QUANT_AVX512),
+         ("small_m1", SMALL, 4, 1, "chain", xtern.XT_QUANT_SCALAR),
+         ("small_m3", SMALL, 4, 3, "chain", xtern.XT_QUANT_AVX512),
+         ("small_m17", SMALL, 3, 17, "down_first", xtern.XT_QUANT_SCALAR)]
+
+
+@pytest.mark.parametrize("name,shapes,layers,M,order,mode", CASES, ids=[c[0] for c in CASES])
+def test_stack_matches_oracle(name, shapes, layers, M, order, mode):
+    log(f"stack {name}: layers={layers} M={M} order={order} mode={mode}")
+    rng = np.random.default_rng(hash(name) & 0xffff)
+    ops, checks = build(rng, shapes, layers, M, order, sparse_down=(M == 3))
+    exp = expected(checks, mode)
+    st = xtern.Stack(ops, M, mode)
+    for rep in range(3):  # repeated launches: the counters reset themselves
+        for _, _, ys, _, _ in checks:
+            for y in ys:
+                y.fill_(float("nan"))
+        st.run()
+        torch.cuda.synchronize()
+        assert not st.gave_up()
+        compare(checks, exp, f"run {rep}")
+
+
+def test_stack_in_graph_replays():
+    log("stack graph replay")
+    rng = np.random.default_rng(5)
+    ops, checks = build(rng, SMALL, 3, 2, "chain")
+    exp = expected(checks, xtern.XT_QUANT_AVX512)
+    st = xtern.Stack(ops, 2)
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        st.run(stream=s)
+    s.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        st.run(stream=s)
+    for rep in range(3):
+        for _, _, ys, _, _ in checks:
+            for y in ys:
+                y.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        compare(checks, exp, f"replay {rep}")
+    assert not st.gave_up()
+
+
+def test_stack_rejects_bad_ops():
+    log("stack argument errors")
+    rng = np.random.default_rng(1)
+    m = Mat(rng, 256, 32)
+    x = torch.zeros((1, 256), device="cuda")
+    y = torch.zeros((1, 32), device="cuda")
+    with pytest.raises(xtern.XternError):
+        xtern.Stack([([m.w], x, [y], 0)], 1)          # dep on itself
+    with pytest.raises(xtern.XternError):
+        xtern.Stack([([m.w], x, [y], None)], 33)      # M above 32
+    p5 = xtern.DeviceWeights(xtern.XT_PACK5, 256, 32,
+                             np.concatenate([xtern.pack_ternary5(r) for r in m.t]), m.ws)
+    with pytest.raises(xtern.XternError):
+        xtern.Stack([([p5], x, [y], None)], 1)        # Pack5 not on the stack

@@ -802,6 +802,142 @@ int xt_workspace_release(void) {
     return ws_status(ws_table().release_all(&err), err);
 }
 
+struct xt_stack {
+    xt::StackArgs args;
+    int blocks;
+    int device;
+    void* dev_mem;  // ops, items, counters, scratch (one allocation)
+};
+
+int xt_stack_create(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stack** out) {
+    if (!out) return fail(XT_ERR_INVALID, "out is NULL");
+    *out = nullptr;
+    if (!ops || nops < 1) return fail(XT_ERR_INVALID, "need at least one op");
+    if (nops > 4095) return fail(XT_ERR_UNSUPPORTED, "at most 4095 ops per stack");
+    if (M < 1 || M > 32) return fail(XT_ERR_UNSUPPORTED, "stack M must be 1..32");
+    if (mode != XT_QUANT_AVX512 && mode != XT_QUANT_SCALAR)
+        return fail(XT_ERR_INVALID, "unknown quantisation mode");
+    const int rgi = xt::kStackRowGroups;
+    std::vector<xt::StackOpDev> dops((size_t)nops);
+    std::vector<uint32_t> items;
+    size_t scratch = 0;
+    std::vector<size_t> qoff((size_t)nops);
+    for (int i = 0; i < nops; ++i) {
+        const xt_stack_op& op = ops[i];
+        const std::string at = "op " + std::to_string(i) + ": ";
+        if (op.n < 1 || op.n > 4) return fail(XT_ERR_INVALID, at + "n must be 1..4");
+        if (!op.x) return fail(XT_ERR_INVALID, at + "x is NULL");
+        if (op.dep < -1 || op.dep >= i)
+            return fail(XT_ERR_INVALID, at + "dep must be -1 or an earlier op");
+        xt::StackOpDev& d = dops[(size_t)i];
+        memset(&d, 0, sizeof d);
+        int blocks = 0;
+        for (int p = 0; p < op.n; ++p) {
+            const xt_weights* w = op.w[p];
+            if (!w || !op.y[p]) return fail(XT_ERR_INVALID, at + "NULL weights or output");
+            if (w->fmt != XT_PACK4 && w->fmt != XT_XORSPARSE)
+                return fail(XT_ERR_UNSUPPORTED, at + "stack weights must be Pack4 or XorSparse");
+            if (w->K != op.w[0]->K) return fail(XT_ERR_INVALID, at + "projections must share in_dim");
+            if (w->K % 4 != 0 || w->nch > xt::stack_max_chunks())
+                return fail(XT_ERR_UNSUPPORTED, at + "in_dim must be a multiple of 4 and at most " +
+                                                    std::to_string(xt::stack_max_chunks() * 256));
+            d.tiles[p] = w->tiles;
+            d.ws[p] = w->ws;
+            d.y[p] = op.y[p];
+            d.N[p] = (int)w->N;
+            blocks += (int)(((w->N + 15) / 16 + rgi - 1) / rgi);
+            d.gend[p] = blocks;
+        }
+        d.nproj = op.n;
+        d.K = (int)op.w[0]->K;
+        d.nch = (int)op.w[0]->nch;
+        d.ldq = d.nch * 256;
+        d.x = op.x;
+        d.dep = op.dep;
+        d.nq = M > 1 ? (int)M : 0;
+        d.ngemv = blocks;
+        if (d.nq + blocks >= (1 << 20)) return fail(XT_ERR_UNSUPPORTED, at + "too many rows");
+        for (int t = 0; t < d.nq + blocks; ++t) items.push_back(((uint32_t)i << 20) | (uint32_t)t);
+        if (M > 1) {
+            qoff[(size_t)i] = scratch;
+            scratch += align_up((size_t)M * d.ldq, 256) + align_up((size_t)M * 4, 256);
+        }
+    }
+    int dev = 0, cus = 0, per_cu = 0;
+    XT_HIP(hipGetDevice(&dev));
+    XT_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    XT_HIP(xt::stack_blocks_per_cu(&per_cu));
+    if (per_cu < 1) return fail(XT_ERR_UNSUPPORTED, "stack kernel does not fit a CU");
+    const size_t ops_b = align_up(sizeof(xt::StackOpDev) * nops, 256);
+    const size_t items_b = align_up(items.size() * 4, 256);
+    const size_t ctr_b = (size_t)(4 + 2 * nops) * 128;
+    char* mem = nullptr;
+    hipError_t e = hipMalloc(reinterpret_cast<void**>(&mem), ops_b + items_b + ctr_b + scratch);
+    if (e != hipSuccess) return fail(XT_ERR_NOMEM, std::string("stack allocation: ") + hipGetErrorString(e));
+    char* sc = mem + ops_b + items_b + ctr_b;
+    for (int i = 0; i < nops && M > 1; ++i) {
+        xt::StackOpDev& d = dops[(size_t)i];
+        d.q = reinterpret_cast<int8_t*>(sc + qoff[(size_t)i]);
+        d.inv = reinterpret_cast<float*>(sc + qoff[(size_t)i] + align_up((size_t)M * d.ldq, 256));
+    }
+    e = hipMemcpy(mem, dops.data(), sizeof(xt::StackOpDev) * nops, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(mem + ops_b, items.data(), items.size() * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemset(mem + ops_b + items_b, 0, ctr_b);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        (void)hipFree(mem);
+        return hip_fail(e, "stack upload");
+    }
+    xt_stack* st = new (std::nothrow) xt_stack();
+    if (!st) {
+        (void)hipFree(mem);
+        return fail(XT_ERR_NOMEM, "stack handle");
+    }
+    st->args.ops = reinterpret_cast<const xt::StackOpDev*>(mem);
+    st->args.items = reinterpret_cast<const uint32_t*>(mem + ops_b);
+    st->args.ctr = reinterpret_cast<unsigned*>(mem + ops_b + items_b);
+    st->args.nitems = (int)items.size();
+    st->args.nops = nops;
+    st->args.M = (int)M;
+    st->args.mode = mode;
+    // polls (about a microsecond each) before a dependency wait gives up
+    const char* sl = getenv("XTERN_STACK_SPIN_LIMIT");
+    st->args.spin_limit = sl ? atoi(sl) : (1 << 20);
+    st->blocks = std::min(cus * per_cu, (int)items.size());
+    st->device = dev;
+    st->dev_mem = mem;
+    *out = st;
+    return XT_OK;
+}
+
+int xt_stack_run(const xt_stack* st, void* stream) {
+    if (!st) return fail(XT_ERR_INVALID, "stack is NULL");
+    hipError_t e = xt::launch_stack(st->args, st->blocks, static_cast<hipStream_t>(stream));
+    if (e != hipSuccess) return hip_fail(e, "stack launch");
+    return XT_OK;
+}
+
+int xt_stack_check(xt_stack* st, int* gave_up) {
+    if (!st || !gave_up) return fail(XT_ERR_INVALID, "NULL argument");
+    XT_HIP(hipDeviceSynchronize());
+    unsigned flag = 0;
+    unsigned* slot = st->args.ctr + 2 * 32;  // the error slot
+    XT_HIP(hipMemcpy(&flag, slot, sizeof flag, hipMemcpyDeviceToHost));
+    if (flag) XT_HIP(hipMemset(slot, 0, sizeof flag));
+    *gave_up = flag ? 1 : 0;
+    return XT_OK;
+}
+
+int xt_stack_destroy(xt_stack* st) {
+    if (!st) return XT_OK;
+    hipError_t e = hipDeviceSynchronize();
+    hipError_t e2 = hipFree(st->dev_mem);
+    delete st;
+    if (e != hipSuccess) return hip_fail(e, "stack destroy");
+    if (e2 != hipSuccess) return hip_fail(e2, "stack destroy");
+    return XT_OK;
+}
+
 int xt_int_quantize_host(int bits, const float* w, int64_t out_dim, int64_t in_dim, void* out,
                          float* scales) {
     if (bits != 8 && bits != 4) return fail(XT_ERR_INVALID, "bits must be 8 or 4");

@@ -134,6 +134,34 @@ hipError_t launch_mlp_mid(const MidArgs& a, int M, hipStream_t s);
 // Address (on the current device) and size of the static device scratch used
 // by the allocation-free entry point; resolved once per device.
 hipError_t scratch_region(void** ptr, size_t* bytes);
+// Persistent decode stack (xtern_stack.hip): one launch over a list of ops.
+constexpr int kStackRowGroups = 4;  // 16-row groups per GEMV item
+struct StackOpDev {
+    const uint8_t* tiles[4];  // Pack4 tiles of each projection
+    const float* ws[4];
+    float* y[4];              // [M][N[p]] outputs
+    const float* x;           // [M][K] f32 input
+    int8_t* q;                // [M][ldq] quantised input (M > 1), launch scratch
+    float* inv;               // [M]
+    int N[4];
+    int gend[4];              // cumulative GEMV items per projection
+    int nproj, K, nch, ldq;
+    int dep;                  // op whose outputs x reads (wait for all its GEMV items), or -1
+    int nq;                   // quantiser items (M > 1: M, else 0)
+    int ngemv;                // GEMV items
+    int pad;
+};
+struct StackArgs {
+    const StackOpDev* ops;
+    const uint32_t* items;    // op << 20 | item index within the op
+    unsigned* ctr;            // (4 + 2 * nops) slots of 128 bytes, zero between launches
+    int nitems, nops, M, mode;
+    int spin_limit;           // polls before a dependency wait gives up
+};
+int stack_threads();
+int stack_max_chunks();  // chunks of K an op may have (4 per wave)
+hipError_t launch_stack(const StackArgs& a, int blocks, hipStream_t s);
+hipError_t stack_blocks_per_cu(int* n);
 // HF prepacked striped bytes [N/f][K] (device) -> tiles (device).
 hipError_t launch_hf_tiles(int fmt, const uint8_t* stored, int64_t K, int64_t N, uint8_t* tiles,
                            hipStream_t s);

@@ -108,6 +108,19 @@ _lib.xt_ternary_linear_f32_noalloc.argtypes = [_vp, _vp, _i64, _vp, ctypes.c_int
 _lib.xt_ternary_linear_multi_f32.argtypes = [_vp, ctypes.c_int, _vp, _i64, _vp, ctypes.c_int, _vp]
 
 
+class _StackOp(ctypes.Structure):
+    """struct xt_stack_op (include/xtern.h)."""
+    _fields_ = [("w", _vp * 4), ("n", ctypes.c_int), ("x", _vp), ("y", _vp * 4),
+                ("dep", ctypes.c_int)]
+
+
+_lib.xt_stack_create.argtypes = [ctypes.POINTER(_StackOp), ctypes.c_int, _i64, ctypes.c_int,
+                                 ctypes.POINTER(_vp)]
+_lib.xt_stack_run.argtypes = [_vp, _vp]
+_lib.xt_stack_check.argtypes = [_vp, ctypes.POINTER(ctypes.c_int)]
+_lib.xt_stack_destroy.argtypes = [_vp]
+
+
 class XternError(RuntimeError):
     """A libxtern call returned a negative status (message from xt_last_error)."""
 
@@ -702,3 +715,43 @@ def linear_multi_q(ws, q, inv, stream=None):
 
 from .layers import (TernaryLinear, DynamicLinear, TernaryRep, FastRmsNorm, Mlp,  # noqa: E402,F401
                      Int8Linear, Int4Linear)
+
+
+class Stack:
+    """A decode stack (xt_stack_*): ops = [(weights list, x, ys list, dep)],
+    x [M, in_dim] f32 and ys [M, out_dim] f32 device tensors that the stack
+    keeps referencing; run() is one launch over every op."""
+
+    def __init__(self, ops, M, mode=XT_QUANT_AVX512):
+        torch = _torch()
+        arr = (_StackOp * len(ops))()
+        self._keep = []
+        for i, (ws, x, ys, dep) in enumerate(ops):
+            if len(ws) != len(ys) or not 1 <= len(ws) <= 4:
+                raise XternError(XT_ERR_INVALID, f"op {i}: need 1..4 weights and as many outputs")
+            o = arr[i]
+            o.n = len(ws)
+            o.x = _dev_ptr(x, torch.float32, "x").value
+            o.dep = -1 if dep is None else int(dep)
+            for p, (w, y) in enumerate(zip(ws, ys)):
+                o.w[p] = w.handle.value
+                o.y[p] = _dev_ptr(y, torch.float32, "y").value
+            self._keep += [x] + list(ys) + list(ws)
+        h = ctypes.c_void_p()
+        _check(_lib.xt_stack_create(arr, len(ops), M, mode, ctypes.byref(h)))
+        self.handle = h
+
+    def run(self, stream=None):
+        _check(_lib.xt_stack_run(self.handle, _stream_ptr(stream)))
+
+    def gave_up(self):
+        """Wait for the device; True if a dependency wait gave up since the
+        last check (then those runs' outputs are not valid)."""
+        f = ctypes.c_int()
+        _check(_lib.xt_stack_check(self.handle, ctypes.byref(f)))
+        return bool(f.value)
+
+    def __del__(self):
+        if getattr(self, "handle", None):
+            _lib.xt_stack_destroy(self.handle)
+            self.handle = None
