@@ -813,13 +813,17 @@ int xt_stack_create(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_st
     if (!out) return fail(XT_ERR_INVALID, "out is NULL");
     *out = nullptr;
     if (!ops || nops < 1) return fail(XT_ERR_INVALID, "need at least one op");
-    if (nops > 4095) return fail(XT_ERR_UNSUPPORTED, "at most 4095 ops per stack");
+    const int max_ops = std::min<int>(xt::kStackMaxOps, xt::kStackDescLdsBytes / sizeof(xt::StackOpDev));
+    if (nops > max_ops)
+        return fail(XT_ERR_UNSUPPORTED, "at most " + std::to_string(max_ops) +
+                                            " ops per stack (split longer lists into several stacks)");
     if (M < 1 || M > 32) return fail(XT_ERR_UNSUPPORTED, "stack M must be 1..32");
     if (mode != XT_QUANT_AVX512 && mode != XT_QUANT_SCALAR)
         return fail(XT_ERR_INVALID, "unknown quantisation mode");
-    const int rgi = xt::kStackRowGroups;
+    const int rq = xt::stack_rows_per_quant_item();
+    const bool one = xt::stack_pipelined((int)M);  // M = 1: rows quantised once per op
+    int slots = 0;
     std::vector<xt::StackOpDev> dops((size_t)nops);
-    std::vector<uint32_t> items;
     size_t scratch = 0;
     std::vector<size_t> qoff((size_t)nops);
     for (int i = 0; i < nops; ++i) {
@@ -831,6 +835,10 @@ int xt_stack_create(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_st
             return fail(XT_ERR_INVALID, at + "dep must be -1 or an earlier op");
         xt::StackOpDev& d = dops[(size_t)i];
         memset(&d, 0, sizeof d);
+        // row groups per GEMV item (the M = 1 pipeline takes 8 for short K)
+        int rgi = xt::kStackRowGroups;
+        if (one) slots = std::max(slots, xt::stack_one_slots((int)op.w[0]->nch, &rgi));
+        d.rg = rgi;
         int blocks = 0;
         for (int p = 0; p < op.n; ++p) {
             const xt_weights* w = op.w[p];
@@ -841,6 +849,8 @@ int xt_stack_create(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_st
             if (w->K % 4 != 0 || w->nch > xt::stack_max_chunks())
                 return fail(XT_ERR_UNSUPPORTED, at + "in_dim must be a multiple of 4 and at most " +
                                                     std::to_string(xt::stack_max_chunks() * 256));
+            if (w->tile_bytes >= ((size_t)1 << 31))
+                return fail(XT_ERR_UNSUPPORTED, at + "weights above 2 GiB per projection");
             d.tiles[p] = w->tiles;
             d.ws[p] = w->ws;
             d.y[p] = op.y[p];
@@ -854,35 +864,126 @@ int xt_stack_create(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_st
         d.ldq = d.nch * 256;
         d.x = op.x;
         d.dep = op.dep;
-        d.nq = M > 1 ? (int)M : 0;
+        d.dep_items = op.dep >= 0 ? dops[(size_t)op.dep].ngemv : 0;
+        d.nq = (M > 1 || one) ? (int)((M + rq - 1) / rq) : 0;
         d.ngemv = blocks;
         if (d.nq + blocks >= (1 << 20)) return fail(XT_ERR_UNSUPPORTED, at + "too many rows");
-        for (int t = 0; t < d.nq + blocks; ++t) items.push_back(((uint32_t)i << 20) | (uint32_t)t);
-        if (M > 1) {
+        if (op.dep >= 0) dops[(size_t)op.dep].pub = 1;
+        if (d.nq > 0) {
             qoff[(size_t)i] = scratch;
-            scratch += align_up((size_t)M * d.ldq, 256) + align_up((size_t)M * 4, 256);
+            scratch += align_up((size_t)M * d.ldq, 256) + align_up((size_t)M * 4, 256) +
+                       (one ? align_up((size_t)M * 128, 256) : 0);
         }
+    }
+    // Work list: each op's GEMV items in op order; an op's quantiser items
+    // (M > 1) go right after the GEMV items of the op it depends on (at the
+    // front when it has none), so they are done long before its GEMV items
+    // are taken.  Every item follows everything it waits for.
+    std::vector<uint32_t> items;
+    std::vector<double> cost;
+    auto push_quant = [&](int i) {
+        const xt::StackOpDev& d = dops[(size_t)i];
+        for (int t = 0; t < d.nq; ++t) {
+            items.push_back(((uint32_t)i << 20) | (uint32_t)t);
+            cost.push_back(16384.0 + 8.0 * rq * d.K);  // two reads of the rows
+        }
+    };
+    // Op order: ops that others wait for go as early as their own inputs
+    // allow, the rest keep the caller's order.  (Ops with no dependency path
+    // between them may run in any order: they share no buffers, per the
+    // contract in xtern.h.)  Every op still follows the op it depends on.
+    std::vector<int> order;
+    {
+        std::vector<char> placed((size_t)nops, 0);
+        std::vector<int> pend;
+        for (int i = 0; i < nops; ++i) pend.push_back(i);
+        while ((int)order.size() < nops) {
+            int pick = -1;
+            for (int i : pend)
+                if (!placed[(size_t)i] && (ops[i].dep < 0 || placed[(size_t)ops[i].dep]) &&
+                    dops[(size_t)i].pub) {
+                    pick = i;
+                    break;
+                }
+            if (pick < 0)
+                for (int i : pend)
+                    if (!placed[(size_t)i] && (ops[i].dep < 0 || placed[(size_t)ops[i].dep])) {
+                        pick = i;
+                        break;
+                    }
+            placed[(size_t)pick] = 1;
+            order.push_back(pick);
+        }
+    }
+    for (int i = 0; i < nops; ++i)
+        if (ops[i].dep < 0) push_quant(i);
+    for (int i : order) {
+        const xt::StackOpDev& d = dops[(size_t)i];
+        for (int t = 0; t < d.ngemv; ++t) {
+            items.push_back(((uint32_t)i << 20) | (uint32_t)(d.nq + t));
+            cost.push_back(16384.0 + 1024.0 * d.rg * d.nch + (double)M * d.K);  // + weights
+        }
+        for (int k = i + 1; k < nops; ++k)
+            if (ops[k].dep == i) push_quant(k);
     }
     int dev = 0, cus = 0, per_cu = 0;
     XT_HIP(hipGetDevice(&dev));
     XT_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    XT_HIP(xt::stack_blocks_per_cu(&per_cu));
+    XT_HIP(xt::stack_blocks_per_cu((int)M, slots, &per_cu));
     if (per_cu < 1) return fail(XT_ERR_UNSUPPORTED, "stack kernel does not fit a CU");
+    // Every workgroup resident at once (see xtern_stack.hip): grid = occupancy.
+    int grid = std::min(cus * per_cu, (int)items.size());
+    if (const char* b = getenv("XTERN_STACK_BLOCKS"))  // (tuning) fewer workgroups
+        if (atoi(b) > 0) grid = std::min(grid, atoi(b));
+    // Deal the list out: each item, in list order, to the workgroup that is
+    // predicted to finish its earlier items first (bytes as the cost).
+    std::vector<std::vector<uint32_t>> per((size_t)grid);
+    {
+        typedef std::pair<double, int> Slot;
+        std::vector<Slot> heap;
+        for (int b = 0; b < grid; ++b) heap.push_back(Slot(0.0, b));
+        auto later = [](const Slot& x, const Slot& y) { return x > y; };
+        std::make_heap(heap.begin(), heap.end(), later);
+        for (size_t t = 0; t < items.size(); ++t) {
+            std::pop_heap(heap.begin(), heap.end(), later);
+            Slot& s0 = heap.back();
+            per[(size_t)s0.second].push_back(items[t]);
+            s0.first += cost[t];
+            std::push_heap(heap.begin(), heap.end(), later);
+        }
+    }
+    std::vector<int> sched_off((size_t)grid + 1, 0);
+    std::vector<uint32_t> sched;
+    sched.reserve(items.size());
+    for (int b = 0; b < grid; ++b) {
+        if (per[(size_t)b].size() > (size_t)xt::kStackMaxWgItems)
+            return fail(XT_ERR_UNSUPPORTED, "stack too long for one launch (" +
+                                                std::to_string(items.size()) + " items)");
+        sched.insert(sched.end(), per[(size_t)b].begin(), per[(size_t)b].end());
+        sched_off[(size_t)b + 1] = (int)sched.size();
+    }
     const size_t ops_b = align_up(sizeof(xt::StackOpDev) * nops, 256);
-    const size_t items_b = align_up(items.size() * 4, 256);
+    const size_t off_b = align_up(sched_off.size() * 4, 256);
+    const size_t items_b = align_up(sched.size() * 4, 256);
     const size_t ctr_b = (size_t)(4 + 2 * nops) * 128;
     char* mem = nullptr;
-    hipError_t e = hipMalloc(reinterpret_cast<void**>(&mem), ops_b + items_b + ctr_b + scratch);
+    hipError_t e = hipMalloc(reinterpret_cast<void**>(&mem), ops_b + off_b + items_b + ctr_b + scratch);
     if (e != hipSuccess) return fail(XT_ERR_NOMEM, std::string("stack allocation: ") + hipGetErrorString(e));
-    char* sc = mem + ops_b + items_b + ctr_b;
-    for (int i = 0; i < nops && M > 1; ++i) {
+    char* sc = mem + ops_b + off_b + items_b + ctr_b;
+    for (int i = 0; i < nops; ++i) {
         xt::StackOpDev& d = dops[(size_t)i];
+        if (d.nq == 0) continue;
+        const size_t qb = align_up((size_t)M * d.ldq, 256);
         d.q = reinterpret_cast<int8_t*>(sc + qoff[(size_t)i]);
-        d.inv = reinterpret_cast<float*>(sc + qoff[(size_t)i] + align_up((size_t)M * d.ldq, 256));
+        d.inv = reinterpret_cast<float*>(sc + qoff[(size_t)i] + qb);
+        if (one) d.csum = reinterpret_cast<int32_t*>(sc + qoff[(size_t)i] + qb + align_up((size_t)M * 4, 256));
     }
     e = hipMemcpy(mem, dops.data(), sizeof(xt::StackOpDev) * nops, hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = hipMemcpy(mem + ops_b, items.data(), items.size() * 4, hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = hipMemset(mem + ops_b + items_b, 0, ctr_b);
+    if (e == hipSuccess)
+        e = hipMemcpy(mem + ops_b, sched_off.data(), sched_off.size() * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess)
+        e = hipMemcpy(mem + ops_b + off_b, sched.data(), sched.size() * 4, hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemset(mem + ops_b + off_b + items_b, 0, ctr_b);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
         (void)hipFree(mem);
@@ -894,16 +995,22 @@ int xt_stack_create(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_st
         return fail(XT_ERR_NOMEM, "stack handle");
     }
     st->args.ops = reinterpret_cast<const xt::StackOpDev*>(mem);
-    st->args.items = reinterpret_cast<const uint32_t*>(mem + ops_b);
-    st->args.ctr = reinterpret_cast<unsigned*>(mem + ops_b + items_b);
+    st->args.sched_off = reinterpret_cast<const int*>(mem + ops_b);
+    st->args.sched = reinterpret_cast<const uint32_t*>(mem + ops_b + off_b);
+    st->args.ctr = reinterpret_cast<unsigned*>(mem + ops_b + off_b + items_b);
     st->args.nitems = (int)items.size();
     st->args.nops = nops;
     st->args.M = (int)M;
     st->args.mode = mode;
+    st->args.slots = slots;
     // polls (about a microsecond each) before a dependency wait gives up
     const char* sl = getenv("XTERN_STACK_SPIN_LIMIT");
     st->args.spin_limit = sl ? atoi(sl) : (1 << 20);
-    st->blocks = std::min(cus * per_cu, (int)items.size());
+#ifdef XT_STACK_TRACE
+    if (getenv("XTERN_STACK_TRACE"))
+        XT_HIP(hipMalloc(reinterpret_cast<void**>(&st->args.trace), items.size() * 64));
+#endif
+    st->blocks = grid;
     st->device = dev;
     st->dev_mem = mem;
     *out = st;
@@ -921,12 +1028,23 @@ int xt_stack_check(xt_stack* st, int* gave_up) {
     if (!st || !gave_up) return fail(XT_ERR_INVALID, "NULL argument");
     XT_HIP(hipDeviceSynchronize());
     unsigned flag = 0;
-    unsigned* slot = st->args.ctr + 2 * 32;  // the error slot
+    unsigned* slot = st->args.ctr + 2 * 32;  // the error slot (xtern_stack.hip kCtrError)
     XT_HIP(hipMemcpy(&flag, slot, sizeof flag, hipMemcpyDeviceToHost));
     if (flag) XT_HIP(hipMemset(slot, 0, sizeof flag));
     *gave_up = flag ? 1 : 0;
     return XT_OK;
 }
+
+#ifdef XT_STACK_TRACE
+// Tuning builds: copy the per-item stamps (8 per item) to the host.
+extern "C" int xt_stack_trace_copy(const xt_stack* st, uint64_t* out, int64_t n) {
+    if (!st->args.trace) return fail(XT_ERR_INVALID, "no trace buffer");
+    XT_HIP(hipDeviceSynchronize());
+    XT_HIP(hipMemcpy(out, st->args.trace, std::min<int64_t>(n, (int64_t)st->args.nitems * 8) * 8,
+                     hipMemcpyDeviceToHost));
+    return XT_OK;
+}
+#endif
 
 int xt_stack_destroy(xt_stack* st) {
     if (!st) return XT_OK;

@@ -135,7 +135,10 @@ hipError_t launch_mlp_mid(const MidArgs& a, int M, hipStream_t s);
 // by the allocation-free entry point; resolved once per device.
 hipError_t scratch_region(void** ptr, size_t* bytes);
 // Persistent decode stack (xtern_stack.hip): one launch over a list of ops.
-constexpr int kStackRowGroups = 4;  // 16-row groups per GEMV item
+constexpr int kStackRowGroups = 4;          // 16-row groups per GEMV item (M > 1)
+constexpr int kStackMaxOps = 4095;
+constexpr int kStackMaxWgItems = 1024;      // items one workgroup may be dealt
+constexpr int kStackDescLdsBytes = 40 * 1024;  // every op descriptor is copied to LDS
 struct StackOpDev {
     const uint8_t* tiles[4];  // Pack4 tiles of each projection
     const float* ws[4];
@@ -143,25 +146,36 @@ struct StackOpDev {
     const float* x;           // [M][K] f32 input
     int8_t* q;                // [M][ldq] quantised input (M > 1), launch scratch
     float* inv;               // [M]
+    int32_t* csum;            // [M][32] sums of each 256-column chunk of q (M = 1 launch)
     int N[4];
     int gend[4];              // cumulative GEMV items per projection
     int nproj, K, nch, ldq;
     int dep;                  // op whose outputs x reads (wait for all its GEMV items), or -1
-    int nq;                   // quantiser items (M > 1: M, else 0)
+    int dep_items;            // that op's GEMV item count
+    int nq;                   // quantiser items (M > 1: ceil(M / rows per item), else 0)
     int ngemv;                // GEMV items
-    int pad;
+    int pub;                  // another op depends on this one: count its completions
+    int rg;                   // 16-row groups per GEMV item (4, or 8 for short K at M = 1)
 };
 struct StackArgs {
     const StackOpDev* ops;
-    const uint32_t* items;    // op << 20 | item index within the op
+    const int* sched_off;     // [grid + 1]: workgroup b takes sched[sched_off[b] .. sched_off[b+1])
+    const uint32_t* sched;    // items (op << 20 | item index within the op), per workgroup in list order
     unsigned* ctr;            // (4 + 2 * nops) slots of 128 bytes, zero between launches
     int nitems, nops, M, mode;
     int spin_limit;           // polls before a dependency wait gives up
+    int slots;                // M = 1: chunk slots per wave the ops need
+    uint64_t* trace;          // tuning builds only (XT_STACK_TRACE): 8 stamps per item
 };
 int stack_threads();
 int stack_max_chunks();  // chunks of K an op may have (4 per wave)
+int stack_rows_per_quant_item();
 hipError_t launch_stack(const StackArgs& a, int blocks, hipStream_t s);
-hipError_t stack_blocks_per_cu(int* n);
+hipError_t stack_blocks_per_cu(int M, int slots, int* n);
+// M = 1 pipelined launch: chunk slots per wave an op of nch chunks needs, and
+// its row groups per item (*rg); whether a launch of M rows takes it.
+int stack_one_slots(int nch, int* rg);
+bool stack_pipelined(int M);
 // HF prepacked striped bytes [N/f][K] (device) -> tiles (device).
 hipError_t launch_hf_tiles(int fmt, const uint8_t* stored, int64_t K, int64_t N, uint8_t* tiles,
                            hipStream_t s);

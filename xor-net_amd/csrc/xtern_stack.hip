@@ -9,52 +9,96 @@
 // quantisation (quantization.rs:95-195), exact i32 dots, (f32)dot * inv *
 // w_scale.
 //
-// Work list.  The host flattens the ops into items, op by op: M > 1 ops
-// first have M quantiser items (one input row each), then every op has one
-// GEMV item per block of up to kSRG 16-row groups of one of its projections
-// (all of K).  Workgroups take items in list order from a ticket counter:
-// the first item of workgroup b is item b, every later one comes from one
-// device-scope atomic add (issued while the current item's weights stream).
-// An item that depends on earlier items waits for their completion counter,
-// so the earliest unfinished item always has its inputs and is held by a
-// running workgroup: the launch finishes whatever the number of resident
-// workgroups.  Waits are bounded (a flag tells the host if one gave up).
+// Work list.  The host flattens the ops into items: M > 1 ops have
+// quantiser items (kSW input rows each), every op has one GEMV item per block
+// of up to kSRG 16-row groups of one of its projections (all of K).  It then
+// deals the list out to the workgroups (greedy, by bytes), each workgroup
+// getting its items in list order, and every item after the items it waits
+// for.  With every workgroup of the launch resident at once (the grid is
+// sized to the occupancy), the earliest unfinished item is always being
+// worked on and has its inputs, so the launch always finishes.  Waits are
+// bounded anyway: one that gives up sets a flag for the host, and all later
+// waits of the launch return at once.
+//
+// Each workgroup copies every op descriptor and its own item list into LDS at
+// entry, so an item starts without a global load (which would also wait for
+// the previous item's stores: memory operations complete in issue order).  Weights are read with
+// buffer loads whose per-wave part of the address is a scalar offset, and
+// whose out-of-range parts (rows past N, chunks past K) read as zero without
+// touching memory.
 //
 // Coherence across the eight XCDs (each has its own L2): everything one item
 // writes for another item of the same launch (op outputs, quantised rows,
 // scales) is written with device-scope stores and read with device-scope
-// loads, and each completion count is bumped only after the item's stores
-// have completed (s_waitcnt + barrier).  No cache-wide fences.
+// loads, and a completion count is bumped only after the item's stores have
+// completed (s_waitcnt + barrier).  No cache-wide fences.  A workgroup that
+// has seen an op complete remembers it (one LDS bit), so later items that
+// depend on the same op skip the poll.
 //
 // The last workgroup to finish resets the counters, so the next launch
 // (stream order) starts from zero without a memset.
 #include <hip/hip_runtime.h>
+#include <stddef.h>
 #include <stdint.h>
+#include <stdlib.h>
 
 #include "xtern_device.h"
 #include "xtern_internal.h"
+
+// XT_STACK_TRACE (0 in the library) compiles per-item timestamps for a
+// tuning build: thread 0 of the workgroup records s_memrealtime (100 MHz) at
+// the item's phase boundaries into StackArgs::trace[item * 8 + k].
+#ifndef XT_STACK_TRACE
+#define XT_STACK_TRACE 0
+#endif
 
 namespace xt {
 
 namespace {
 
-constexpr int kSW = 8;            // waves per workgroup
-constexpr int kSNT = kSW * 64;    // threads per workgroup
+constexpr int kSW = 8;                 // waves per workgroup
+constexpr int kSNT = kSW * 64;         // threads per workgroup
 constexpr int kSRG = kStackRowGroups;  // 16-row groups per GEMV item
+constexpr int kDescWords = sizeof(StackOpDev) / 4;
+static_assert(kDescWords <= 64 && sizeof(StackOpDev) % 4 == 0, "a descriptor is one wave load");
 
-// Counter slots, 128 bytes apart: ticket, exit count, error flag, spare, then
-// the GEMV completions of every op, then the quantiser completions.
+// Counter slots, 128 bytes apart: exit count, error flag, spares, then the
+// GEMV completions of every op, then the quantiser completions.
 __device__ __forceinline__ unsigned* ctr_at(unsigned* c, int slot) { return c + slot * 32; }
-constexpr int kCtrTicket = 0, kCtrExit = 1, kCtrError = 2, kCtrDone0 = 4;
+constexpr int kCtrExit = 1, kCtrError = 2, kCtrDone0 = 4;
 
-// Device-scope (all XCDs) loads and stores.
+__device__ __forceinline__ void stamp(const StackArgs& a, int pos, int k, unsigned tag) {
+#if XT_STACK_TRACE
+    if (a.trace && threadIdx.x == 0) {
+        uint64_t* t = a.trace + (size_t)pos * 8;
+        t[k] = __builtin_amdgcn_s_memrealtime();
+        if (k == 0) t[7] = tag;
+    }
+#else
+    (void)a, (void)pos, (void)k, (void)tag;
+#endif
+}
+
+// Buffer resources (uniform).  num_records bounds every access: a load past
+// it returns zeros and reads no memory.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t rsrc(const void* base, unsigned bytes) {
     return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
                                              0x00020000);
 }
-constexpr int kCohAux = 16;  // cache policy: device scope
-__device__ __forceinline__ v4i ld_coh16(__amdgpu_buffer_rsrc_t r, unsigned off) {
-    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCohAux);
+constexpr unsigned kOutOfRange = 0x80000000u;  // a scalar offset past every resource
+constexpr int kAuxStream = 2;   // cache policy: non-temporal (weights, read once)
+constexpr int kAuxCoh = 16;     // cache policy: device scope (data written in the launch)
+__device__ __forceinline__ v4i ld_coh16(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff = 0) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kAuxCoh);
+}
+__device__ __forceinline__ v4i ld_w16(__amdgpu_buffer_rsrc_t r, unsigned voff, unsigned soff) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kAuxStream);
+}
+// Stores through a buffer resource (the descriptor's pointers carry no
+// address space, and flat accesses would also count against LDS waits).
+__device__ __forceinline__ void st_buf(__amdgpu_buffer_rsrc_t r, unsigned off, unsigned v, bool coh) {
+    if (coh) __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, kAuxCoh);
+    else __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, 0);
 }
 __device__ __forceinline__ void st_coh(float* p, float v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -81,148 +125,220 @@ __device__ __forceinline__ void wait_count(unsigned* c, unsigned target, unsigne
     }
 }
 
-// Every thread's stores have completed, then one count bump.
-__device__ __forceinline__ void publish(unsigned* c) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0) __hip_atomic_fetch_add(c, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+constexpr int kDescLdsWords = kStackDescLdsBytes / 4;
+constexpr int kKnownWords = kStackMaxOps * 2 / 32 + 1;
 
 struct Shared {
     v4i red[kSW][kSRG][64];
+    unsigned desc[kDescLdsWords];          // every op descriptor
+    unsigned items[kStackMaxWgItems];      // this workgroup's items, in order
+    unsigned known[kKnownWords];           // completions this workgroup has seen
+    unsigned qrow[2][kSNT * 4];            // M = 1: the item's i8 input row (by parity)
+    unsigned csum[2][32];                  //        and its chunk sums
     float wmax[kSW];
-    unsigned next;
     unsigned last;
 };
 
-// Quantiser item: row m of op's input into q / inv (quantization.rs:95-195).
-__device__ void quant_item(const StackArgs& a, const StackOpDev* __restrict__ op, int opi, int m,
-                           Shared& sh, unsigned* tk) {
-    const int K = op->K, n4 = K >> 2, ldq = op->ldq;
-    const int dep = op->dep;
-    if (threadIdx.x == 0) {
-        *tk = __hip_atomic_fetch_add(ctr_at(a.ctr, kCtrTicket), 1u, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
-        if (dep >= 0)
-            wait_count(ctr_at(a.ctr, kCtrDone0 + dep), (unsigned)a.ops[dep].ngemv,
-                       ctr_at(a.ctr, kCtrError), a.spin_limit);
+__device__ __forceinline__ unsigned* done_ctr(const StackArgs& a, int op) {
+    return ctr_at(a.ctr, kCtrDone0 + op);
+}
+__device__ __forceinline__ unsigned* qdone_ctr(const StackArgs& a, int op) {
+    return ctr_at(a.ctr, kCtrDone0 + a.nops + op);
+}
+
+// An op descriptor held as one vector register: lane k holds dword k (from
+// the LDS copy).  Fields come out with v_readlane at a uniform (possibly
+// computed) lane, straight into scalar registers.  (A descriptor struct in
+// registers with a computed index into one of its arrays lands in scratch
+// memory, and a scratch load waits for every memory operation in flight.)
+struct OpRef {
+    unsigned v;
+    __device__ __forceinline__ int i(unsigned off) const {
+        return (int)__builtin_amdgcn_readlane(v, (int)(off / 4));
     }
-    __syncthreads();
-    const __amdgpu_buffer_rsrc_t xr = rsrc(op->x, (unsigned)(a.M * K * 4));
-    float4 v[8];
+    template <typename T>
+    __device__ __forceinline__ T* ptr(unsigned off) const {
+        const uint32_t lo = __builtin_amdgcn_readlane(v, (int)(off / 4));
+        const uint32_t hi = __builtin_amdgcn_readlane(v, (int)(off / 4 + 1));
+        return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
+    }
+};
+#define OPF(field) ((unsigned)offsetof(StackOpDev, field))
+__device__ __forceinline__ OpRef load_op(const Shared& sh, int opi) {
+    const int lane = threadIdx.x & 63;
+    return OpRef{sh.desc[opi * kDescWords + min(lane, kDescWords - 1)]};
+}
+// Values the compiler cannot prove wave-uniform, moved to scalar registers
+// (a buffer resource or scalar offset built from a vector register turns
+// every load into a loop over the distinct values).
+template <typename T>
+__device__ __forceinline__ T* sgpr_ptr(T* p) {
+    const uint64_t v = reinterpret_cast<uint64_t>(p);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+    const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+    return reinterpret_cast<T*>(((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
+
+__device__ __forceinline__ bool known(const Shared& sh, int slot) {
+    return (sh.known[slot >> 5] >> (slot & 31)) & 1u;
+}
+
+// Wait (lane 0 of this wave; no workgroup barrier) until counter `slot`
+// (an op's GEMV completions: slot = op; its quantiser rows: nops + op)
+// reaches target, unless this workgroup has already seen it get there.
+__device__ __forceinline__ void wave_wait(const StackArgs& a, Shared& sh, int slot, unsigned target) {
+    const unsigned bit = 1u << (slot & 31);
+    if (sh.known[slot >> 5] & bit) return;  // (uniform: an LDS word read by every lane)
+    if ((threadIdx.x & 63) == 0) {
+        wait_count(ctr_at(a.ctr, kCtrDone0 + slot), target, ctr_at(a.ctr, kCtrError), a.spin_limit);
+        atomicOr(&sh.known[slot >> 5], bit);
+    }
+    __builtin_amdgcn_wave_barrier();
+}
+
+// Quantiser item: rows r0 .. r0 + kSW - 1 of op's input (one row per wave)
+// into q / inv (quantization.rs:95-195): pass 1 the row's absmax, pass 2
+// quantise and store (the row is read twice; no barrier).
+__device__ void quant_item(const StackArgs& a, Shared& sh, const OpRef& d, int opi, int r0) {
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int K = d.i(OPF(K)), n4 = K >> 2, ldq = d.i(OPF(ldq)), M = a.M;
+    const int rows = min(kSW, M - r0);
+    const int dep = d.i(OPF(dep));
+    if (dep >= 0) wave_wait(a, sh, dep, (unsigned)d.i(OPF(dep_items)));
+    const int m = r0 + min(wave, rows - 1);
+    // one row per resource: pieces past K read as zero
+    const __amdgpu_buffer_rsrc_t xr = rsrc(d.ptr<const float>(OPF(x)) + (size_t)m * K, (unsigned)(K * 4));
     float mx = 0.0f;
+    for (int f0 = 0; f0 < n4; f0 += 4 * 64) {
+        v4i r[4];
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-        const int f = threadIdx.x + u * kSNT;
-        const v4i r = ld_coh16(xr, (unsigned)(((size_t)m * K + 4 * min(f, n4 - 1)) * 4));
-        v[u] = f < n4 ? make_float4(__int_as_float(r[0]), __int_as_float(r[1]), __int_as_float(r[2]),
-                                    __int_as_float(r[3]))
-                      : make_float4(0.f, 0.f, 0.f, 0.f);
-        mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
+        for (int u = 0; u < 4; ++u) r[u] = ld_coh16(xr, (unsigned)(f0 + u * 64 + lane) * 16u);
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) mx = fmaxf(mx, fabsf(__int_as_float(r[u][e])));
     }
-    const int wm = wave_reduce_bits(__float_as_int(mx), [](int p, int q) {
+    const float rmx = __int_as_float(wave_reduce_bits(__float_as_int(mx), [](int p, int q) {
         return __float_as_int(fmaxf(__int_as_float(p), __int_as_float(q)));
-    });
-    if ((threadIdx.x & 63) == 0) sh.wmax[threadIdx.x >> 6] = __int_as_float(wm);
-    __syncthreads();
-    float rmx = sh.wmax[0];
-#pragma unroll
-    for (int w = 1; w < kSW; ++w) rmx = fmaxf(rmx, sh.wmax[w]);
+    }));
     const float scale = (rmx > 0.0f) ? __fdiv_rn(127.0f, rmx) : 1.0f;
     const float invs = (rmx > 0.0f) ? __fdiv_rn(rmx, 127.0f) : 1.0f;
     const int kmain = (K / 16) * 16;
-    unsigned* qrow = reinterpret_cast<unsigned*>(op->q + (size_t)m * ldq);
+    const __amdgpu_buffer_rsrc_t qr = rsrc(d.ptr<int8_t>(OPF(q)) + (size_t)m * ldq, (unsigned)ldq);
+    int32_t* csum = d.ptr<int32_t>(OPF(csum));
+    const __amdgpu_buffer_rsrc_t cr = rsrc(csum ? csum + (size_t)m * 32 : nullptr, csum ? 128u : 0u);
+    const bool mine = wave < rows;
     auto body = [&](auto mode_c) {
+        for (int f0 = 0; f0 < ldq / 4; f0 += 64) {  // one 256-column chunk per trip
+            const int f = f0 + lane;
+            const v4i r = ld_coh16(xr, (unsigned)f * 16u);  // zeros past K: code 0
+            unsigned w = 0;
 #pragma unroll
-        for (int u = 0; u < 8; ++u) {
-            const int f = threadIdx.x + u * kSNT;
-            if (f < ldq / 4) {
-                const float e[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
-                unsigned w = 0;
-#pragma unroll
-                for (int t = 0; t < 4; ++t)
-                    w |= (unsigned)(quant_one(e[t], scale, decltype(mode_c)::value, 4 * f + t < kmain) & 255)
-                         << (8 * t);
-                st_coh(qrow + f, f < n4 ? w : 0u);
+            for (int t = 0; t < 4; ++t)
+                w |= (unsigned)(quant_one(__int_as_float(r[t]), scale, decltype(mode_c)::value,
+                                          4 * f + t < kmain) & 255) << (8 * t);
+            if (mine) st_buf(qr, (unsigned)f * 4u, w, true);
+            if (csum) {  // (uniform) the chunk's sum of quantised activations
+                const int cs = wave_reduce_bits(__builtin_amdgcn_sdot4((int)w, 0x01010101, 0, false),
+                                                [](int p_, int q_) { return p_ + q_; });
+                if (mine && lane == 0) st_buf(cr, (unsigned)(f0 / 64) * 4u, (unsigned)cs, true);
             }
         }
     };
     if (a.mode == XT_QUANT_AVX512) body(std::integral_constant<int, XT_QUANT_AVX512>{});
     else body(std::integral_constant<int, XT_QUANT_SCALAR>{});
-    // (ldq <= 16384 = 8 pieces per thread: the loop above covers the padding)
-    if (threadIdx.x == 0) st_coh(op->inv + m, invs);
-    publish(ctr_at(a.ctr, kCtrDone0 + a.nops + opi));
+    if (mine && lane == 0)
+        st_buf(rsrc(d.ptr<float>(OPF(inv)), (unsigned)(M * 4)), (unsigned)m * 4u, __float_as_uint(invs), true);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0)
+        __hip_atomic_fetch_add(qdone_ctr(a, opi), (unsigned)rows, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // GEMV item: row groups G0 .. G0 + kSRG - 1 of projection p over all of K,
 // for every token.  Wave w multiplies chunks w, w + kSW, ... (NCW of them at
-// most); FUSED (M = 1): the item quantises the f32 input row itself, one
-// pass, as the decode GEMV does; otherwise it reads the rows quantised by
-// the op's quantiser items.
-template <int NCW, bool FUSED>
-__device__ void gemv_item(const StackArgs& a, const StackOpDev* __restrict__ op, int opi, int blk,
-                          Shared& sh, unsigned* tk) {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+// most).  ONE (M = 1): the item quantises the f32 input row itself in one
+// pass (each wave its own chunks' pieces, the row maximum through LDS), as
+// the decode GEMV does; otherwise it reads the rows the op's quantiser
+// items wrote.
+template <int NCW, bool ONE>
+__device__ void gemv_item(const StackArgs& a, Shared& sh, const OpRef& d, int opi, int blk,
+                          int pos) {
+    const int lane = threadIdx.x & 63, wave = wave_id();
     const int g = lane >> 4, j = lane & 15;
-    const int np = op->nproj;
-    const int p = (np > 1 && blk >= op->gend[0]) + (np > 2 && blk >= op->gend[1]) +
-                  (np > 3 && blk >= op->gend[2]);
-    const int b0 = p ? op->gend[p - 1] : 0;
+    const int np = d.i(OPF(nproj));
+    const int ge0 = d.i(OPF(gend)), ge1 = d.i(OPF(gend) + 4), ge2 = d.i(OPF(gend) + 8);
+    const int p = (np > 1 && blk >= ge0) + (np > 2 && blk >= ge1) + (np > 3 && blk >= ge2);
+    const int b0 = p == 0 ? 0 : d.i(OPF(gend) + 4 * (p - 1));
     const int G0 = (blk - b0) * kSRG;
-    const int N = op->N[p], NG = (N + 15) >> 4;
-    const int nch = op->nch, K = op->K, M = a.M;
-    const uint8_t* tiles = op->tiles[p];
+    const int N = d.i(OPF(N) + 4 * p), NG = (N + 15) >> 4;
+    const int nch = d.i(OPF(nch)), K = d.i(OPF(K)), M = a.M;
+    const int dep = d.i(OPF(dep));
+    const bool pub = d.i(OPF(pub)) != 0;
+    const __amdgpu_buffer_rsrc_t wr =
+        rsrc(d.ptr<const uint8_t>(OPF(tiles) + 8 * p), (unsigned)(NG * nch * 1024));
+    const __amdgpu_buffer_rsrc_t xr = rsrc(d.ptr<const float>(OPF(x)), (unsigned)(K * 4));
+    const unsigned voff = (unsigned)lane * 16u;
 
+    // ONE without a dependency: the input row is ready, so its pieces are
+    // requested first (they are needed first, for the row maximum); pieces
+    // past K read as zero
+    // (an input written before the launch takes cached loads; one written in
+    // this launch device-scope loads, first when its op is known complete)
+    v4i x0[NCW];
+    const bool x_first = ONE && (dep < 0 || known(sh, dep));
+    if (ONE && dep < 0) {
+#pragma unroll
+        for (int t = 0; t < NCW; ++t)
+            x0[t] = __builtin_amdgcn_raw_buffer_load_b128(xr, voff, (unsigned)(wave + t * kSW) * 1024u, 0);
+    } else if (x_first) {
+#pragma unroll
+        for (int t = 0; t < NCW; ++t) x0[t] = ld_coh16(xr, voff, (unsigned)(wave + t * kSW) * 1024u);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     v4i wv[NCW][kSRG];
 #pragma unroll
     for (int t = 0; t < NCW; ++t) {
-        const int c = min(wave + t * kSW, nch - 1);
+        const int c = wave + t * kSW;
 #pragma unroll
-        for (int r = 0; r < kSRG; ++r)
-            wv[t][r] = ld_stream(tiles + (((size_t)min(G0 + r, NG - 1) * nch + c) * 64 + lane) * 16);
+        for (int r = 0; r < kSRG; ++r)  // (rows past N and chunks past K: zeros, no memory read)
+            wv[t][r] = ld_w16(wr, voff, c < nch ? (unsigned)(((G0 + r) * nch + c) * 1024) : kOutOfRange);
     }
+    __builtin_amdgcn_sched_barrier(0);
+    stamp(a, pos, 1, 0);
     const int o = (G0 + min(wave, kSRG - 1)) * 16 + j;
-    const float wscale = op->ws[p][min(o, N - 1)];
-    if (threadIdx.x == 0) {
-        *tk = __hip_atomic_fetch_add(ctr_at(a.ctr, kCtrTicket), 1u, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
-        if (FUSED) {
-            if (op->dep >= 0)
-                wait_count(ctr_at(a.ctr, kCtrDone0 + op->dep), (unsigned)a.ops[op->dep].ngemv,
-                           ctr_at(a.ctr, kCtrError), a.spin_limit);
-        } else {
-            wait_count(ctr_at(a.ctr, kCtrDone0 + a.nops + opi), (unsigned)M, ctr_at(a.ctr, kCtrError),
-                       a.spin_limit);
+    const float wscale = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+        rsrc(d.ptr<const float>(OPF(ws) + 8 * p), (unsigned)(N * 4)), (unsigned)min(o, N - 1) * 4u, 0, 0));
+    if (ONE) {
+        if (!x_first) {  // written in this launch: device-scope loads after the wait
+            wave_wait(a, sh, dep, (unsigned)d.i(OPF(dep_items)));
+#pragma unroll
+            for (int t = 0; t < NCW; ++t) x0[t] = ld_coh16(xr, voff, (unsigned)(wave + t * kSW) * 1024u);
         }
+    } else {
+        wave_wait(a, sh, a.nops + opi, (unsigned)M);
     }
-    __syncthreads();
+    stamp(a, pos, 2, 0);
 
-    const int ntb = FUSED ? 1 : (M + 15) >> 4;
+    const int ntb = ONE ? 1 : (M + 15) >> 4;
     for (int tb = 0; tb < ntb; ++tb) {
-        const int mt = FUSED ? 1 : min(16, M - 16 * tb);  // tokens of this block
-        v4i av[NCW][4];
+        const int mt = ONE ? 1 : min(16, M - 16 * tb);  // tokens of this block
         float invr[4];
-        if constexpr (FUSED) {
-            const int n4 = K >> 2;
-            const __amdgpu_buffer_rsrc_t xr = rsrc(op->x, (unsigned)(K * 4));
-            float4 x0[NCW];
+        unsigned w4[NCW];
+        v4i aq[ONE ? 1 : NCW][4];
+        if constexpr (ONE) {
             float mx = 0.0f;
 #pragma unroll
-            for (int t = 0; t < NCW; ++t) {
-                const int f = (wave + t * kSW) * 64 + lane;
-                const v4i r = ld_coh16(xr, (unsigned)(4 * min(f, n4 - 1) * 4));
-                x0[t] = f < n4 ? make_float4(__int_as_float(r[0]), __int_as_float(r[1]),
-                                             __int_as_float(r[2]), __int_as_float(r[3]))
-                               : make_float4(0.f, 0.f, 0.f, 0.f);
-                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(x0[t].x), fabsf(x0[t].y)),
-                                     fmaxf(fabsf(x0[t].z), fabsf(x0[t].w))));
-            }
-            // (pieces of chunks beyond nch lie past K and read as zero)
+            for (int t = 0; t < NCW; ++t)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) mx = fmaxf(mx, fabsf(__int_as_float(x0[t][e])));
             const int wm = wave_reduce_bits(__float_as_int(mx), [](int p_, int q_) {
                 return __float_as_int(fmaxf(__int_as_float(p_), __int_as_float(q_)));
             });
             if (lane == 0) sh.wmax[wave] = __int_as_float(wm);
             __syncthreads();
+            stamp(a, pos, 3, 0);
             float rmx = sh.wmax[0];
 #pragma unroll
             for (int w = 1; w < kSW; ++w) rmx = fmaxf(rmx, sh.wmax[w]);
@@ -231,46 +347,36 @@ __device__ void gemv_item(const StackArgs& a, const StackOpDev* __restrict__ op,
 #pragma unroll
             for (int r = 0; r < 4; ++r) invr[r] = iv;
             const int kmain = (K / 16) * 16;
-            unsigned w4[NCW];
             auto pack = [&](auto mode_c) {
 #pragma unroll
                 for (int t = 0; t < NCW; ++t) {
                     const int f = (wave + t * kSW) * 64 + lane;
-                    const float e4[4] = {x0[t].x, x0[t].y, x0[t].z, x0[t].w};
                     unsigned r = 0;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        r |= (unsigned)(quant_one(e4[e], scale, decltype(mode_c)::value, 4 * f + e < kmain) & 255)
-                             << (8 * e);
-                    w4[t] = f < n4 ? r : 0u;
+                    for (int e = 0; e < 4; ++e)  // (zeros past K quantise to 0)
+                        r |= (unsigned)(quant_one(__int_as_float(x0[t][e]), scale, decltype(mode_c)::value,
+                                                  4 * f + e < kmain) & 255) << (8 * e);
+                    w4[t] = r;
                 }
             };
             if (a.mode == XT_QUANT_AVX512) pack(std::integral_constant<int, XT_QUANT_AVX512>{});
             else pack(std::integral_constant<int, XT_QUANT_SCALAR>{});
-            // lane (g, j) of k-step s takes the chunk's packed pieces 16 s + 4 g + d
-#pragma unroll
-            for (int t = 0; t < NCW; ++t)
-#pragma unroll
-                for (int s = 0; s < 4; ++s)
-#pragma unroll
-                    for (int d = 0; d < 4; ++d)
-                        av[t][s][d] = __builtin_amdgcn_ds_bpermute((16 * s + 4 * g + d) << 2, (int)w4[t]);
         } else {
-            const int ldq = op->ldq;
-            const __amdgpu_buffer_rsrc_t qr = rsrc(op->q, (unsigned)(M * ldq));
-            const __amdgpu_buffer_rsrc_t ir = rsrc(op->inv, (unsigned)(M * 4));
+            const int ldq = d.i(OPF(ldq));
+            const __amdgpu_buffer_rsrc_t qr = rsrc(d.ptr<const int8_t>(OPF(q)), (unsigned)(M * ldq));
+            const __amdgpu_buffer_rsrc_t ir = rsrc(d.ptr<const float>(OPF(inv)), (unsigned)(M * 4));
             const int row = 16 * tb + min(j, mt - 1);
 #pragma unroll
             for (int t = 0; t < NCW; ++t) {
                 const int c = min(wave + t * kSW, nch - 1);
 #pragma unroll
                 for (int s = 0; s < 4; ++s)
-                    av[t][s] = ld_coh16(qr, (unsigned)((size_t)row * ldq + c * 256 + s * 64 + 16 * g));
+                    aq[t][s] = ld_coh16(qr, (unsigned)((size_t)row * ldq + c * 256 + s * 64 + 16 * g));
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r)
                 invr[r] = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-                    ir, (unsigned)(16 * tb + min(4 * g + r, mt - 1)) * 4, 0, kCohAux));
+                    ir, (unsigned)(16 * tb + min(4 * g + r, mt - 1)) * 4, 0, kAuxCoh));
         }
         // (the weights stay packed across token blocks: without this the
         // compiler hoists every decoded weight out of the loop)
@@ -283,15 +389,26 @@ __device__ void gemv_item(const StackArgs& a, const StackOpDev* __restrict__ op,
         for (int r = 0; r < kSRG; ++r) acc[r] = v4i{0, 0, 0, 0};
 #pragma unroll
         for (int t = 0; t < NCW; ++t) {
-            const bool live = wave + t * kSW < nch;
+            // chunks past K: ONE's activations are zero there; the quantised
+            // rows of the other path are not, so those waves skip the chunk
+            const bool live = ONE || wave + t * kSW < nch;
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                const v4i x = (live && j < mt) ? av[t][s] : v4i{0, 0, 0, 0};
+                v4i av;
+                if constexpr (ONE) {
+                    // lane (g, j) of k-step s takes the chunk's packed pieces 16 s + 4 g + d
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        av[e] = __builtin_amdgcn_ds_bpermute((16 * s + 4 * g + e) << 2, (int)w4[t]);
+                } else {
+                    av = aq[t][s];
+                }
+                const v4i x = (live && j < mt) ? av : v4i{0, 0, 0, 0};
 #pragma unroll
                 for (int r = 0; r < kSRG; ++r) {
                     v4i b = decode4(wv[t][r][s]);
 #pragma unroll
-                    for (int d = 0; d < 4; ++d) b[d] = signed_codes(b[d]);
+                    for (int e = 0; e < 4; ++e) b[e] = signed_codes(b[e]);
                     acc[r] = mfma(x, b, acc[r]);
                 }
             }
@@ -300,47 +417,308 @@ __device__ void gemv_item(const StackArgs& a, const StackOpDev* __restrict__ op,
 #pragma unroll
         for (int r = 0; r < kSRG; ++r) sh.red[wave][r][lane] = acc[r];
         __syncthreads();
+        stamp(a, pos, 4, 0);
         if (wave < kSRG && G0 + wave < NG && o < N) {
             v4i sum = sh.red[0][wave][lane];
 #pragma unroll
             for (int w = 1; w < kSW; ++w) sum += sh.red[w][wave][lane];
-            float* y = op->y[p];
+            const __amdgpu_buffer_rsrc_t yr = rsrc(d.ptr<float>(OPF(y) + 8 * p), (unsigned)(M * N * 4));
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int i = 4 * g + r;
-                if (i < mt)  // layers.rs:294 -- (dot as f32 * inv_scale) * w_scale
-                    st_coh(y + (size_t)(16 * tb + i) * N + o,
-                           __fmul_rn(__fmul_rn((float)sum[r], invr[r]), wscale));
+                // layers.rs:294 -- (dot as f32 * inv_scale) * w_scale; device-scope
+                // stores only where another op of the launch reads the output
+                const float v = __fmul_rn(__fmul_rn((float)sum[r], invr[r]), wscale);
+                if (i < mt) st_buf(yr, (unsigned)((16 * tb + i) * N + o) * 4u, __float_as_uint(v), pub);
             }
         }
     }
-    publish(ctr_at(a.ctr, kCtrDone0 + opi));
+    stamp(a, pos, 5, 0);
+    if (pub) {  // another op reads these outputs inside the launch
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (threadIdx.x == 0)
+            __hip_atomic_fetch_add(done_ctr(a, opi), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+        __syncthreads();  // the reduction stage is read before the next item writes it
+    }
+    stamp(a, pos, 6, 0);
 }
 
-__global__ __launch_bounds__(kSNT) void stack_kernel(const StackArgs a) {
-    __shared__ Shared sh;
-    unsigned t = blockIdx.x;
-    while (t < (unsigned)a.nitems) {
-        const uint32_t it = a.items[t];
-        const int opi = (int)(it >> 20), local = (int)(it & 0xfffff);
-        const StackOpDev* op = a.ops + opi;
-        unsigned tk = 0;
-        if (local < op->nq) {
-            quant_item(a, op, opi, local, sh, &tk);
-        } else {
-            const int blk = local - op->nq;
-            const int ncw = (op->nch + kSW - 1) / kSW;
-            if (a.M == 1) {
-                if (ncw <= 2) gemv_item<2, true>(a, op, opi, blk, sh, &tk);
-                else gemv_item<4, true>(a, op, opi, blk, sh, &tk);
-            } else {
-                if (ncw <= 2) gemv_item<2, false>(a, op, opi, blk, sh, &tk);
-                else gemv_item<4, false>(a, op, opi, blk, sh, &tk);
+// ---------------------------------------------------------------------------
+// M = 1: software-pipelined items over rows quantised once per op.
+//
+// The op's quantiser item writes its input row as i8 plus the sum of each
+// 256-column chunk.  A GEMV item covers rg row groups (8 when K has at most
+// 16 chunks, else 4): wave w multiplies row group w % rg and the chunks c
+// with c % (8 / rg) == w / rg, so every wave holds one accumulator and at
+// most NS weight tiles, and all waves carry the same load.  Weights enter the
+// MFMA as codes (w + 1) and each wave subtracts the chunk sums of the chunks
+// it multiplied: the decode is 3 shifts and 4 ANDs per 16 weights.  The i8
+// row goes through LDS (double-buffered by item parity); the A fragment of a
+// k-step is one ds_read_b128 that the 16 token lanes share.
+//
+// While item k computes, item k + 1's weights and row are in flight: each
+// item issues the same number of loads (slots it does not need at an
+// out-of-range offset: zeros, no memory access), so the compiler's wait
+// counts stay exact and a wait for item k never waits for item k + 1.
+// ---------------------------------------------------------------------------
+template <int NS>
+struct OneBuf {
+    v4i w[NS];   // weight tiles of this wave's chunk slots
+    v4i q;       // 16 bytes of the i8 input row (thread t: bytes 16 t ..)
+    v4i cs;      // threads 0..7: chunk sums 4 t .. 4 t + 3
+    float inv;   // the row's inverse scale
+};
+
+struct OneGeo {
+    int opi, p, G0, N, NG, nch, rg, dep_ready, pub;
+    int quant;  // a quantiser item (runs in the compute stage; its loads are empty)
+    // resources as base + size (built where used: resources kept in the
+    // struct would be copied through scratch memory)
+    const void* wp;
+    const void* qp;
+    const void* cp;
+    const void* ip;
+    unsigned wn, qn, cn, in_;
+    __device__ __forceinline__ __amdgpu_buffer_rsrc_t wr() const { return rsrc(wp, wn); }
+    __device__ __forceinline__ __amdgpu_buffer_rsrc_t qr() const { return rsrc(qp, qn); }
+    __device__ __forceinline__ __amdgpu_buffer_rsrc_t cr() const { return rsrc(cp, cn); }
+    __device__ __forceinline__ __amdgpu_buffer_rsrc_t ir() const { return rsrc(ip, in_); }
+};
+
+// k >= n gives an empty item (no chunks, empty resources).
+__device__ __forceinline__ OneGeo one_geo(const Shared& sh, int k, int n, int nops) {
+    OneGeo g;
+    if (k >= n) {
+        g.opi = g.p = g.G0 = 0;
+        g.N = g.NG = 1;
+        g.nch = 0;
+        g.rg = 8;
+        g.dep_ready = 1;
+        g.pub = 0;
+        g.quant = 0;
+        g.wp = g.qp = g.cp = g.ip = nullptr;
+        g.wn = g.qn = g.cn = g.in_ = 0u;
+        return g;
+    }
+    const unsigned it = __builtin_amdgcn_readfirstlane(sh.items[k]);
+    g.opi = (int)(it >> 20);
+    const OpRef d = load_op(sh, g.opi);
+    const int blk = (int)(it & 0xfffff) - d.i(OPF(nq));
+    if (blk < 0) {  // quantiser item
+        g.p = g.G0 = 0;
+        g.N = g.NG = 1;
+        g.nch = 0;
+        g.rg = 8;
+        g.dep_ready = 1;
+        g.pub = 0;
+        g.quant = 1;
+        g.wp = g.qp = g.cp = g.ip = nullptr;
+        g.wn = g.qn = g.cn = g.in_ = 0u;
+        return g;
+    }
+    g.quant = 0;
+    const int np = d.i(OPF(nproj));
+    const int ge0 = d.i(OPF(gend)), ge1 = d.i(OPF(gend) + 4), ge2 = d.i(OPF(gend) + 8);
+    g.p = (np > 1 && blk >= ge0) + (np > 2 && blk >= ge1) + (np > 3 && blk >= ge2);
+    const int b0 = g.p == 0 ? 0 : d.i(OPF(gend) + 4 * (g.p - 1));
+    g.rg = d.i(OPF(rg));
+    g.G0 = (blk - b0) * g.rg;
+    g.N = d.i(OPF(N) + 4 * g.p);
+    g.NG = (g.N + 15) >> 4;
+    g.nch = d.i(OPF(nch));
+    g.pub = d.i(OPF(pub));
+    g.dep_ready = known(sh, nops + g.opi);  // the op's row has been seen quantised
+    g.wp = d.ptr<const uint8_t>(OPF(tiles) + 8 * g.p);
+    g.wn = (unsigned)(g.NG * g.nch * 1024);
+    g.qp = d.ptr<const int8_t>(OPF(q));
+    g.qn = (unsigned)d.i(OPF(ldq));
+    g.cp = d.ptr<const int32_t>(OPF(csum));
+    g.cn = 128u;
+    g.ip = d.ptr<const float>(OPF(inv));
+    g.in_ = 4u;
+    return g;
+}
+
+// chunk of slot i for this wave, or -1
+__device__ __forceinline__ int one_chunk(const OneGeo& g, int wave, int i) {
+    const int per = kSW / g.rg;  // waves per row group: 1 or 2
+    const int c = (wave / g.rg) + per * i;
+    return c < g.nch ? c : -1;
+}
+
+template <int NS>
+__device__ __forceinline__ void one_issue_w(const OneGeo& g, OneBuf<NS>& B) {
+    const int wave = wave_id();
+    const unsigned voff = (unsigned)(threadIdx.x & 63) * 16u;
+    const int r = wave % g.rg;
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+        const int c = one_chunk(g, wave, i);
+        B.w[i] = ld_w16(g.wr(), voff, c >= 0 ? (unsigned)(((g.G0 + r) * g.nch + c) * 1024) : kOutOfRange);
+    }
+}
+// The i8 row, chunk sums and scale (device scope: written in this launch);
+// out of range (zeros) when `now` is false, to be loaded again later.
+template <int NS>
+__device__ __forceinline__ void one_issue_q(const OneGeo& g, OneBuf<NS>& B, bool now) {
+    const unsigned t = threadIdx.x;
+    const unsigned so = now ? 0u : kOutOfRange;
+    B.q = ld_coh16(g.qr(), t * 16u, so);
+    B.cs = ld_coh16(g.cr(), (t & 7u) * 16u, so);
+    B.inv = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(g.ir(), 0u, so, kAuxCoh));
+}
+
+template <int NS>
+__device__ __forceinline__ void one_pre(const StackArgs& a, Shared& sh, const OneGeo& g, OneBuf<NS>& B,
+                                        int pos) {
+    stamp(a, pos, 1, 0);
+    const bool now = g.dep_ready != 0;  // (quantiser and empty items: ready)
+    if (!now) wave_wait(a, sh, a.nops + g.opi, 1u);
+    OneBuf<NS> L;
+    one_issue_q<NS>(g, L, !now);
+    B.q = now ? B.q : L.q;
+    B.cs = now ? B.cs : L.cs;
+    B.inv = now ? B.inv : L.inv;
+}
+
+template <int NS>
+__device__ __forceinline__ void one_compute(const StackArgs& a, Shared& sh, const OneGeo& g,
+                                            OneBuf<NS>& B, int parity, int pos) {
+    if (g.quant) {  // (uniform)
+        quant_item(a, sh, load_op(sh, g.opi), g.opi, 0);
+        return;
+    }
+    const int lane = threadIdx.x & 63, wave = wave_id();
+    const int gq = lane >> 4, j = lane & 15;
+    stamp(a, pos, 2, 0);
+    unsigned* qb = sh.qrow[parity];
+    *reinterpret_cast<v4i*>(qb + threadIdx.x * 4) = B.q;
+    if (threadIdx.x < 8) *reinterpret_cast<v4i*>(sh.csum[parity] + threadIdx.x * 4) = B.cs;
+    const int r = wave % g.rg;
+    const int o = (g.G0 + r) * 16 + j;
+    const OpRef d = load_op(sh, g.opi);
+    const float wscale = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(
+        rsrc(d.ptr<const float>(OPF(ws) + 8 * g.p), (unsigned)(g.N * 4)), (unsigned)min(o, g.N - 1) * 4u, 0, 0));
+    __syncthreads();
+    stamp(a, pos, 3, 0);
+    v4i acc = v4i{0, 0, 0, 0};
+    int xsum = 0;
+#pragma unroll
+    for (int i = 0; i < NS; ++i) {
+        const int c = one_chunk(g, wave, i);
+        if (c >= 0) {  // (uniform)
+            xsum += (int)sh.csum[parity][c];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+                const v4i av = *reinterpret_cast<const v4i*>(qb + (c * 256 + s * 64 + gq * 16) / 4);
+                acc = mfma(av, decode4(B.w[i][s]), acc);
             }
         }
-        if (threadIdx.x == 0) sh.next = tk + gridDim.x;
+    }
+    acc[0] -= xsum;  // codes are w + 1 (token 0: element 0 of the lanes with gq == 0)
+    const bool split = g.rg == 4;  // two waves per row group: add through LDS
+    if (split) {
+        sh.red[wave][0][lane] = acc;
         __syncthreads();
-        t = sh.next;
+    }
+    stamp(a, pos, 4, 0);
+    if (wave < g.rg && gq == 0 && g.G0 + r < g.NG && o < g.N) {
+        const int sum = split ? sh.red[wave][0][lane][0] + sh.red[wave + 4][0][lane][0] : acc[0];
+        // layers.rs:294 -- (dot as f32 * inv_scale) * w_scale; device-scope
+        // stores only where another op of the launch reads the output
+        const float v = __fmul_rn(__fmul_rn((float)sum, B.inv), wscale);
+        const __amdgpu_buffer_rsrc_t yr = rsrc(d.ptr<float>(OPF(y) + 8 * g.p), (unsigned)(g.N * 4));
+        st_buf(yr, (unsigned)o * 4u, __float_as_uint(v), g.pub != 0);
+    }
+    stamp(a, pos, 5, 0);
+    if (g.pub) {  // another op reads these outputs inside the launch
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (threadIdx.x == 0)
+            __hip_atomic_fetch_add(done_ctr(a, g.opi), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else if (split) {
+        __syncthreads();  // the reduction stage is read before the next item writes it
+    }
+    stamp(a, pos, 6, 0);
+}
+
+// (A quantiser item -- one per op, listed early -- runs in its compute slot.)
+template <int NS>
+__global__ __launch_bounds__(kSNT, 2) void stack_one_kernel(const StackArgs a) {
+    __shared__ Shared sh;
+    const int i0 = a.sched_off[blockIdx.x], n = a.sched_off[blockIdx.x + 1] - i0;
+    for (int i = threadIdx.x; i < n; i += kSNT) sh.items[i] = a.sched[i0 + i];
+    for (int i = threadIdx.x; i < a.nops * kDescWords; i += kSNT)
+        sh.desc[i] = reinterpret_cast<const unsigned*>(a.ops)[i];
+    for (int i = threadIdx.x; i < kKnownWords; i += kSNT) sh.known[i] = 0u;
+    __syncthreads();
+    const int k0 = 0, m = n;
+    OneBuf<NS> A, B;
+    OneGeo ga, gb;
+    auto item = [&](int k) { return k0 + k; };
+    ga = one_geo(sh, item(0), n, a.nops);
+    one_issue_q<NS>(ga, A, ga.dep_ready != 0);
+    one_issue_w<NS>(ga, A);
+    // two items per trip: A holds item k, B item k + 1 (the next item's loads
+    // are issued on every trip, empty past the end)
+    for (int k = 0; k < m; k += 2) {
+        stamp(a, i0 + item(k), 0, blockIdx.x | ((unsigned)ga.opi << 16));
+        one_pre<NS>(a, sh, ga, A, i0 + item(k));
+        gb = one_geo(sh, item(k + 1), n, a.nops);
+        one_issue_q<NS>(gb, B, gb.dep_ready != 0);
+        one_issue_w<NS>(gb, B);
+        one_compute<NS>(a, sh, ga, A, 0, i0 + item(k));
+        if (k + 1 >= m) break;
+        stamp(a, i0 + item(k + 1), 0, blockIdx.x | ((unsigned)gb.opi << 16));
+        one_pre<NS>(a, sh, gb, B, i0 + item(k + 1));
+        ga = one_geo(sh, item(k + 2), n, a.nops);
+        one_issue_q<NS>(ga, A, ga.dep_ready != 0);
+        one_issue_w<NS>(ga, A);
+        one_compute<NS>(a, sh, gb, B, 1, i0 + item(k + 1));
+    }
+    if (threadIdx.x == 0) {
+        __builtin_amdgcn_s_waitcnt(0);
+        const unsigned old = __hip_atomic_fetch_add(ctr_at(a.ctr, kCtrExit), 1u, __ATOMIC_RELAXED,
+                                                    __HIP_MEMORY_SCOPE_AGENT);
+        sh.last = old == gridDim.x - 1;
+    }
+    __syncthreads();
+    if (sh.last) {
+        for (int i = threadIdx.x; i < a.nops; i += kSNT) {
+            st_coh(done_ctr(a, i), 0u);
+            st_coh(qdone_ctr(a, i), 0u);
+        }
+        if (threadIdx.x == 0) st_coh(ctr_at(a.ctr, kCtrExit), 0u);
+    }
+}
+
+// ONE: the M = 1 launch (every GEMV item quantises its row).  WPE: waves per
+// SIMD the register budget allows (4: two workgroups per CU).
+template <bool ONE, int WPE>
+__global__ __launch_bounds__(kSNT, WPE) void stack_kernel(const StackArgs a) {
+    __shared__ Shared sh;
+    // this workgroup's items and (when they fit) every op descriptor into LDS
+    const int i0 = a.sched_off[blockIdx.x], n = a.sched_off[blockIdx.x + 1] - i0;
+    for (int i = threadIdx.x; i < n; i += kSNT) sh.items[i] = a.sched[i0 + i];
+    for (int i = threadIdx.x; i < a.nops * kDescWords; i += kSNT)
+        sh.desc[i] = reinterpret_cast<const unsigned*>(a.ops)[i];
+    for (int i = threadIdx.x; i < kKnownWords; i += kSNT) sh.known[i] = 0u;
+    __syncthreads();
+    for (int k = 0; k < n; ++k) {
+        const unsigned it = __builtin_amdgcn_readfirstlane(sh.items[k]);
+        const int opi = (int)(it >> 20), local = (int)(it & 0xfffff);
+        stamp(a, i0 + k, 0, blockIdx.x | ((unsigned)opi << 16));
+        const OpRef op = load_op(sh, opi);
+        const int nq = op.i(OPF(nq));
+        if (!ONE && local < nq) {
+            quant_item(a, sh, op, opi, local * kSW);
+        } else {
+            const int blk = local - nq;
+            if ((op.i(OPF(nch)) + kSW - 1) / kSW <= 2) gemv_item<2, ONE>(a, sh, op, opi, blk, i0 + k);
+            else gemv_item<4, ONE>(a, sh, op, opi, blk, i0 + k);
+        }
     }
     // the last workgroup out resets the counters for the next launch (its
     // own completion bumps have been performed before its exit is counted)
@@ -353,13 +731,10 @@ __global__ __launch_bounds__(kSNT) void stack_kernel(const StackArgs a) {
     __syncthreads();
     if (sh.last) {
         for (int i = threadIdx.x; i < a.nops; i += kSNT) {
-            st_coh(ctr_at(a.ctr, kCtrDone0 + i), 0u);
-            st_coh(ctr_at(a.ctr, kCtrDone0 + a.nops + i), 0u);
+            st_coh(done_ctr(a, i), 0u);
+            st_coh(qdone_ctr(a, i), 0u);
         }
-        if (threadIdx.x == 0) {
-            st_coh(ctr_at(a.ctr, kCtrTicket), 0u);
-            st_coh(ctr_at(a.ctr, kCtrExit), 0u);
-        }
+        if (threadIdx.x == 0) st_coh(ctr_at(a.ctr, kCtrExit), 0u);
     }
 }
 
@@ -367,15 +742,31 @@ __global__ __launch_bounds__(kSNT) void stack_kernel(const StackArgs a) {
 
 int stack_threads() { return kSNT; }
 int stack_max_chunks() { return 4 * kSW; }
+int stack_rows_per_quant_item() { return kSW; }
+
+// M = 1 launches take the pipelined kernel whose chunk slots per wave (NS)
+// cover every op of the stack; XTERN_STACK_PLAIN (tuning) the general one.
+static const void* stack_fn(int M, int ns) {
+    static const bool plain = getenv("XTERN_STACK_PLAIN") != nullptr;
+    if (M != 1 || plain) return reinterpret_cast<const void*>(stack_kernel<false, 2>);
+    if (ns <= 8) return reinterpret_cast<const void*>(stack_one_kernel<8>);
+    if (ns <= 10) return reinterpret_cast<const void*>(stack_one_kernel<10>);
+    if (ns <= 14) return reinterpret_cast<const void*>(stack_one_kernel<14>);
+    return reinterpret_cast<const void*>(stack_one_kernel<16>);
+}
+int stack_one_slots(int nch, int* rg) {
+    *rg = nch <= 16 ? 8 : 4;
+    return *rg == 8 ? nch : (nch + 1) / 2;
+}
+bool stack_pipelined(int M) { return M == 1 && getenv("XTERN_STACK_PLAIN") == nullptr; }
 
 hipError_t launch_stack(const StackArgs& a, int blocks, hipStream_t s) {
-    hipLaunchKernelGGL(stack_kernel, dim3(blocks), dim3(kSNT), 0, s, a);
-    return hipGetLastError();
+    void* args[] = {const_cast<StackArgs*>(&a)};
+    return hipLaunchKernel(stack_fn(a.M, a.slots), dim3(blocks), dim3(kSNT), args, 0, s);
 }
 
-hipError_t stack_blocks_per_cu(int* n) {
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(n, reinterpret_cast<const void*>(stack_kernel),
-                                                        kSNT, 0);
+hipError_t stack_blocks_per_cu(int M, int slots, int* n) {
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(n, stack_fn(M, slots), kSNT, 0);
 }
 
 }  // namespace xt
