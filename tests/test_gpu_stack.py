@@ -18,6 +18,10 @@ BITNET = {"q": (2560, 2560), "k": (2560, 640), "v": (2560, 640), "o": (2560, 256
           "gate": (2560, 6912), "up": (2560, 6912), "down": (6912, 2560)}
 SMALL = {"q": (256, 96), "k": (256, 32), "v": (256, 48), "o": (256, 256),
          "gate": (256, 300), "up": (256, 300), "down": (300 + 4, 256)}
+# K = 4096 (16 chunks: 4 row groups per M = 1 item) and K = 8192 (the
+# largest in_dim: 2 row groups per item, 4 waves per row group)
+MID = {"q": (4096, 256), "k": (4096, 64), "v": (4096, 80), "o": (4096, 512),
+       "gate": (4096, 1000), "up": (4096, 1000), "down": (8192, 4096)}
 
 
 def log(msg):
@@ -114,7 +118,9 @@ CASES = [("bitnet_m1_down_first", BITNET, 2, 1, "down_first", xtern.XT_QUANT_AVX
          ("bitnet_m32_down_first", BITNET, 1, 32, "down_first", xtern.XT_QUANT_AVX512),
          ("small_m1", SMALL, 4, 1, "chain", xtern.XT_QUANT_SCALAR),
          ("small_m3", SMALL, 4, 3, "chain", xtern.XT_QUANT_AVX512),
-         ("small_m17", SMALL, 3, 17, "down_first", xtern.XT_QUANT_SCALAR)]
+         ("small_m17", SMALL, 3, 17, "down_first", xtern.XT_QUANT_SCALAR),
+         ("mid_m1_chain", MID, 2, 1, "chain", xtern.XT_QUANT_AVX512),
+         ("mid_m3_down_first", MID, 1, 3, "down_first", xtern.XT_QUANT_SCALAR)]
 
 
 @pytest.mark.parametrize("name,shapes,layers,M,order,mode", CASES, ids=[c[0] for c in CASES])
