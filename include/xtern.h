@@ -65,7 +65,14 @@ enum {
  *                two's-complement nibbles per byte, column 2c low
  *                (dynamic_linear.rs:382-410).  As in Int4Linear's dot, the
  *                last column of an odd in_dim contributes nothing. */
-enum { XT_PACK4 = 0, XT_PACK5 = 1, XT_XORSPARSE = 2, XT_INT8 = 3, XT_INT4 = 4 };
+/*   XT_XORSPARSE_STREAM  the same XorSparse row blob as XT_XORSPARSE, kept
+ *                on the device in its compact form (block masks and set-order
+ *                sign bits, no expansion to 2-bit tiles): products read about
+ *                0.77x the tile bytes and expand the signs in registers.
+ *                in_dim up to 16384; products only (not the fused MLP or the
+ *                decode stack). */
+enum { XT_PACK4 = 0, XT_PACK5 = 1, XT_XORSPARSE = 2, XT_INT8 = 3, XT_INT4 = 4,
+       XT_XORSPARSE_STREAM = 5 };
 
 /* Activation rounding: which of the reference's two quantiser paths to
  * reproduce bit for bit (src/bit1_58/quantization.rs:170-195).
@@ -221,6 +228,17 @@ int xt_weights_info(const xt_weights* w, int* fmt, int64_t* in_dim, int64_t* out
 size_t xt_tile_bytes(int fmt, int64_t in_dim, int64_t out_dim);
 int xt_repack_host(int fmt, int64_t in_dim, int64_t out_dim, const void* host_bytes,
                    size_t nbytes, void* tiles_out);
+
+/* The device layout of XT_XORSPARSE_STREAM weights, built on the host (no
+ * GPU): *len = its size; with out (cap >= *len) the bytes, and sections[3]
+ * = byte offsets of the segment offsets (u32 [ceil(out/16)][ceil(in/64)]:
+ * bit offset of each 16-row group's block in the sign stream), the masks
+ * (u64 [group][block][16 rows], rows past out_dim 0) and the sign stream
+ * (u32 words; per group and block the 16 rows' set-order sign bits in row
+ * order, bit 1 = negative).  No reference counterpart: lets tests check the
+ * layout without a GPU. */
+int xt_xorsparse_stream_host(int64_t in_dim, int64_t out_dim, const void* blob, size_t nbytes,
+                             void* out, size_t cap, size_t* len, uint64_t* sections);
 
 /* Per-row absmax quantisation of x [M][K] f32 (device) into q [M][K] i8 and
  * inv_scale [M] f32 (device).  Bit-exact with quantize_f32_to_i8

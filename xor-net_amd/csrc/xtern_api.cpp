@@ -30,6 +30,9 @@ struct xt_weights {
     float* ws;          // device, N floats
     size_t tile_bytes;
     int device;
+    // XT_XORSPARSE_STREAM: the sections of `tiles` (build_xs_stream)
+    int64_t xs_nb;
+    size_t xs_mask_off, xs_sign_off, xs_seg_bytes, xs_mask_bytes, xs_sign_bytes;
 };
 
 namespace {
@@ -191,11 +194,46 @@ int run_product_int(const xt_weights* const* ws, int n, const int8_t* q, int ldq
     return XT_OK;
 }
 
+// XorSparse compact stream: one launch per projection and 16 token rows
+// (ldq >= ceil(K/64) * 64: the callers pad to whole 256-column chunks).
+int run_product_xs(const xt_weights* const* ws, int n, const int8_t* q, int ldq, const float* inv,
+                   int64_t M, float* const* ys, int32_t* acc, hipStream_t s) {
+    const int mb = xt::xs_max_rows();
+    for (int p = 0; p < n; ++p) {
+        const xt_weights* w = ws[p];
+        for (int64_t m0 = 0; m0 < M; m0 += mb) {
+            const int mr = (int)std::min<int64_t>(mb, M - m0);
+            xt::XsArgs a;
+            memset(&a, 0, sizeof a);
+            a.seg = reinterpret_cast<const uint32_t*>(w->tiles);
+            a.mask = reinterpret_cast<const uint32_t*>(w->tiles + w->xs_mask_off);
+            a.sign = reinterpret_cast<const uint32_t*>(w->tiles + w->xs_sign_off);
+            a.seg_bytes = (unsigned)w->xs_seg_bytes;
+            a.mask_bytes = (unsigned)w->xs_mask_bytes;
+            a.sign_bytes = (unsigned)w->xs_sign_bytes;
+            a.q = q + m0 * ldq;
+            a.q_bytes = (unsigned)((size_t)mr * ldq);
+            a.ldq = ldq;
+            a.inv = inv + m0;
+            a.ws = w->ws;
+            a.y = ys[p] + m0 * w->N;
+            a.acc = (n == 1 && acc) ? acc + m0 * w->N : nullptr;
+            a.M = mr;
+            a.N = (int)w->N;
+            a.nb = (int)w->xs_nb;
+            hipError_t e = xt::launch_xs_gemv(a, s);
+            if (e != hipSuccess) return hip_fail(e, "XorSparse stream GEMV launch");
+        }
+    }
+    return XT_OK;
+}
+
 int run_product(const xt_weights* const* ws, int n, const int8_t* q, int ldq, const float* inv,
                 const int32_t* rowsum, int64_t M, float* const* ys, int32_t* acc,
                 hipStream_t s, Scratch* sc = nullptr) {
     const int fmt = ws[0]->fmt;
     if (xt::is_int_format(fmt)) return run_product_int(ws, n, q, ldq, inv, M, ys, acc, s);
+    if (fmt == XT_XORSPARSE_STREAM) return run_product_xs(ws, n, q, ldq, inv, M, ys, acc, s);
     int ng_total = 0;
     for (int p = 0; p < n; ++p) ng_total += (int)((ws[p]->N + 15) / 16);
     const xt::MMConfig cfg =
@@ -269,7 +307,7 @@ int run_product(const xt_weights* const* ws, int n, const int8_t* q, int ldq, co
 // computing them for the long-K kernel costs more in the quantiser than the
 // kernel's own extra MFMA per k-step saves).
 bool wants_rowsum(const xt_weights* w, int64_t M) {
-    if (xt::is_int_format(w->fmt)) return false;
+    if (xt::is_int_format(w->fmt) || w->fmt == XT_XORSPARSE_STREAM) return false;
     return xt::choose_config(w->fmt, (int)M, 0, (int)w->nch, true).kind == 1;
 }
 
@@ -323,6 +361,7 @@ int gemv_fused_quant(const xt_weights* const* ws, int n, const float* x, int64_t
                      float* const* ys, int mode, hipStream_t s) {
     const bool disabled = getenv("XTERN_NO_FUSED_QUANT") != nullptr;
     const int fmt = ws[0]->fmt;
+    if (fmt == XT_XORSPARSE_STREAM) return 1;  // (its kernel takes i8 rows)
     const int64_t K = ws[0]->K;
     const int nch = (int)ws[0]->nch;
     static const bool staged = getenv("XTERN_GEMV_STAGED") != nullptr;
@@ -438,6 +477,9 @@ int mlp_run(const xt_weights* gate, const xt_weights* up, const xt_weights* down
         return fail(XT_ERR_INVALID, "gate and up projections must have the same shape and format");
     if (xt::is_int_format(gate->fmt))
         return fail(XT_ERR_UNSUPPORTED, "gate/up projections must be ternary");
+    if (gate->fmt == XT_XORSPARSE_STREAM || down->fmt == XT_XORSPARSE_STREAM)
+        return fail(XT_ERR_UNSUPPORTED,
+                    "the fused MLP takes tile formats; run XorSparse stream weights as separate products");
     if (down->K != gate->N)
         return fail(XT_ERR_INVALID, "down in_dim " + std::to_string(down->K) +
                                         " != intermediate size " + std::to_string(gate->N));
@@ -506,6 +548,8 @@ size_t xt_tile_bytes(int fmt, int64_t in_dim, int64_t out_dim) {
 int xt_repack_host(int fmt, int64_t in_dim, int64_t out_dim, const void* host_bytes,
                    size_t nbytes, void* tiles_out) {
     if (!host_bytes || !tiles_out) return fail(XT_ERR_INVALID, "NULL buffer");
+    if (fmt < 0 || fmt > 4)
+        return fail(XT_ERR_INVALID, "unknown tile format (XorSparse stream: xt_xorsparse_stream_host)");
     std::string err;
     if (xt::repack(fmt, in_dim, out_dim, host_bytes, nbytes, tiles_out, &err))
         return fail(XT_ERR_INVALID, err);
@@ -516,14 +560,15 @@ namespace {
 
 // A handle with device memory for `fmt`'s tiles and N scales (scales
 // uploaded, tiles left for the caller to fill).
-int weights_alloc(int fmt, int64_t K, int64_t N, const float* w_scales, xt_weights** out) {
+int weights_alloc(int fmt, int64_t K, int64_t N, const float* w_scales, xt_weights** out,
+                  size_t bytes = 0) {
     xt_weights* w = new (std::nothrow) xt_weights();
     if (!w) return fail(XT_ERR_NOMEM, "handle");
     w->fmt = fmt;
     w->K = K;
     w->N = N;
     w->nch = (K + xt::chunk_cols(fmt) - 1) / xt::chunk_cols(fmt);
-    w->tile_bytes = xt::tile_bytes(fmt, K, N);
+    w->tile_bytes = bytes ? bytes : xt::tile_bytes(fmt, K, N);
     hipError_t e = hipGetDevice(&w->device);
     if (e == hipSuccess) e = hipMalloc(&w->tiles, w->tile_bytes);
     if (e == hipSuccess) e = hipMalloc(&w->ws, (size_t)N * sizeof(float));
@@ -539,15 +584,68 @@ int weights_alloc(int fmt, int64_t K, int64_t N, const float* w_scales, xt_weigh
     return XT_OK;
 }
 
+// XT_XORSPARSE_STREAM: the blob re-laid as masks + set-order sign stream
+// (build_xs_stream), uploaded as one buffer.
+int weights_create_xs(int64_t K, int64_t N, const void* blob, size_t nbytes, const float* w_scales,
+                      xt_weights** out) {
+    if (K > (int64_t)xt::xs_max_blocks() * 64)
+        return fail(XT_ERR_UNSUPPORTED, "XorSparse stream weights take in_dim up to " +
+                                            std::to_string(xt::xs_max_blocks() * 64));
+    if (N > (int64_t)1 << 30) return fail(XT_ERR_UNSUPPORTED, "out_dim above 2^30 is not supported");
+    std::vector<uint8_t> host;
+    xt::XsLayout L;
+    std::string err;
+    if (xt::build_xs_stream(K, N, static_cast<const uint8_t*>(blob), nbytes, &host, &L, &err))
+        return fail(XT_ERR_INVALID, err);
+    xt_weights* w = nullptr;
+    if (int rc = weights_alloc(XT_XORSPARSE_STREAM, K, N, w_scales, &w, L.total)) return rc;
+    w->xs_nb = L.nb;
+    w->xs_mask_off = L.mask_off;
+    w->xs_sign_off = L.sign_off;
+    w->xs_seg_bytes = (size_t)(L.ng * L.nb) * 4;
+    w->xs_mask_bytes = (size_t)(L.ng * L.nb) * 128;
+    w->xs_sign_bytes = L.sign_bytes;
+    hipError_t e = hipMemcpy(w->tiles, host.data(), L.total, hipMemcpyHostToDevice);
+    if (e != hipSuccess) {
+        (void)xt_weights_destroy(w);
+        return hip_fail(e, "weight upload");
+    }
+    *out = w;
+    return XT_OK;
+}
+
 }  // namespace
+
+int xt_xorsparse_stream_host(int64_t in_dim, int64_t out_dim, const void* blob, size_t nbytes,
+                             void* out, size_t cap, size_t* len, uint64_t* sections) {
+    if (!blob || !len) return fail(XT_ERR_INVALID, "NULL blob or length pointer");
+    if (in_dim <= 0 || out_dim <= 0) return fail(XT_ERR_INVALID, "in_dim and out_dim must be positive");
+    std::vector<uint8_t> host;
+    xt::XsLayout L;
+    std::string err;
+    if (xt::build_xs_stream(in_dim, out_dim, static_cast<const uint8_t*>(blob), nbytes, &host, &L, &err))
+        return fail(XT_ERR_INVALID, err);
+    *len = L.total;
+    if (sections) {
+        sections[0] = L.seg_off;
+        sections[1] = L.mask_off;
+        sections[2] = L.sign_off;
+    }
+    if (out) {
+        if (cap < L.total) return fail(XT_ERR_INVALID, "buffer too small for the XorSparse stream");
+        memcpy(out, host.data(), L.total);
+    }
+    return XT_OK;
+}
 
 int xt_weights_create(int fmt, int64_t in_dim, int64_t out_dim, const void* host_bytes,
                       size_t nbytes, const float* w_scales, xt_weights** out) {
     if (!out) return fail(XT_ERR_INVALID, "out is NULL");
     *out = nullptr;
     if (!host_bytes || !w_scales) return fail(XT_ERR_INVALID, "NULL weight bytes or w_scales");
-    if (fmt < 0 || fmt > 4) return fail(XT_ERR_INVALID, "unknown weight format");
+    if (fmt < 0 || fmt > XT_XORSPARSE_STREAM) return fail(XT_ERR_INVALID, "unknown weight format");
     if (in_dim <= 0 || out_dim <= 0) return fail(XT_ERR_INVALID, "in_dim and out_dim must be positive");
+    if (fmt == XT_XORSPARSE_STREAM) return weights_create_xs(in_dim, out_dim, host_bytes, nbytes, w_scales, out);
     const size_t tb = xt::tile_bytes(fmt, in_dim, out_dim);
     std::vector<uint8_t> host;
     try {

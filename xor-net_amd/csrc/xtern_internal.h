@@ -131,6 +131,27 @@ struct MidArgs {
 constexpr int kActIdentity = 100;  // MidArgs::act: no activation (up unused)
 int mid_max_cols();
 hipError_t launch_mlp_mid(const MidArgs& a, int M, hipStream_t s);
+
+// GEMV over the XorSparse compact stream (xtern_xs.hip).  Sections as built
+// by build_xs_stream; q [M][ldq] i8 with ldq >= ceil(K/64) * 64 (zero past
+// K), M <= 16, nb = ceil(K/64) <= xs_max_blocks().
+struct XsArgs {
+    const uint32_t* seg;
+    const uint32_t* mask;
+    const uint32_t* sign;
+    unsigned seg_bytes, mask_bytes, sign_bytes;
+    const int8_t* q;
+    unsigned q_bytes;
+    int ldq;
+    const float* inv;
+    const float* ws;
+    float* y;
+    int32_t* acc;  // or null
+    int M, N, nb;
+};
+hipError_t launch_xs_gemv(const XsArgs& a, hipStream_t s);
+int xs_max_blocks();
+int xs_max_rows();
 // Address (on the current device) and size of the static device scratch used
 // by the allocation-free entry point; resolved once per device.
 hipError_t scratch_region(void** ptr, size_t* bytes);

@@ -207,6 +207,105 @@ int repack_int4(int64_t K, int64_t N, const uint8_t* src, size_t nbytes, uint8_t
 
 }  // namespace
 
+int build_xs_stream(int64_t K, int64_t N, const uint8_t* blob, size_t nbytes,
+                    std::vector<uint8_t>* out, XsLayout* lay, std::string* err) {
+    const int64_t nb = (K + 63) / 64, ng = (N + 15) / 16;
+    std::vector<uint64_t> mask, sgn;
+    try {
+        mask.assign((size_t)(ng * 16 * nb), 0);
+        sgn.assign((size_t)(ng * 16 * nb), 0);
+    } catch (...) {
+        *err = "host buffer for the XorSparse stream";
+        return -1;
+    }
+    // the blob, validated as for the tile layout (sparse.rs:135-194)
+    size_t p = 0;
+    uint64_t bits = 0;
+    for (int64_t o = 0; o < N; ++o) {
+        if (p + 4 > nbytes) {
+            *err = "XorSparse blob truncated at row " + std::to_string(o);
+            return -1;
+        }
+        const uint32_t nbr = (uint32_t)blob[p] | ((uint32_t)blob[p + 1] << 8) |
+                             ((uint32_t)blob[p + 2] << 16) | ((uint32_t)blob[p + 3] << 24);
+        p += 4;
+        if ((int64_t)nbr != nb) {
+            *err = "XorSparse row " + std::to_string(o) + ": num_blocks " + std::to_string(nbr) +
+                   " != ceil(in_dim/64) = " + std::to_string(nb);
+            return -1;
+        }
+        for (int64_t b = 0; b < nb; ++b) {
+            if (p + 8 > nbytes) {
+                *err = "XorSparse blob truncated at row " + std::to_string(o);
+                return -1;
+            }
+            uint64_t m = 0;
+            for (int t = 0; t < 8; ++t) m |= (uint64_t)blob[p + t] << (8 * t);
+            p += 8;
+            const int nnz = __builtin_popcountll(m);
+            const size_t sbytes = (size_t)(nnz + 7) / 8;
+            if (p + sbytes > nbytes) {
+                *err = "XorSparse blob truncated at row " + std::to_string(o);
+                return -1;
+            }
+            if (b * 64 + 64 > K && (m >> (K - b * 64)) != 0) {
+                *err = "XorSparse row " + std::to_string(o) + ": mask sets lanes beyond in_dim";
+                return -1;
+            }
+            uint64_t sb = 0;
+            for (size_t t = 0; t < sbytes; ++t) sb |= (uint64_t)blob[p + t] << (8 * t);
+            p += sbytes;
+            if (nnz < 64) sb &= ((uint64_t)1 << nnz) - 1;
+            mask[(size_t)(o * nb + b)] = m;
+            sgn[(size_t)(o * nb + b)] = sb;
+            bits += (uint64_t)nnz;
+        }
+    }
+    // Sections (each within a 32-bit buffer range; the kernel adds offsets
+    // below 2^31)
+    const uint64_t words = (bits + 31) / 32 + 3;  // + the window the last lane reads
+    XsLayout L;
+    L.nb = nb;
+    L.ng = ng;
+    L.seg_off = 0;
+    const uint64_t seg_b = (uint64_t)(ng * nb) * 4, mask_b = (uint64_t)(ng * nb) * 128;
+    L.mask_off = (size_t)((seg_b + 255) / 256 * 256);
+    L.sign_off = (size_t)((L.mask_off + mask_b + 255) / 256 * 256);
+    L.sign_bytes = (size_t)(words * 4);
+    L.total = L.sign_off + L.sign_bytes;
+    if (bits >= ((uint64_t)1 << 32) - 256 || mask_b >= ((uint64_t)1 << 31) ||
+        words * 4 >= ((uint64_t)1 << 31)) {
+        *err = "XorSparse stream above 2 GiB per section is not supported";
+        return -1;
+    }
+    try {
+        out->assign(L.total, 0);
+    } catch (...) {
+        *err = "host buffer for the XorSparse stream";
+        return -1;
+    }
+    uint8_t* base = out->data();
+    uint32_t* seg = reinterpret_cast<uint32_t*>(base + L.seg_off);
+    uint64_t* msk = reinterpret_cast<uint64_t*>(base + L.mask_off);
+    uint32_t* sw = reinterpret_cast<uint32_t*>(base + L.sign_off);
+    uint64_t pos = 0;
+    for (int64_t G = 0; G < ng; ++G)
+        for (int64_t b = 0; b < nb; ++b) {
+            seg[G * nb + b] = (uint32_t)pos;
+            for (int j = 0; j < 16; ++j) {
+                const int64_t o = G * 16 + j;
+                const uint64_t m = o < N ? mask[(size_t)(o * nb + b)] : 0;
+                const uint64_t sb = o < N ? sgn[(size_t)(o * nb + b)] : 0;
+                msk[(G * nb + b) * 16 + j] = m;
+                const int n = __builtin_popcountll(m);
+                for (int i = 0; i < n; ++i, ++pos)
+                    if ((sb >> i) & 1) sw[pos >> 5] |= 1u << (pos & 31);
+            }
+        }
+    *lay = L;
+    return 0;
+}
+
 // Int8Linear::new / Int4Linear::new (dynamic_linear.rs:236-258, :389-410).
 int int_quantize(int bits, const float* w, int64_t N, int64_t K, uint8_t* out, float* scales) {
     const float qmax = bits == 8 ? 127.0f : 7.0f;

@@ -56,6 +56,7 @@ XT_ERR_NOMEM = -3
 XT_ERR_UNSUPPORTED = -4
 
 XT_PACK4, XT_PACK5, XT_XORSPARSE = 0, 1, 2
+XT_XORSPARSE_STREAM = 5   # the XorSparse blob kept compact on the device
 XT_QUANT_AVX512, XT_QUANT_SCALAR = 0, 1
 
 _vp = ctypes.c_void_p
@@ -71,6 +72,8 @@ _lib.xt_weights_info.argtypes = [_vp, ctypes.POINTER(ctypes.c_int), ctypes.POINT
 _lib.xt_tile_bytes.argtypes = [ctypes.c_int, _i64, _i64]
 _lib.xt_tile_bytes.restype = _sz
 _lib.xt_repack_host.argtypes = [ctypes.c_int, _i64, _i64, _vp, _sz, _vp]
+_lib.xt_xorsparse_stream_host.argtypes = [_i64, _i64, _vp, _sz, _vp, _sz, ctypes.POINTER(_sz),
+                                          ctypes.POINTER(ctypes.c_uint64)]
 _lib.xt_hf_destripe.argtypes = [ctypes.c_int, _i64, _i64, _vp, _sz, _vp]
 _lib.xt_weights_create_hf.argtypes = [ctypes.c_int, _i64, _i64, _vp, _sz, ctypes.c_float,
                                       ctypes.c_int, ctypes.POINTER(_vp)]
@@ -314,8 +317,11 @@ class DeviceWeights:
         return self
 
     def read_tiles(self):
-        """The device tiles, copied to a host uint8 array."""
-        out = np.zeros(tile_bytes(self.fmt, self.in_dim, self.out_dim), dtype=np.uint8)
+        """The device tiles (XT_XORSPARSE_STREAM: the stream layout), copied
+        to a host uint8 array."""
+        n = (self.device_bytes() - 4 * self.out_dim if self.fmt == XT_XORSPARSE_STREAM
+             else tile_bytes(self.fmt, self.in_dim, self.out_dim))
+        out = np.zeros(n, dtype=np.uint8)
         _check(_lib.xt_weights_read_tiles(self.handle, out.ctypes.data_as(_vp), out.size))
         return out
 
@@ -339,6 +345,21 @@ class DeviceWeights:
 def tile_bytes(fmt, in_dim, out_dim):
     return _lib.xt_tile_bytes(fmt, in_dim, out_dim)
 
+
+
+def xorsparse_stream_host(in_dim, out_dim, blob):
+    """xt_xorsparse_stream_host: the device layout of XT_XORSPARSE_STREAM
+    weights built on the host.  Returns (uint8 array, (seg_off, mask_off,
+    sign_off))."""
+    buf = np.ascontiguousarray(np.frombuffer(bytes(blob), dtype=np.uint8))
+    n = _sz()
+    sec = (ctypes.c_uint64 * 3)()
+    _check(_lib.xt_xorsparse_stream_host(in_dim, out_dim, buf.ctypes.data_as(_vp), buf.size, None, 0,
+                                         ctypes.byref(n), sec))
+    out = np.zeros(n.value, dtype=np.uint8)
+    _check(_lib.xt_xorsparse_stream_host(in_dim, out_dim, buf.ctypes.data_as(_vp), buf.size,
+                                         out.ctypes.data_as(_vp), out.size, ctypes.byref(n), sec))
+    return out, (int(sec[0]), int(sec[1]), int(sec[2]))
 
 def repack_host(fmt, in_dim, out_dim, host_bytes):
     """Host repack into the device tile layout (no GPU needed)."""
