@@ -62,9 +62,10 @@ def tern_bytes(np, rng, N, K, fmt, p0=0.35):
 
 def make_copies(np, xtern, fmt, K, N, wb, ws, min_total):
     """Distinct device copies of one matrix, >= min_total bytes together."""
-    one = xtern.tile_bytes(fmt, K, N)
+    first = xtern.DeviceWeights(fmt, K, N, wb, ws)
+    one = first.device_bytes()
     n = max(1, -(-min_total // one))
-    return [xtern.DeviceWeights(fmt, K, N, wb, ws) for _ in range(n)]
+    return [first] + [xtern.DeviceWeights(fmt, K, N, wb, ws) for _ in range(n - 1)]
 
 
 def workload_c1(np, torch, xtern, rng):
@@ -251,7 +252,9 @@ def gemv_configs(np, torch, xtern, rng):
     cases = [("c2_pack5", xtern.XT_PACK5, 3200, 8640, (1, 8)),
              ("c2_pack5", xtern.XT_PACK5, 8640, 3200, (1, 8)),
              ("c3_xorsparse", xtern.XT_XORSPARSE, 4096, 14336, (1, 4, 16)),
-             ("c3_xorsparse", xtern.XT_XORSPARSE, 14336, 4096, (1, 4, 16))]
+             ("c3_xorsparse", xtern.XT_XORSPARSE, 14336, 4096, (1, 4, 16)),
+             ("c3_xorsparse_stream", xtern.XT_XORSPARSE_STREAM, 4096, 14336, (1, 4, 16)),
+             ("c3_xorsparse_stream", xtern.XT_XORSPARSE_STREAM, 14336, 4096, (1, 4, 16))]
     for name, fmt, K, N, Ms in cases:
         if fmt == xtern.XT_PACK5:
             wb, _ = tern_bytes(np, rng, N, K, fmt, p0=0.4)
@@ -265,6 +268,8 @@ def gemv_configs(np, torch, xtern, rng):
             del t
         ws = np.full(N, 0.8, np.float32)
         copies = make_copies(np, xtern, fmt, K, N, wb, ws, 2 * MALL_BYTES)
+        if fmt == xtern.XT_XORSPARSE_STREAM:  # the compact stream the kernel reads
+            wbytes = copies[0].device_bytes() - 4 * N
         for M in Ms:
             us_q, us_f = time_product(np, torch, xtern, copies, K, N, M, rng)
             alg = wbytes + M * K + 4 * M + 4 * N + 4 * M * N
@@ -274,6 +279,7 @@ def gemv_configs(np, torch, xtern, rng):
                  "hbm_frac": round(gbs / HBM_PEAK_GBS, 4)}
             if blob:
                 r["compact_blob_bytes"] = blob
+                r["weight_bytes_read"] = int(wbytes)
             out.append(r)
         del copies
         torch.cuda.empty_cache()
