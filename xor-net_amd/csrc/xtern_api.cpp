@@ -934,7 +934,7 @@ int xt_stack_create(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_st
         xt::StackOpDev& d = dops[(size_t)i];
         memset(&d, 0, sizeof d);
         // row groups per GEMV item (the M = 1 pipeline takes 8 for short K)
-        int rgi = xt::kStackRowGroups;
+        int rgi = xt::stack_gemv_rg((int)op.w[0]->nch);
         if (one) slots = std::max(slots, xt::stack_one_slots((int)op.w[0]->nch, &rgi));
         d.rg = rgi;
         int blocks = 0;

@@ -156,7 +156,7 @@ int xs_max_rows();
 // by the allocation-free entry point; resolved once per device.
 hipError_t scratch_region(void** ptr, size_t* bytes);
 // Persistent decode stack (xtern_stack.hip): one launch over a list of ops.
-constexpr int kStackRowGroups = 4;          // 16-row groups per GEMV item (M > 1)
+constexpr int kStackRowGroupsMax = 8;       // 16-row groups per GEMV item (M > 1): stack_gemv_rg
 constexpr int kStackMaxOps = 4095;
 constexpr int kStackMaxWgItems = 1024;      // items one workgroup may be dealt
 constexpr int kStackDescLdsBytes = 40 * 1024;  // every op descriptor is copied to LDS
@@ -190,6 +190,7 @@ struct StackArgs {
 };
 int stack_threads();
 int stack_max_chunks();  // chunks of K an op may have (4 per wave)
+int stack_gemv_rg(int nch);  // row groups per GEMV item of the M > 1 kernel
 int stack_rows_per_quant_item();
 hipError_t launch_stack(const StackArgs& a, int blocks, hipStream_t s);
 hipError_t stack_blocks_per_cu(int M, int slots, int* n);

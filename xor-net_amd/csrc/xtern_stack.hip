@@ -11,7 +11,8 @@
 //
 // Work list.  The host flattens the ops into items: M > 1 ops have
 // quantiser items (kSW input rows each), every op has one GEMV item per block
-// of up to kSRG 16-row groups of one of its projections (all of K).  It then
+// of 8 (K up to 16 chunks) or 4 16-row groups of one of its projections (all
+// of K).  It then
 // deals the list out to the workgroups (greedy, by bytes), each workgroup
 // getting its items in list order, and every item after the items it waits
 // for.  With every workgroup of the launch resident at once (the grid is
@@ -61,7 +62,6 @@ namespace {
 
 constexpr int kSW = 8;                 // waves per workgroup
 constexpr int kSNT = kSW * 64;         // threads per workgroup
-constexpr int kSRG = kStackRowGroups;  // 16-row groups per GEMV item
 constexpr int kDescWords = sizeof(StackOpDev) / 4;
 static_assert(kDescWords <= 64 && sizeof(StackOpDev) % 4 == 0, "a descriptor is one wave load");
 
@@ -135,7 +135,7 @@ constexpr int kDescLdsWords = kStackDescLdsBytes / 4;
 constexpr int kKnownWords = kStackMaxOps * 2 / 32 + 1;
 
 struct Shared {
-    v4i red[kSW][kSRG][64];
+    v4i red[kSW][kStackRowGroupsMax][64];
     unsigned desc[kDescLdsWords];          // every op descriptor
     unsigned items[kStackMaxWgItems];      // this workgroup's items, in order
     unsigned known[kKnownWords];           // completions this workgroup has seen
@@ -273,13 +273,13 @@ __device__ void quant_item(const StackArgs& a, Shared& sh, const OpRef& d, int o
         __hip_atomic_fetch_add(qdone_ctr(a, opi), (unsigned)rows, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// GEMV item: row groups G0 .. G0 + kSRG - 1 of projection p over all of K,
+// GEMV item: row groups G0 .. G0 + RG - 1 of projection p over all of K,
 // for every token.  Wave w multiplies chunks w, w + kSW, ... (NCW of them at
 // most).  ONE (M = 1): the item quantises the f32 input row itself in one
 // pass (each wave its own chunks' pieces, the row maximum through LDS), as
 // the decode GEMV does; otherwise it reads the rows the op's quantiser
 // items wrote.
-template <int NCW, bool ONE>
+template <int NCW, bool ONE, int RG>
 __device__ void gemv_item(const StackArgs& a, Shared& sh, const OpRef& d, int opi, int blk,
                           int pos) {
     const int lane = threadIdx.x & 63, wave = wave_id();
@@ -288,7 +288,7 @@ __device__ void gemv_item(const StackArgs& a, Shared& sh, const OpRef& d, int op
     const int ge0 = d.i(OPF(gend)), ge1 = d.i(OPF(gend) + 4), ge2 = d.i(OPF(gend) + 8);
     const int p = (np > 1 && blk >= ge0) + (np > 2 && blk >= ge1) + (np > 3 && blk >= ge2);
     const int b0 = p == 0 ? 0 : d.i(OPF(gend) + 4 * (p - 1));
-    const int G0 = (blk - b0) * kSRG;
+    const int G0 = (blk - b0) * RG;
     const int N = d.i(OPF(N) + 4 * p), NG = (N + 15) >> 4;
     const int nch = d.i(OPF(nch)), K = d.i(OPF(K)), M = a.M;
     const int dep = d.i(OPF(dep));
@@ -314,17 +314,17 @@ __device__ void gemv_item(const StackArgs& a, Shared& sh, const OpRef& d, int op
         for (int t = 0; t < NCW; ++t) x0[t] = ld_coh16(xr, voff, (unsigned)(wave + t * kSW) * 1024u);
     }
     __builtin_amdgcn_sched_barrier(0);
-    v4i wv[NCW][kSRG];
+    v4i wv[NCW][RG];
 #pragma unroll
     for (int t = 0; t < NCW; ++t) {
         const int c = wave + t * kSW;
 #pragma unroll
-        for (int r = 0; r < kSRG; ++r)  // (rows past N and chunks past K: zeros, no memory read)
+        for (int r = 0; r < RG; ++r)  // (rows past N and chunks past K: zeros, no memory read)
             wv[t][r] = ld_w16(wr, voff, c < nch ? (unsigned)(((G0 + r) * nch + c) * 1024) : kOutOfRange);
     }
     __builtin_amdgcn_sched_barrier(0);
     stamp(a, pos, 1, 0);
-    const int o = (G0 + min(wave, kSRG - 1)) * 16 + j;
+    const int o = (G0 + min(wave, RG - 1)) * 16 + j;
     const float wscale = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(
         rsrc(d.ptr<const float>(OPF(ws) + 8 * p), (unsigned)(N * 4)), (unsigned)min(o, N - 1) * 4u, 0, 0));
     if (ONE) {
@@ -400,10 +400,10 @@ __device__ void gemv_item(const StackArgs& a, Shared& sh, const OpRef& d, int op
 #pragma unroll
         for (int t = 0; t < NCW; ++t)
 #pragma unroll
-            for (int r = 0; r < kSRG; ++r) asm volatile("" : "+v"(wv[t][r]));
-        v4i acc[kSRG];
+            for (int r = 0; r < RG; ++r) asm volatile("" : "+v"(wv[t][r]));
+        v4i acc[RG];
 #pragma unroll
-        for (int r = 0; r < kSRG; ++r) acc[r] = v4i{0, 0, 0, 0};
+        for (int r = 0; r < RG; ++r) acc[r] = v4i{0, 0, 0, 0};
 #pragma unroll
         for (int t = 0; t < NCW; ++t) {
             // chunks past K: ONE's activations are zero there; the quantised
@@ -422,7 +422,7 @@ __device__ void gemv_item(const StackArgs& a, Shared& sh, const OpRef& d, int op
                 }
                 const v4i x = (live && j < mt) ? av : v4i{0, 0, 0, 0};
 #pragma unroll
-                for (int r = 0; r < kSRG; ++r) {
+                for (int r = 0; r < RG; ++r) {
                     v4i b = decode4(wv[t][r][s]);
 #pragma unroll
                     for (int e = 0; e < 4; ++e) b[e] = signed_codes(b[e]);
@@ -432,10 +432,10 @@ __device__ void gemv_item(const StackArgs& a, Shared& sh, const OpRef& d, int op
         }
         if (tb > 0) __syncthreads();  // the previous block's sums are read
 #pragma unroll
-        for (int r = 0; r < kSRG; ++r) sh.red[wave][r][lane] = acc[r];
+        for (int r = 0; r < RG; ++r) sh.red[wave][r][lane] = acc[r];
         __syncthreads();
         stamp(a, pos, 4, 0);
-        if (wave < kSRG && G0 + wave < NG && o < N) {
+        if (wave < RG && G0 + wave < NG && o < N) {
             v4i sum = sh.red[0][wave][lane];
 #pragma unroll
             for (int w = 1; w < kSW; ++w) sum += sh.red[w][wave][lane];
@@ -1092,8 +1092,9 @@ __global__ __launch_bounds__(kSNT, WPE) void stack_kernel(const StackArgs a) {
             quant_item(a, sh, op, opi, local * kSW, 1u);
         } else {
             const int blk = local - nq;
-            if ((op.i(OPF(nch)) + kSW - 1) / kSW <= 2) gemv_item<2, ONE>(a, sh, op, opi, blk, i0 + k);
-            else gemv_item<4, ONE>(a, sh, op, opi, blk, i0 + k);
+            // (row groups per item as the host dealt them: stack_gemv_rg)
+            if ((op.i(OPF(nch)) + kSW - 1) / kSW <= 2) gemv_item<2, ONE, 8>(a, sh, op, opi, blk, i0 + k);
+            else gemv_item<4, ONE, 4>(a, sh, op, opi, blk, i0 + k);
         }
     }
     // the last workgroup out resets the counters for the next launch (its
@@ -1119,6 +1120,7 @@ __global__ __launch_bounds__(kSNT, WPE) void stack_kernel(const StackArgs a) {
 int stack_threads() { return kSNT; }
 int stack_max_chunks() { return 4 * kSW; }
 int stack_rows_per_quant_item() { return kSW; }
+int stack_gemv_rg(int nch) { return (nch + kSW - 1) / kSW <= 2 ? 8 : 4; }
 
 // M = 1 launches take the pipelined kernel whose chunk slots per wave (NS)
 // cover every op of the stack; XTERN_STACK_PLAIN (tuning) the general one.
