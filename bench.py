@@ -22,7 +22,7 @@ Also reported, from the same process:
                VNNI dot, min(nproc, 8) threads, per-token tasks) on a bounded
                sample of the same workload
 
-    python bench.py [--steps K] [--warmup W] [--workload c1|c0|c2|c3|c4]
+    python bench.py [--steps K] [--warmup W] [--workload c1|c0|c3|c4]
                     [--no-cpu] [--copy-calibration]
 """
 import argparse
@@ -244,7 +244,7 @@ def time_product(np, torch, xtern, copies, K, N, M, rng, reps=200):
     return gq.time_ms(max(1, reps // n)) * 1e3, gf.time_ms(max(1, reps // n)) * 1e3
 
 
-def gemv_configs(np, torch, xtern, rng):
+def gemv_configs(np, torch, xtern, rng, only=None):
     """BASELINE configs[2] (Pack5) and configs[3] (XorSparse): µs per call,
     GB/s of algorithmic bytes (device weight bytes + M*K i8 + scales + f32
     out) against the 8 TB/s HBM peak; weights rotate over > 2x the MALL."""
@@ -256,6 +256,8 @@ def gemv_configs(np, torch, xtern, rng):
              ("c3_xorsparse_stream", xtern.XT_XORSPARSE_STREAM, 4096, 14336, (1, 4, 16)),
              ("c3_xorsparse_stream", xtern.XT_XORSPARSE_STREAM, 14336, 4096, (1, 4, 16))]
     for name, fmt, K, N, Ms in cases:
+        if only and not name.startswith(only):
+            continue
         if fmt == xtern.XT_PACK5:
             wb, _ = tern_bytes(np, rng, N, K, fmt, p0=0.4)
             wbytes = N * ((K + 4) // 5)
@@ -663,8 +665,12 @@ def main():
     if args.workload == "c4":
         print(json.dumps({"c4": stack_c4(np, torch, xtern, rng)}))
         return
+    if args.workload == "c3":
+        print(json.dumps({"c3": gemv_configs(np, torch, xtern, rng, only="c3")}))
+        return
     if args.workload != "c1":
-        raise SystemExit("workloads: c1 (the headline step), c0 (the M=1 GEMV alone), c4 (stack)")
+        raise SystemExit("workloads: c1 (the headline step), c0 (the M=1 GEMV alone), "
+                         "c3 (XorSparse: tiles and compact stream), c4 (stack)")
     log("setting up c1 weights (rotating copies) ...")
     wl = workload_c1(np, torch, xtern, rng)
 
