@@ -1552,6 +1552,25 @@ __host__ __device__ constexpr int g32s_xch_slot(int ncmax) { return ncmax >= 3 ?
 #endif
 constexpr int kG32sAhead = XT_G32S_AHEAD;
 
+// XT_G32S_TRACE (0 in the library): a tuning build records, per workgroup,
+// s_memrealtime (100 MHz) at entry (0), chunk 0 landed (1), MFMA loop done
+// (2), halves exchanged (3), outputs issued (4); loader wave 8 at all its
+// loads issued (5) and landed (6).  xt_debug_g32s_trace copies them out.
+#ifndef XT_G32S_TRACE
+#define XT_G32S_TRACE 0
+#endif
+#if XT_G32S_TRACE
+__device__ unsigned long long xt_g32s_trace[1024][8];
+#define XT_G32S_STAMP(k, who)                                                    \
+    do {                                                                         \
+        if ((who) && lin < 1024) xt_g32s_trace[lin][k] = wall_clock64();         \
+    } while (0)
+#else
+#define XT_G32S_STAMP(k, who) \
+    do {                      \
+    } while (0)
+#endif
+
 template <int NCMAX>
 __global__ __launch_bounds__(768) void gemm32s_kernel(const MMArgs a) {
     constexpr int CH = 256;
@@ -1569,6 +1588,7 @@ __global__ __launch_bounds__(768) void gemm32s_kernel(const MMArgs a) {
     asm volatile("" ::"s"(pb.np), "s"(pb.t0), "s"(pb.t1), "s"(pb.t2), "s"(pb.t3), "s"(gx), "s"(gy), "s"(gz));
     __builtin_amdgcn_sched_barrier(0);  // one round of argument loads
     const int lin = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
+    XT_G32S_STAMP(0, threadIdx.x == 0);
     const int t = xcd_remap(lin, gx * gy * gz);
     const int by = t % gy;
     const int bx = (t / gy) % gx;
@@ -1614,11 +1634,13 @@ __global__ __launch_bounds__(768) void gemm32s_kernel(const MMArgs a) {
                 __builtin_amdgcn_s_barrier();
             }
         }
+        XT_G32S_STAMP(5, threadIdx.x == 512);
 #pragma unroll
         for (int c = NCMAX - D + 1; c < NCMAX; ++c) {
             wait_vmcnt(2 * (NCMAX - 1 - c));
             __builtin_amdgcn_s_barrier();
         }
+        XT_G32S_STAMP(6, threadIdx.x == 512);
         __builtin_amdgcn_s_barrier();  // the MFMA waves' exchange
         __builtin_amdgcn_s_barrier();  // and output staging barriers
         return;
@@ -1671,6 +1693,7 @@ __global__ __launch_bounds__(768) void gemm32s_kernel(const MMArgs a) {
         for (int k = 0; k < 16; ++k) acc[s][k] = 0;
     v4i acur[4];
     __syncthreads();  // chunk 0 has landed
+    XT_G32S_STAMP(1, threadIdx.x == 0);
     read_a(0, acur);
 #pragma unroll
     for (int c = 0; c < NCMAX; ++c) {
@@ -1692,6 +1715,7 @@ __global__ __launch_bounds__(768) void gemm32s_kernel(const MMArgs a) {
     }
 #pragma unroll
     for (int k = 0; k < 16; ++k) acc[0][k] += acc[1][k] + acc[2][k] + acc[3][k];
+    XT_G32S_STAMP(2, threadIdx.x == 0);
 
     // Add the halves L through LDS, in slots 0-1 when every wave is past
     // their reads (their chunks completed before the last chunk's barrier),
@@ -1713,6 +1737,7 @@ __global__ __launch_bounds__(768) void gemm32s_kernel(const MMArgs a) {
         }
     }
     __syncthreads();
+    XT_G32S_STAMP(3, threadIdx.x == 0);
     // Code-domain sums of the 32 x 128 tile -> LDS (slot 1), then whole rows.
     int32_t* dtile = reinterpret_cast<int32_t*>(xch + 4096);  // [32][128], two slots on
 #pragma unroll
@@ -1756,6 +1781,7 @@ __global__ __launch_bounds__(768) void gemm32s_kernel(const MMArgs a) {
             }
         }
     }
+    XT_G32S_STAMP(4, threadIdx.x == 0);
 }
 
 int gemm32s_ncmax() { return 18; }
@@ -2699,6 +2725,15 @@ hipError_t launch_mlp_mid(const MidArgs& a0, int M, hipStream_t s) {
 }
 
 }  // namespace xt
+
+#if XT_G32S_TRACE
+extern "C" int xt_debug_g32s_trace(unsigned long long* out) {
+    return hipMemcpyFromSymbol(out, HIP_SYMBOL(xt::xt_g32s_trace), sizeof(unsigned long long) * 1024 * 8) ==
+                   hipSuccess
+               ? 0
+               : -2;
+}
+#endif
 
 #if XT_MID_STATS
 extern "C" int xt_debug_mid_stats(unsigned long long* out) {
