@@ -722,13 +722,22 @@ bool gemv_fits(int fmt, int M, int nch, int waves, int ncw) {
 // as quantize_kernel): each lane reads its pieces as f32, the per-token
 // absmax goes through the waves' shuffles and LDS (one barrier), then each
 // lane quantises its own pieces.  No separate quantiser launch.
-template <int FMT, int WAVES, int NCW, bool FUSED, int RG>
+// AM > 0 (M <= AM, q given): the wave's activation bytes (rows < M of its
+// chunks, 256 / 320 bytes each) are loaded once, one distinct 16-byte piece
+// per lane, passed through a wave-private LDS slice and read back as MFMA
+// fragments, instead of every lane loading its four / five pieces from
+// memory (16 token lanes per fragment, most of them duplicates for small M).
+template <int FMT, int WAVES, int NCW, bool FUSED, int RG, int AM = 0>
 __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
     constexpr int STEPS = (FMT == XT_PACK5) ? 5 : 4;
     constexpr int CH = STEPS * 64;
     // 1 KiB tiles per chunk: Int8 one per k-step, Int4 one per two k-steps
     constexpr int TPC = (FMT == XT_INT8) ? 4 : (FMT == XT_INT4 ? 2 : 1);
+    constexpr int APR = NCW * CH / 16;                   // pieces per row and wave
+    constexpr int APW = AM > 0 ? AM * APR : 1;           // pieces per wave
+    constexpr int ALL = (APW + 63) / 64;                 // of them per lane
     __shared__ v4i red[WAVES][RG][64];
+    __shared__ v4i aslice[WAVES][APW];
     __shared__ unsigned tmax[WAVES][16];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -763,7 +772,40 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
         wsrc[r] = pv.tiles + ((size_t)min(G0 + r, NG - 1) * nch * TPC * 64 + lane) * 16;
     v4i wv[NCW][RG][TPC];
     v4i av[NCW][STEPS];
-    if constexpr (!FUSED) {
+    if constexpr (AM > 0) {
+        static_assert(!FUSED, "AM takes quantised rows");
+        const int npc = M * APR;  // pieces of rows < M
+        v4i ap[ALL];
+#pragma unroll
+        for (int u = 0; u < ALL; ++u) {
+            const int p = min(lane + 64 * u, npc - 1);
+            const int m = p / APR, pr = p - m * APR;
+            const int c = min(wave + (pr / (CH / 16)) * WAVES, nch - 1);
+            ap[u] = ld_cached(q + (size_t)m * ldq + (size_t)c * CH + (pr % (CH / 16)) * 16);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < NCW; ++t) {
+            const int c = min(wave + t * WAVES, nch - 1);
+#pragma unroll
+            for (int r = 0; r < RG; ++r)
+#pragma unroll
+                for (int u = 0; u < TPC; ++u)
+                    wv[t][r][u] = ld_stream(wsrc[r] + ((size_t)c * TPC + u) * kTileBytes);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // (a wave's LDS accesses complete in order: the reads below see
+        // these stores without a barrier)
+#pragma unroll
+        for (int u = 0; u < ALL; ++u)
+            if (lane + 64 * u < npc) aslice[wave][lane + 64 * u] = ap[u];
+        __asm__ volatile("" ::: "memory");
+        const int jr = min(j, M - 1) * APR;
+#pragma unroll
+        for (int t = 0; t < NCW; ++t)
+#pragma unroll
+            for (int s = 0; s < STEPS; ++s) av[t][s] = aslice[wave][jr + t * (CH / 16) + 4 * s + g];
+    } else if constexpr (!FUSED) {
         const int8_t* arow = q + (size_t)min(j, M - 1) * ldq + 16 * g;
 #pragma unroll
         for (int t = 0; t < NCW; ++t) {
@@ -1074,6 +1116,42 @@ int gemv2_fused_max(int fmt, int nch, int rg) {
     return gemv2_waves(nch) * 64 * 32;
 }
 
+// Quantised rows given: the activation pieces through a wave-private LDS
+// slice when the wave multiplies two or more chunks and the slice of M rows
+// fits (measured: 14336 -> 4096 at M = 1 / 4 6.42 -> 5.24-5.39 / 6.93 ->
+// 6.04 us; Pack5 3200 -> 8640 at M = 1 / 8 4.80 -> 4.48-4.54 / 5.99 ->
+// 5.23; with one chunk per wave it did not help: 4096 -> 14336 at M = 1
+// 5.33 -> 5.55).
+template <int FMT, int W, int NCW, int RG, int AM>
+static constexpr bool gemv2_am_fits() {
+    return (size_t)W * AM * NCW * (FMT == XT_PACK5 ? 320 : 256) + (size_t)W * RG * 1024 <= 120 * 1024;
+}
+template <int FMT, int W, int NCW, int RG>
+static hipError_t launch_gemv2_am(const MMArgs& a, int ntiles, hipStream_t s) {
+    static const bool off = getenv("XTERN_GEMV_NO_AM") != nullptr;  // (measurement switch)
+    const dim3 g(ntiles), b(W * 64);
+    if constexpr (NCW >= 2) {
+        if (!off && a.M == 1) {
+            hipLaunchKernelGGL((gemv2_kernel<FMT, W, NCW, false, RG, 1>), g, b, 0, s, a);
+            return hipGetLastError();
+        }
+        if constexpr (gemv2_am_fits<FMT, W, NCW, RG, 4>()) {
+            if (!off && a.M <= 4) {
+                hipLaunchKernelGGL((gemv2_kernel<FMT, W, NCW, false, RG, 4>), g, b, 0, s, a);
+                return hipGetLastError();
+            }
+        }
+        if constexpr (gemv2_am_fits<FMT, W, NCW, RG, 8>()) {
+            if (!off && a.M <= 8) {
+                hipLaunchKernelGGL((gemv2_kernel<FMT, W, NCW, false, RG, 8>), g, b, 0, s, a);
+                return hipGetLastError();
+            }
+        }
+    }
+    hipLaunchKernelGGL((gemv2_kernel<FMT, W, NCW, false, RG>), g, b, 0, s, a);
+    return hipGetLastError();
+}
+
 // The staging-free GEMV applies to ternary tiles (given or fused-quantised rows).
 template <int RG>
 static hipError_t launch_gemv2_rg(int fmt, const MMArgs& a, int ntiles, hipStream_t s) {
@@ -1095,7 +1173,7 @@ static hipError_t launch_gemv2_rg(int fmt, const MMArgs& a, int ntiles, hipStrea
                 hipLaunchKernelGGL((gemv2_kernel<XT_PACK4, W_, NCW_, true, RG>), dim3(ntiles), dim3(W_ * 64), st_, s, a); \
             }                                                                                    \
         } else if (fmt == XT_PACK5) {                                                            \
-            hipLaunchKernelGGL((gemv2_kernel<XT_PACK5, W_, NCW_, false, RG>), dim3(ntiles), dim3(W_ * 64), 0, s, a); \
+            return launch_gemv2_am<XT_PACK5, W_, NCW_, RG>(a, ntiles, s);                      \
         } else if (fmt == XT_INT8) {                                                             \
             if constexpr (NCW_ <= 2)                                                             \
                 hipLaunchKernelGGL((gemv2_kernel<XT_INT8, W_, NCW_, false, RG>), dim3(ntiles), dim3(W_ * 64), 0, s, a); \
@@ -1107,7 +1185,7 @@ static hipError_t launch_gemv2_rg(int fmt, const MMArgs& a, int ntiles, hipStrea
             else                                                                                 \
                 return hipErrorInvalidValue;                                                     \
         } else {                                                                                 \
-            hipLaunchKernelGGL((gemv2_kernel<XT_PACK4, W_, NCW_, false, RG>), dim3(ntiles), dim3(W_ * 64), 0, s, a); \
+            return launch_gemv2_am<XT_PACK4, W_, NCW_, RG>(a, ntiles, s);                      \
         }                                                                                        \
         return hipGetLastError();                                                                \
     }
@@ -1115,7 +1193,7 @@ static hipError_t launch_gemv2_rg(int fmt, const MMArgs& a, int ntiles, hipStrea
     // 8640: 4.8 vs 5.3 us at M = 1, 6.0 vs 6.2 at M = 8; Pack4 is fastest
     // with one chunk per wave)
     if (fmt == XT_PACK5 && !a.x && nch > 4 && nch <= 10) {
-        hipLaunchKernelGGL((gemv2_kernel<XT_PACK5, 5, 2, false, RG>), dim3(ntiles), dim3(5 * 64), 0, s, a);
+        return launch_gemv2_am<XT_PACK5, 5, 2, RG>(a, ntiles, s);
         return hipGetLastError();
     }
     // Above 16 chunks, 14 waves where they cover K with the same chunks per
