@@ -963,7 +963,9 @@ int xt_stack_create(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_st
         d.x = op.x;
         d.dep = op.dep;
         d.dep_items = op.dep >= 0 ? dops[(size_t)op.dep].ngemv : 0;
-        d.nq = (M > 1 || one) ? (int)((M + rq - 1) / rq) : 0;
+        // quantiser items for every op: both kernels read the rows they write
+        // (a GEMV item of the general kernel dereferences d.q / d.inv)
+        d.nq = (int)((M + rq - 1) / rq);
         d.ngemv = blocks;
         if (d.nq + blocks >= (1 << 20)) return fail(XT_ERR_UNSUPPORTED, at + "too many rows");
         if (op.dep >= 0) dops[(size_t)op.dep].pub = 1;
@@ -1070,7 +1072,7 @@ int xt_stack_create(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_st
     char* sc = mem + ops_b + off_b + items_b + ctr_b;
     for (int i = 0; i < nops; ++i) {
         xt::StackOpDev& d = dops[(size_t)i];
-        if (d.nq == 0) continue;
+        if (d.nq == 0) continue;  // (not reached: every op has quantiser items)
         const size_t qb = align_up((size_t)M * d.ldq, 256);
         d.q = reinterpret_cast<int8_t*>(sc + qoff[(size_t)i]);
         d.inv = reinterpret_cast<float*>(sc + qoff[(size_t)i] + qb);

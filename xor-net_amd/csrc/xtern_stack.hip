@@ -1123,11 +1123,11 @@ int stack_rows_per_quant_item() { return kSW; }
 int stack_gemv_rg(int nch) { return (nch + kSW - 1) / kSW <= 2 ? 8 : 4; }
 
 // M = 1 launches take the pipelined kernel whose chunk slots per wave (NS)
-// cover every op of the stack; XTERN_STACK_PLAIN (tuning) the general one.
+// cover every op of the stack; M > 1 the general one (which reads rows its
+// quantiser items wrote: the host lists those items for every op).
 #if XT_STACK_PIPE3
 static const void* stack_fn(int M, int ns) {
-    static const bool plain = getenv("XTERN_STACK_PLAIN") != nullptr;
-    if (M != 1 || plain) return reinterpret_cast<const void*>(stack_kernel<false, 2>);
+    if (M != 1) return reinterpret_cast<const void*>(stack_kernel<false, 2>);
     if (ns <= 8) return reinterpret_cast<const void*>(stack_one_kernel<8>);
     return reinterpret_cast<const void*>(stack_one_kernel<10>);
 }
@@ -1139,8 +1139,7 @@ int stack_one_slots(int nch, int* rg) {
 }
 #else
 static const void* stack_fn(int M, int ns) {
-    static const bool plain = getenv("XTERN_STACK_PLAIN") != nullptr;
-    if (M != 1 || plain) return reinterpret_cast<const void*>(stack_kernel<false, 2>);
+    if (M != 1) return reinterpret_cast<const void*>(stack_kernel<false, 2>);
     if (ns <= 8) return reinterpret_cast<const void*>(stack_one_kernel<8>);
     if (ns <= 10) return reinterpret_cast<const void*>(stack_one_kernel<10>);
     if (ns <= 14) return reinterpret_cast<const void*>(stack_one_kernel<14>);
@@ -1151,7 +1150,7 @@ int stack_one_slots(int nch, int* rg) {
     return *rg == 8 ? nch : (nch + 1) / 2;
 }
 #endif
-bool stack_pipelined(int M) { return M == 1 && getenv("XTERN_STACK_PLAIN") == nullptr; }
+bool stack_pipelined(int M) { return M == 1; }
 
 hipError_t launch_stack(const StackArgs& a, int blocks, hipStream_t s) {
     void* args[] = {const_cast<StackArgs*>(&a)};
