@@ -734,10 +734,13 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
     // 1 KiB tiles per chunk: Int8 one per k-step, Int4 one per two k-steps
     constexpr int TPC = (FMT == XT_INT8) ? 4 : (FMT == XT_INT4 ? 2 : 1);
     constexpr int APR = NCW * CH / 16;                   // pieces per row and wave
+    constexpr int APS = APR + 1;                         // row stride in the slice: one
+                                                         // piece of padding, so the rows
+                                                         // of a fragment read hit distinct banks
     constexpr int APW = AM > 0 ? AM * APR : 1;           // pieces per wave
     constexpr int ALL = (APW + 63) / 64;                 // of them per lane
     __shared__ v4i red[WAVES][RG][64];
-    __shared__ v4i aslice[WAVES][APW];
+    __shared__ v4i aslice[WAVES][AM > 0 ? AM * APS : 1];
     __shared__ unsigned tmax[WAVES][16];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -798,9 +801,9 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
         // these stores without a barrier)
 #pragma unroll
         for (int u = 0; u < ALL; ++u)
-            if (lane + 64 * u < npc) aslice[wave][lane + 64 * u] = ap[u];
+            if (lane + 64 * u < npc) aslice[wave][lane + 64 * u + (lane + 64 * u) / APR] = ap[u];
         __asm__ volatile("" ::: "memory");
-        const int jr = min(j, M - 1) * APR;
+        const int jr = min(j, M - 1) * APS;
 #pragma unroll
         for (int t = 0; t < NCW; ++t)
 #pragma unroll
@@ -1124,7 +1127,7 @@ int gemv2_fused_max(int fmt, int nch, int rg) {
 // 5.33 -> 5.55).
 template <int FMT, int W, int NCW, int RG, int AM>
 static constexpr bool gemv2_am_fits() {
-    return (size_t)W * AM * NCW * (FMT == XT_PACK5 ? 320 : 256) + (size_t)W * RG * 1024 <= 120 * 1024;
+    return (size_t)W * AM * (NCW * (FMT == XT_PACK5 ? 320 : 256) + 16) + (size_t)W * RG * 1024 <= 120 * 1024;
 }
 template <int FMT, int W, int NCW, int RG>
 static hipError_t launch_gemv2_am(const MMArgs& a, int ntiles, hipStream_t s) {
