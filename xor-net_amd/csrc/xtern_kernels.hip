@@ -273,6 +273,9 @@ __device__ __forceinline__ ProjView select_proj(const ProjBounds& pb, int bx) {
 // planes, runs the epilogue and clears the counter for the next call.
 // OWN_ROWSUM (MB == 1): the activation row sums come from one extra MFMA per
 // k-step against an all-ones B operand instead of the caller.
+#ifndef XT_MM_SLICE
+#define XT_MM_SLICE 1
+#endif
 template <int FMT, int MB, int NB, int WAVES, int PF, bool OWN_ROWSUM>
 __global__ __launch_bounds__(WAVES * 64) void mm_kernel(const MMArgs a) {
     constexpr int STEPS = (FMT == XT_PACK5) ? 5 : 4;
@@ -282,6 +285,16 @@ __global__ __launch_bounds__(WAVES * 64) void mm_kernel(const MMArgs a) {
     static_assert(!OWN_ROWSUM || MB == 1, "in-kernel row sums need MB == 1");
     __shared__ v4i red[WAVES][NACC][64];
     __shared__ int last_flag;
+    // SLICE (one 16-token block, 2-bit tiles): each activation load covers
+    // 4 token rows x 256 bytes, one distinct 16-byte piece per lane, instead
+    // of 16 rows x 64 bytes (an instruction spanning 16 rows at the row
+    // stride kept the address path stalled on translation); the pieces go
+    // through a wave-private LDS slice (rows padded by one piece) and come
+    // back as MFMA fragments.  No barrier: a wave's LDS accesses complete in
+    // order.
+    constexpr bool SLICE = XT_MM_SLICE && FMT != XT_PACK5 && MB == 1 &&
+                           WAVES * NACC * 1024 + WAVES * PF * 16 * 17 * 16 <= 150 * 1024;
+    __shared__ v4i aslice[WAVES][SLICE ? PF : 1][SLICE ? 16 * 17 : 1];
 
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -334,6 +347,15 @@ __global__ __launch_bounds__(WAVES * 64) void mm_kernel(const MMArgs a) {
                                  ? ld_stream(tiles + ((size_t)(G * nch + c) * 64 + lane) * 16)
                                  : zero;
             }
+            if constexpr (SLICE) {
+                // (clamped rows and chunk: zeroed when read back)
+                const int cc = min(c, cend - 1);
+#pragma unroll
+                for (int u = 0; u < 4; ++u) {
+                    const int row = min(mbase + 4 * u + (lane >> 4), M - 1);
+                    av[pp][0][u] = ld_cached(qbase + (size_t)row * ldq + cc * CH + (lane & 15) * 16);
+                }
+            } else {
 #pragma unroll
             for (int mb = 0; mb < MB; ++mb) {
                 const int row = mbase + mb * 16 + j;
@@ -342,6 +364,26 @@ __global__ __launch_bounds__(WAVES * 64) void mm_kernel(const MMArgs a) {
                     av[pp][mb][s] = (c < cend && row < M)
                                         ? ld_cached(qbase + (size_t)row * ldq + c * CH + s * 64 + g * 16)
                                         : zero;
+            }
+            }
+        }
+        if constexpr (SLICE) {
+            // rows 4u + lane / 16, piece lane % 16 -> the fragments of
+            // lane (g, j): row j, pieces 4 s + g
+#pragma unroll
+            for (int pp = 0; pp < PF; ++pp)
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    aslice[wave][pp][(4 * u + (lane >> 4)) * 17 + (lane & 15)] = av[pp][0][u];
+            __asm__ volatile("" ::: "memory");
+#pragma unroll
+            for (int pp = 0; pp < PF; ++pp) {
+                const bool live = c0 + pp * WAVES < cend && mbase + j < M;
+#pragma unroll
+                for (int s = 0; s < STEPS; ++s) {
+                    const v4i v = aslice[wave][pp][j * 17 + 4 * s + g];
+                    av[pp][0][s] = live ? v : zero;
+                }
             }
         }
 #pragma unroll
