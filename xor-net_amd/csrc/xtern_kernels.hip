@@ -782,7 +782,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
     constexpr int APW = AM > 0 ? AM * APR : 1;           // pieces per wave
     constexpr int ALL = (APW + 63) / 64;                 // of them per lane
     __shared__ v4i red[WAVES][RG][64];
-    __shared__ v4i aslice[WAVES][AM > 0 ? AM * APS : 1];
+    __shared__ v4i aslice[WAVES][AM == 16 ? 16 * 17 : (AM > 0 ? AM * APS : 1)];
     __shared__ unsigned tmax[WAVES][16];
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
@@ -817,7 +817,44 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
         wsrc[r] = pv.tiles + ((size_t)min(G0 + r, NG - 1) * nch * TPC * 64 + lane) * 16;
     v4i wv[NCW][RG][TPC];
     v4i av[NCW][STEPS];
-    if constexpr (AM > 0) {
+    if constexpr (AM == 16) {
+        // 9-16 rows of 2-bit tiles: each activation load covers 4 token rows
+        // x 256 bytes of one chunk (one instruction spanning 16 rows at the
+        // row stride stalls the address path on translation); chunk by
+        // chunk the 16 rows go through the wave's LDS slice (rows padded by
+        // one piece) and come back as MFMA fragments.
+        static_assert(!FUSED && FMT != XT_PACK5, "AM 16: quantised rows, 2-bit tiles");
+#pragma unroll
+        for (int t = 0; t < NCW; ++t) {
+            const int c = min(wave + t * WAVES, nch - 1);
+#pragma unroll
+            for (int u = 0; u < 4; ++u)  // (rows >= M clamped, zeroed at the MFMA)
+                av[t][u] = ld_cached(q + (size_t)min(4 * u + (lane >> 4), M - 1) * ldq + (size_t)c * CH +
+                                     (lane & 15) * 16);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int t = 0; t < NCW; ++t) {
+            const int c = min(wave + t * WAVES, nch - 1);
+#pragma unroll
+            for (int r = 0; r < RG; ++r)
+#pragma unroll
+                for (int u = 0; u < TPC; ++u)
+                    wv[t][r][u] = ld_stream(wsrc[r] + ((size_t)c * TPC + u) * kTileBytes);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        // (a wave's LDS accesses complete in order: each chunk's reads see
+        // its stores, and precede the next chunk's stores)
+#pragma unroll
+        for (int t = 0; t < NCW; ++t) {
+#pragma unroll
+            for (int u = 0; u < 4; ++u) aslice[wave][(4 * u + (lane >> 4)) * 17 + (lane & 15)] = av[t][u];
+            __asm__ volatile("" ::: "memory");
+#pragma unroll
+            for (int st = 0; st < 4; ++st) av[t][st] = aslice[wave][j * 17 + 4 * st + g];
+            __asm__ volatile("" ::: "memory");
+        }
+    } else if constexpr (AM > 0) {
         static_assert(!FUSED, "AM takes quantised rows");
         const int npc = M * APR;  // pieces of rows < M
         v4i ap[ALL];
@@ -1191,6 +1228,15 @@ static hipError_t launch_gemv2_am(const MMArgs& a, int ntiles, hipStream_t s) {
                 hipLaunchKernelGGL((gemv2_kernel<FMT, W, NCW, false, RG, 8>), g, b, 0, s, a);
                 return hipGetLastError();
             }
+        }
+    }
+    // 5-16 rows of 2-bit tiles the slices above do not take: 4-row loads,
+    // staged chunk by chunk (measured: TA address stalls 68 % -> see the
+    // profile of this kernel)
+    if constexpr (FMT == XT_PACK4 && (size_t)W * (16 * 17 * 16 + RG * 1024) <= 150 * 1024) {
+        if (!off && a.M > 4 && a.M <= 16) {
+            hipLaunchKernelGGL((gemv2_kernel<FMT, W, NCW, false, RG, 16>), g, b, 0, s, a);
+            return hipGetLastError();
         }
     }
     hipLaunchKernelGGL((gemv2_kernel<FMT, W, NCW, false, RG>), g, b, 0, s, a);
