@@ -823,7 +823,7 @@ __global__ __launch_bounds__(WAVES * 64) void gemv2_kernel(const MMArgs a) {
         // row stride stalls the address path on translation); chunk by
         // chunk the 16 rows go through the wave's LDS slice (rows padded by
         // one piece) and come back as MFMA fragments.
-        static_assert(!FUSED && FMT != XT_PACK5, "AM 16: quantised rows, 2-bit tiles");
+        static_assert(!FUSED && FMT != XT_PACK5, "AM 16: quantised rows, 256-column chunks");
 #pragma unroll
         for (int t = 0; t < NCW; ++t) {
             const int c = min(wave + t * WAVES, nch - 1);
@@ -1243,6 +1243,24 @@ static hipError_t launch_gemv2_am(const MMArgs& a, int ntiles, hipStream_t s) {
     return hipGetLastError();
 }
 
+// Int8 rows given: 5-16 rows take the 4-row activation loads staged through
+// the LDS slice, as the ternary tiles do (measured on the 128256-row head at
+// M = 16: Int8 63.2 -> 60.2 us; Int4 36.4 -> 38.1, so Int4 keeps the direct
+// loads).
+template <int FMT, int W, int NCW, int RG>
+static hipError_t launch_gemv2_int(const MMArgs& a, int ntiles, hipStream_t s) {
+    static const bool off = getenv("XTERN_GEMV_NO_AM") != nullptr;  // (measurement switch)
+    const dim3 g(ntiles), b(W * 64);
+    if constexpr (FMT == XT_INT8 && (size_t)W * (16 * 17 * 16 + RG * 1024) <= 150 * 1024) {
+        if (!off && a.M > 4 && a.M <= 16) {
+            hipLaunchKernelGGL((gemv2_kernel<FMT, W, NCW, false, RG, 16>), g, b, 0, s, a);
+            return hipGetLastError();
+        }
+    }
+    hipLaunchKernelGGL((gemv2_kernel<FMT, W, NCW, false, RG>), g, b, 0, s, a);
+    return hipGetLastError();
+}
+
 // The staging-free GEMV applies to ternary tiles (given or fused-quantised rows).
 template <int RG>
 static hipError_t launch_gemv2_rg(int fmt, const MMArgs& a, int ntiles, hipStream_t s) {
@@ -1267,12 +1285,12 @@ static hipError_t launch_gemv2_rg(int fmt, const MMArgs& a, int ntiles, hipStrea
             return launch_gemv2_am<XT_PACK5, W_, NCW_, RG>(a, ntiles, s);                      \
         } else if (fmt == XT_INT8) {                                                             \
             if constexpr (NCW_ <= 2)                                                             \
-                hipLaunchKernelGGL((gemv2_kernel<XT_INT8, W_, NCW_, false, RG>), dim3(ntiles), dim3(W_ * 64), 0, s, a); \
+                return launch_gemv2_int<XT_INT8, W_, NCW_, RG>(a, ntiles, s);                        \
             else                                                                                 \
                 return hipErrorInvalidValue;                                                     \
         } else if (fmt == XT_INT4) {                                                             \
             if constexpr (NCW_ <= 2)                                                             \
-                hipLaunchKernelGGL((gemv2_kernel<XT_INT4, W_, NCW_, false, RG>), dim3(ntiles), dim3(W_ * 64), 0, s, a); \
+                return launch_gemv2_int<XT_INT4, W_, NCW_, RG>(a, ntiles, s);                        \
             else                                                                                 \
                 return hipErrorInvalidValue;                                                     \
         } else {                                                                                 \
