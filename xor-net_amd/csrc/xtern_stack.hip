@@ -145,6 +145,8 @@ struct Shared {
     unsigned last;
 };
 
+static_assert(kStackRowGroupsMax * 64 >= 16 * 17, "a wave's reduction stage holds its activation slice");
+
 __device__ __forceinline__ unsigned* done_ctr(const StackArgs& a, int op) {
     return ctr_at(a.ctr, kCtrDone0 + op);
 }
@@ -340,6 +342,9 @@ __device__ void gemv_item(const StackArgs& a, Shared& sh, const OpRef& d, int op
 
     const int ntb = ONE ? 1 : (M + 15) >> 4;
     for (int tb = 0; tb < ntb; ++tb) {
+        // the previous block's sums are read (its reduction stage doubles as
+        // this block's activation slice)
+        if (tb > 0) __syncthreads();
         const int mt = ONE ? 1 : min(16, M - 16 * tb);  // tokens of this block
         float invr[4];
         unsigned w4[NCW];
@@ -382,13 +387,31 @@ __device__ void gemv_item(const StackArgs& a, Shared& sh, const OpRef& d, int op
             const int ldq = d.i(OPF(ldq));
             const __amdgpu_buffer_rsrc_t qr = rsrc(d.ptr<const int8_t>(OPF(q)), (unsigned)(M * ldq));
             const __amdgpu_buffer_rsrc_t ir = rsrc(d.ptr<const float>(OPF(inv)), (unsigned)(M * 4));
-            const int row = 16 * tb + min(j, mt - 1);
+            // Each load covers 4 token rows x 256 contiguous bytes of a
+            // chunk (a load spanning the 16 rows at the row stride kept the
+            // address path stalled on translation); chunk by chunk the rows go
+            // through this wave's part of the reduction stage (rows padded by
+            // one piece) and come back as the MFMA fragments of lane (g, j):
+            // row j, pieces 4 s + g.  A wave's LDS accesses complete in order.
 #pragma unroll
             for (int t = 0; t < NCW; ++t) {
                 const int c = min(wave + t * kSW, nch - 1);
 #pragma unroll
-                for (int s = 0; s < 4; ++s)
-                    aq[t][s] = ld_coh16(qr, (unsigned)((size_t)row * ldq + c * 256 + s * 64 + 16 * g));
+                for (int u = 0; u < 4; ++u) {  // (rows past the block: zeros, no memory read)
+                    const int r = 4 * u + (lane >> 4);
+                    aq[t][u] = ld_coh16(qr, r < mt ? (unsigned)((size_t)(16 * tb + r) * ldq + c * 256 + (lane & 15) * 16)
+                                                   : kOutOfRange);
+                }
+            }
+            v4i* slice = &sh.red[wave][0][0];  // 16 x 17 pieces of the wave's 8 x 64
+#pragma unroll
+            for (int t = 0; t < NCW; ++t) {
+#pragma unroll
+                for (int u = 0; u < 4; ++u) slice[(4 * u + (lane >> 4)) * 17 + (lane & 15)] = aq[t][u];
+                __asm__ volatile("" ::: "memory");
+#pragma unroll
+                for (int s = 0; s < 4; ++s) aq[t][s] = slice[j * 17 + 4 * s + g];
+                __asm__ volatile("" ::: "memory");
             }
 #pragma unroll
             for (int r = 0; r < 4; ++r)
@@ -430,7 +453,6 @@ __device__ void gemv_item(const StackArgs& a, Shared& sh, const OpRef& d, int op
                 }
             }
         }
-        if (tb > 0) __syncthreads();  // the previous block's sums are read
 #pragma unroll
         for (int r = 0; r < RG; ++r) sh.red[wave][r][lane] = acc[r];
         __syncthreads();
