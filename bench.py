@@ -318,12 +318,16 @@ def stack_c4(np, torch, xtern, rng, Ms=(1, 8, 32), layers=30):
     """the BitNet-2B decode-step linear stack, 30 layers
     x {q, k, v, o, gate, up, down}, f32 activations (q/k/v and gate/up share
     one quantised input, as fused_forward_qkv / _mlp).  Weights are distinct
-    device buffers (521 MB, > 2x the MALL).  Two ways, same weights:
-      per_call    one library call per op (120 calls), one HIP graph per stack;
-      persistent  the decode stack (xt_stack_*): every op in ONE launch, with
-                  the residual stream's dependency kept -- layer L's q/k/v and
-                  gate/up read layer L-1's down output, written in the same
-                  launch (ops listed down, q/k/v, o, gate/up per layer).
+    device buffers (521 MB, > 2x the MALL).  Three ways, same weights:
+      per_call       one library call per op (120 calls), one HIP graph per stack;
+      residual_only  the projection stack (xt_stack_*) as ONE launch with only
+                     the residual dependency: layer L's q/k/v and gate/up read
+                     layer L-1's down output; o and down read inputs that are
+                     ready before the launch;
+      chain          ONE launch of the strict chain q/k/v -> o -> gate/up ->
+                     down -> next layer, each op reading the previous op's
+                     raw output (no norm / attention / activation in between:
+                     the library runs none of those inside a launch).
     The persistent outputs are checked bit-exact against the per-call ones."""
     shapes = {"q": (2560, 2560), "k": (2560, 640), "v": (2560, 640), "o": (2560, 2560),
               "gate": (2560, 6912), "up": (2560, 6912), "down": (6912, 2560)}
@@ -349,50 +353,77 @@ def stack_c4(np, torch, xtern, rng, Ms=(1, 8, 32), layers=30):
         g = Graph(torch, stack, 1)
         us = g.time_ms(10) * 1e3
         del g
-        row = {"workload": "c4_bitnet2b_stack", "M": M, "layers": layers,
+        row = {"workload": "c4_bitnet2b_projection_stack", "M": M, "layers": layers,
                "us_per_stack": round(us, 1), "weight_GBs": round(wbytes / (us * 1e-6) / 1e9, 1),
                "hbm_frac": round(wbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                "TOPS": round(ops1 * M / (us * 1e-6) / 1e12, 2)}
 
-        # persistent: one launch, layer L reads layer L-1's down output
+        # persistent, two dependency shapes over the same weights:
+        #  residual_only  layer L's q/k/v and gate/up read layer L-1's down
+        #                 output (written in the launch); o and down read
+        #                 inputs ready before the launch, so o/down items can
+        #                 run ahead of their layer;
+        #  chain          the strict projection chain: q/k/v read the previous
+        #                 down, o reads q, gate/up read o, down reads up --
+        #                 every op waits for the one before it (the dependency
+        #                 shape of a decode step, without its elementwise work).
         xo = [torch.from_numpy(rng.standard_normal((M, 2560)).astype(np.float32)).cuda()
               for _ in range(layers)]
         xdl = [torch.from_numpy(rng.standard_normal((M, 6912)).astype(np.float32)).cuda()
                for _ in range(layers)]
         outs = [{n: torch.empty((M, N), dtype=f32, device="cuda") for n, (K, N) in shapes.items()}
                 for _ in range(layers)]
-        ops = []
-        prev_h, prev_dep = xa, None
-        for L in range(layers):
-            w, o = W[L], outs[L]
-            ops.append(([w["down"]], xdl[L], [o["down"]], None))
-            dn = len(ops) - 1
-            ops.append(([w["q"], w["k"], w["v"]], prev_h, [o["q"], o["k"], o["v"]], prev_dep))
-            ops.append(([w["o"]], xo[L], [o["o"]], None))
-            ops.append(([w["gate"], w["up"]], prev_h, [o["gate"], o["up"]], prev_dep))
-            prev_h, prev_dep = o["down"], dn
-        st = xtern.Stack(ops, M)
-        gs = Graph(torch, lambda _i: st.run(), 1)
-        us_p = gs.time_ms(10) * 1e3
-        if st.gave_up():
-            raise SystemExit("decode stack: a dependency wait gave up")
-        # bit-exact against one call per op
-        for ws_, x_, ys_, _d in ops:
-            ref = [torch.empty_like(y) for y in ys_]
-            if len(ws_) == 1:
-                xtern.linear_f32(ws_[0], x_, out=ref[0])
-            else:
-                xtern.linear_multi_f32(ws_, x_, outs=ref)
-            for a_, b_ in zip(ys_, ref):
-                if not torch.equal(a_, b_):
-                    raise SystemExit("decode stack output differs from the per-call output")
-        row.update({"us_per_stack_persistent": round(us_p, 1),
-                    "persistent_weight_GBs": round(wbytes / (us_p * 1e-6) / 1e9, 1),
-                    "persistent_hbm_frac": round(wbytes / (us_p * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
-                    "persistent_TOPS": round(ops1 * M / (us_p * 1e-6) / 1e12, 2),
-                    "persistent_checked": "bit-exact vs per-call outputs"})
+
+        def ops_residual_only():
+            ops = []
+            prev_h, prev_dep = xa, None
+            for L in range(layers):
+                w, o = W[L], outs[L]
+                ops.append(([w["down"]], xdl[L], [o["down"]], None))
+                dn = len(ops) - 1
+                ops.append(([w["q"], w["k"], w["v"]], prev_h, [o["q"], o["k"], o["v"]], prev_dep))
+                ops.append(([w["o"]], xo[L], [o["o"]], None))
+                ops.append(([w["gate"], w["up"]], prev_h, [o["gate"], o["up"]], prev_dep))
+                prev_h, prev_dep = o["down"], dn
+            return ops
+
+        def ops_chain():
+            ops = []
+            prev_h, prev_dep = xa, None
+            for L in range(layers):
+                w, o = W[L], outs[L]
+                ops.append(([w["q"], w["k"], w["v"]], prev_h, [o["q"], o["k"], o["v"]], prev_dep))
+                ops.append(([w["o"]], o["q"], [o["o"]], len(ops) - 1))
+                ops.append(([w["gate"], w["up"]], o["o"], [o["gate"], o["up"]], len(ops) - 1))
+                ops.append(([w["down"]], o["up"], [o["down"]], len(ops) - 1))
+                prev_h, prev_dep = o["down"], len(ops) - 1
+            return ops
+
+        for tag, ops in (("residual_only", ops_residual_only()), ("chain", ops_chain())):
+            st = xtern.Stack(ops, M)
+            gs = Graph(torch, lambda _i: st.run(), 1)
+            us_p = gs.time_ms(10) * 1e3
+            if st.gave_up():
+                raise SystemExit("decode stack: a dependency wait gave up")
+            # bit-exact against one call per op, in list order (a chained
+            # op's input is the launch's own output of the op before it)
+            for ws_, x_, ys_, _d in ops:
+                ref = [torch.empty_like(y) for y in ys_]
+                if len(ws_) == 1:
+                    xtern.linear_f32(ws_[0], x_, out=ref[0])
+                else:
+                    xtern.linear_multi_f32(ws_, x_, outs=ref)
+                for a_, b_ in zip(ys_, ref):
+                    if not torch.equal(a_, b_):
+                        raise SystemExit(f"stack ({tag}) output differs from the per-call output")
+            row.update({f"{tag}_us_per_stack": round(us_p, 1),
+                        f"{tag}_weight_GBs": round(wbytes / (us_p * 1e-6) / 1e9, 1),
+                        f"{tag}_hbm_frac": round(wbytes / (us_p * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                        f"{tag}_TOPS": round(ops1 * M / (us_p * 1e-6) / 1e12, 2)})
+            del gs, st
+        row["persistent_checked"] = "bit-exact vs per-call outputs (both dependency shapes)"
         res.append(row)
-        del gs, st, outs, xo, xdl
+        del outs, xo, xdl
         torch.cuda.empty_cache()
     del W
     torch.cuda.empty_cache()

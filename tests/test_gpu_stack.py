@@ -5,6 +5,8 @@ src/models/llama/mod.rs:420-470) with the real dependency of the residual
 stream: layer L's q/k/v and gate/up read layer L-1's down output, written
 inside the same launch.  Each op's expected output is the oracle's
 TernaryLinear::forward (layers.rs:262-313) of the oracle's own input chain."""
+import zlib
+
 import numpy as np
 import pytest
 import torch
@@ -126,7 +128,7 @@ CASES = [("bitnet_m1_down_first", BITNET, 2, 1, "down_first", xtern.XT_QUANT_AVX
 @pytest.mark.parametrize("name,shapes,layers,M,order,mode", CASES, ids=[c[0] for c in CASES])
 def test_stack_matches_oracle(name, shapes, layers, M, order, mode):
     log(f"stack {name}: layers={layers} M={M} order={order} mode={mode}")
-    rng = np.random.default_rng(hash(name) & 0xffff)
+    rng = np.random.default_rng(zlib.crc32(name.encode()) & 0xffff)
     ops, checks = build(rng, shapes, layers, M, order, sparse_down=(M == 3))
     exp = expected(checks, mode)
     st = xtern.Stack(ops, M, mode)

@@ -190,3 +190,27 @@ def test_tile_bytes():
     assert xtern.tile_bytes(xtern.XT_PACK5, 3200, 8640) == 540 * 10 * 1024
     assert xtern.tile_bytes(xtern.XT_XORSPARSE, 4096, 14336) == 896 * 16 * 1024
     assert xtern.tile_bytes(0, 0, 5) == 0
+
+
+def test_stack_create_rejects_null_weights_on_cpu():
+    """xt_stack_create validates every op before any device call: a NULL
+    weight handle (first or later projection) or output is an argument error,
+    not a crash."""
+    for bad in range(3):
+        arr = (xtern._StackOp * 1)()
+        arr[0].n = 2
+        arr[0].x = 0x1000
+        arr[0].dep = -1
+        arr[0].y[0] = 0x2000
+        arr[0].y[1] = 0x3000
+        if bad == 0:
+            arr[0].w[1] = 0x4000            # w[0] NULL
+        elif bad == 1:
+            arr[0].w[0] = 0x4000            # w[1] NULL
+        else:
+            arr[0].w[0] = arr[0].w[1] = 0x4000
+            arr[0].y[1] = None              # y[1] NULL
+        h = ctypes.c_void_p()
+        rc = xtern._lib.xt_stack_create(arr, 1, 1, 0, ctypes.byref(h))
+        assert rc == xtern.XT_ERR_INVALID
+        assert b"NULL weights or output" in xtern._lib.xt_last_error()

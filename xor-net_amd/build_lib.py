@@ -68,16 +68,34 @@ def build_diag(verbose=False):
 
 
 def build(verbose=False):
-    cmd = [hipcc()] + HIPCC_FLAGS + [os.path.join(CSRC, s) for s in SOURCES] + ["-o", OUT]
+    """One object per source, compiled in parallel, then one link."""
+    from concurrent.futures import ThreadPoolExecutor
+    objdir = os.path.join(HERE, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    flags = [f for f in HIPCC_FLAGS if f != "-shared"]
+
+    def compile_one(src):
+        obj = os.path.join(objdir, os.path.splitext(src)[0] + ".o")
+        cmd = [hipcc()] + flags + ["-c", os.path.join(CSRC, src), "-o", obj]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        return obj, subprocess.run(cmd, capture_output=True, text=True)
+
+    with ThreadPoolExecutor(max_workers=min(len(SOURCES), 6)) as ex:
+        results = list(ex.map(compile_one, SOURCES))
+    for obj, res in results:
+        if res.returncode != 0:
+            raise RuntimeError("hipcc failed:\n" + res.stderr)
+        errs = [l for l in res.stderr.splitlines()
+                if "packed-fp32-ops" not in l and "warning: unknown target feature" not in l]
+        if verbose and errs:
+            print("\n".join(errs))
+    cmd = [hipcc(), "--offload-arch=gfx950", "-shared", "-fPIC"] + [o for o, _ in results] + ["-o", OUT]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
-    errs = [l for l in res.stderr.splitlines()
-            if "packed-fp32-ops" not in l and "warning: unknown target feature" not in l]
     if res.returncode != 0:
-        raise RuntimeError("hipcc failed:\n" + res.stderr)
-    if verbose and errs:
-        print("\n".join(errs))
+        raise RuntimeError("hipcc (link) failed:\n" + res.stderr)
     return OUT
 
 

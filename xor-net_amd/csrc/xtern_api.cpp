@@ -359,13 +359,11 @@ constexpr int64_t kFusedRowReads = 1200 * 1024;
 
 int gemv_fused_quant(const xt_weights* const* ws, int n, const float* x, int64_t M,
                      float* const* ys, int mode, hipStream_t s) {
-    const bool disabled = getenv("XTERN_NO_FUSED_QUANT") != nullptr;
     const int fmt = ws[0]->fmt;
     if (fmt == XT_XORSPARSE_STREAM) return 1;  // (its kernel takes i8 rows)
     const int64_t K = ws[0]->K;
     const int nch = (int)ws[0]->nch;
-    static const bool staged = getenv("XTERN_GEMV_STAGED") != nullptr;
-    const bool direct = !xt::is_int_format(fmt) && !staged;
+    const bool direct = !xt::is_int_format(fmt);
     // staging-free GEMV: one row only (measured: K = 6912, 8.1 -> 6.6 us at
     // M = 1; already slower at M = 2 for N = 6912, where every workgroup
     // re-reads and re-quantises the rows)
@@ -374,7 +372,7 @@ int gemv_fused_quant(const xt_weights* const* ws, int n, const float* x, int64_t
     // few us against the ~50 us of a 128256-row head (measured: Int8 head
     // forward 158 us fused on the staged GEMV, 50 us product on this one)
     if (xt::is_int_format(fmt) && xt::gemv2_takes(fmt, nch)) return 1;
-    if (disabled || M > 16 || M * K > (direct ? xt::kGemv2FusedQuantMax : xt::kGemvFusedQuantMax) ||
+    if (M > 16 || M * K > (direct ? xt::kGemv2FusedQuantMax : xt::kGemvFusedQuantMax) ||
         (((uintptr_t)x) & 15) || (K & 3))
         return 1;
     int ng_total = 0;
@@ -387,7 +385,7 @@ int gemv_fused_quant(const xt_weights* const* ws, int n, const float* x, int64_t
     int waves = 16;
     if (xt::is_int_format(fmt)) {
         waves = xt::int_gemv_waves(fmt, (int)M, nch);
-    } else if (!staged && !(fmt == XT_PACK5 && nch > 16)) {
+    } else if (!(fmt == XT_PACK5 && nch > 16)) {
         // (Pack5 above 16 chunks always fuses: 8640 -> 3200, 200 workgroups,
         // 7.8 vs 8.7 us; at or below, as the other formats: 3200 -> 3200 4.7
         // vs 6.1, 3200 -> 8640 with 540 workgroups 8.9 vs 7.5)
@@ -931,6 +929,8 @@ int xt_stack_create(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_st
         if (!op.x) return fail(XT_ERR_INVALID, at + "x is NULL");
         if (op.dep < -1 || op.dep >= i)
             return fail(XT_ERR_INVALID, at + "dep must be -1 or an earlier op");
+        for (int p = 0; p < op.n; ++p)
+            if (!op.w[p] || !op.y[p]) return fail(XT_ERR_INVALID, at + "NULL weights or output");
         xt::StackOpDev& d = dops[(size_t)i];
         memset(&d, 0, sizeof d);
         // row groups per GEMV item (the M = 1 pipeline takes 8 for short K)
@@ -1033,8 +1033,6 @@ int xt_stack_create(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_st
     if (per_cu < 1) return fail(XT_ERR_UNSUPPORTED, "stack kernel does not fit a CU");
     // Every workgroup resident at once (see xtern_stack.hip): grid = occupancy.
     int grid = std::min(cus * per_cu, (int)items.size());
-    if (const char* b = getenv("XTERN_STACK_BLOCKS"))  // (tuning) fewer workgroups
-        if (atoi(b) > 0) grid = std::min(grid, atoi(b));
     // Deal the list out: each item, in list order, to the workgroup that is
     // predicted to finish its earlier items first (bytes as the cost).
     std::vector<std::vector<uint32_t>> per((size_t)grid);
@@ -1104,12 +1102,7 @@ int xt_stack_create(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_st
     st->args.mode = mode;
     st->args.slots = slots;
     // polls (about a microsecond each) before a dependency wait gives up
-    const char* sl = getenv("XTERN_STACK_SPIN_LIMIT");
-    st->args.spin_limit = sl ? atoi(sl) : (1 << 20);
-#ifdef XT_STACK_TRACE
-    if (getenv("XTERN_STACK_TRACE"))
-        XT_HIP(hipMalloc(reinterpret_cast<void**>(&st->args.trace), items.size() * 64));
-#endif
+    st->args.spin_limit = 1 << 20;
     st->blocks = grid;
     st->device = dev;
     st->dev_mem = mem;
@@ -1134,17 +1127,6 @@ int xt_stack_check(xt_stack* st, int* gave_up) {
     *gave_up = flag ? 1 : 0;
     return XT_OK;
 }
-
-#ifdef XT_STACK_TRACE
-// Tuning builds: copy the per-item stamps (8 per item) to the host.
-extern "C" int xt_stack_trace_copy(const xt_stack* st, uint64_t* out, int64_t n) {
-    if (!st->args.trace) return fail(XT_ERR_INVALID, "no trace buffer");
-    XT_HIP(hipDeviceSynchronize());
-    XT_HIP(hipMemcpy(out, st->args.trace, std::min<int64_t>(n, (int64_t)st->args.nitems * 8) * 8,
-                     hipMemcpyDeviceToHost));
-    return XT_OK;
-}
-#endif
 
 int xt_stack_destroy(xt_stack* st) {
     if (!st) return XT_OK;

@@ -6,9 +6,6 @@
 //   xtd_mfma_i8     back-to-back v_mfma_i32_32x32x32_i8 (or 16x16x64) on four
 //                   independent accumulators per wave, no memory traffic
 //   xtd_empty       an empty kernel of a given grid (launch floor)
-//   xtd_read_l2     every workgroup reads the same small buffer (L2-resident)
-//                   `iters` times, U 16-byte loads in flight per lane: the
-//                   per-CU load rate when every CU loads at once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -83,29 +80,6 @@ __global__ __launch_bounds__(256) void mfma_kernel(int iters, int seed, int* __r
 
 __global__ void empty_kernel() {}
 
-// Every workgroup reads the n16 16-byte pieces at p (the same ones), iters
-// times; lane loads pieces t, t + NT, ... U at a time.
-template <int U>
-__global__ __launch_bounds__(512) void read_l2_kernel(const v4i* __restrict__ p, int n16, int iters,
-                                                      unsigned* __restrict__ sink) {
-    const int nt = blockDim.x;
-    v4i acc = {0, 0, 0, 0};
-    for (int it = 0; it < iters; ++it) {
-        for (int i0 = threadIdx.x; i0 < n16; i0 += U * nt) {
-            v4i v[U];
-#pragma unroll
-            for (int u = 0; u < U; ++u) {
-                const int i = i0 + u * nt;
-                v[u] = p[i < n16 ? i : n16 - 1];
-            }
-#pragma unroll
-            for (int u = 0; u < U; ++u) acc ^= v[u];
-        }
-    }
-    const unsigned x = (unsigned)(acc[0] ^ acc[1] ^ acc[2] ^ acc[3]);
-    if (x == 0x9e3779b9u) sink[blockIdx.x] = x;
-}
-
 }  // namespace
 
 extern "C" {
@@ -127,19 +101,6 @@ int xtd_mfma_i8(int shape, int blocks, int iters, int* sink, void* stream) {
         hipLaunchKernelGGL(mfma_kernel<32>, dim3(blocks), dim3(256), 0, s, iters, 1, sink);
     else
         hipLaunchKernelGGL(mfma_kernel<16>, dim3(blocks), dim3(256), 0, s, iters, 1, sink);
-    return (int)hipGetLastError();
-}
-
-// Every one of `blocks` workgroups (`threads` each) reads the same `bytes`
-// at p `iters` times with U (4, 8 or 16) loads in flight per lane.
-int xtd_read_l2(const void* p, size_t bytes, int blocks, int threads, int iters, int u,
-                unsigned* sink, void* stream) {
-    hipStream_t s = static_cast<hipStream_t>(stream);
-    const v4i* q = static_cast<const v4i*>(p);
-    const int n16 = (int)(bytes / 16);
-    if (u == 4) hipLaunchKernelGGL(read_l2_kernel<4>, dim3(blocks), dim3(threads), 0, s, q, n16, iters, sink);
-    else if (u == 8) hipLaunchKernelGGL(read_l2_kernel<8>, dim3(blocks), dim3(threads), 0, s, q, n16, iters, sink);
-    else hipLaunchKernelGGL(read_l2_kernel<16>, dim3(blocks), dim3(threads), 0, s, q, n16, iters, sink);
     return (int)hipGetLastError();
 }
 

@@ -186,7 +186,6 @@ struct StackArgs {
     int nitems, nops, M, mode;
     int spin_limit;           // polls before a dependency wait gives up
     int slots;                // M = 1: chunk slots per wave the ops need
-    uint64_t* trace;          // tuning builds only (XT_STACK_TRACE): 8 stamps per item
 };
 int stack_threads();
 int stack_max_chunks();  // chunks of K an op may have (4 per wave)

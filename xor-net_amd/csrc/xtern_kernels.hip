@@ -1210,21 +1210,20 @@ static constexpr bool gemv2_am_fits() {
 }
 template <int FMT, int W, int NCW, int RG>
 static hipError_t launch_gemv2_am(const MMArgs& a, int ntiles, hipStream_t s) {
-    static const bool off = getenv("XTERN_GEMV_NO_AM") != nullptr;  // (measurement switch)
     const dim3 g(ntiles), b(W * 64);
     if constexpr (NCW >= 2) {
-        if (!off && a.M == 1) {
+        if (a.M == 1) {
             hipLaunchKernelGGL((gemv2_kernel<FMT, W, NCW, false, RG, 1>), g, b, 0, s, a);
             return hipGetLastError();
         }
         if constexpr (gemv2_am_fits<FMT, W, NCW, RG, 4>()) {
-            if (!off && a.M <= 4) {
+            if (a.M <= 4) {
                 hipLaunchKernelGGL((gemv2_kernel<FMT, W, NCW, false, RG, 4>), g, b, 0, s, a);
                 return hipGetLastError();
             }
         }
         if constexpr (gemv2_am_fits<FMT, W, NCW, RG, 8>()) {
-            if (!off && a.M <= 8) {
+            if (a.M <= 8) {
                 hipLaunchKernelGGL((gemv2_kernel<FMT, W, NCW, false, RG, 8>), g, b, 0, s, a);
                 return hipGetLastError();
             }
@@ -1234,7 +1233,7 @@ static hipError_t launch_gemv2_am(const MMArgs& a, int ntiles, hipStream_t s) {
     // staged chunk by chunk (measured: TA address stalls 68 % -> see the
     // profile of this kernel)
     if constexpr (FMT == XT_PACK4 && (size_t)W * (16 * 17 * 16 + RG * 1024) <= 150 * 1024) {
-        if (!off && a.M > 4 && a.M <= 16) {
+        if (a.M > 4 && a.M <= 16) {
             hipLaunchKernelGGL((gemv2_kernel<FMT, W, NCW, false, RG, 16>), g, b, 0, s, a);
             return hipGetLastError();
         }
@@ -1249,10 +1248,9 @@ static hipError_t launch_gemv2_am(const MMArgs& a, int ntiles, hipStream_t s) {
 // loads).
 template <int FMT, int W, int NCW, int RG>
 static hipError_t launch_gemv2_int(const MMArgs& a, int ntiles, hipStream_t s) {
-    static const bool off = getenv("XTERN_GEMV_NO_AM") != nullptr;  // (measurement switch)
     const dim3 g(ntiles), b(W * 64);
     if constexpr (FMT == XT_INT8 && (size_t)W * (16 * 17 * 16 + RG * 1024) <= 150 * 1024) {
-        if (!off && a.M > 4 && a.M <= 16) {
+        if (a.M > 4 && a.M <= 16) {
             hipLaunchKernelGGL((gemv2_kernel<FMT, W, NCW, false, RG, 16>), g, b, 0, s, a);
             return hipGetLastError();
         }
@@ -1321,8 +1319,6 @@ static hipError_t launch_gemv2(int fmt, const MMArgs& a, int ntiles, hipStream_t
 }
 
 static bool use_gemv2(int fmt, int nch) {
-    static const bool staged = getenv("XTERN_GEMV_STAGED") != nullptr;
-    if (staged) return false;
     if (fmt == XT_INT8 || fmt == XT_INT4) return nch <= 32;  // weight registers: 4 / 2 tiles a chunk
     return (fmt == XT_PACK4 || fmt == XT_PACK5 || fmt == XT_XORSPARSE) && nch <= 64;
 }
@@ -1739,25 +1735,6 @@ __host__ __device__ constexpr int g32s_xch_slot(int ncmax) { return ncmax >= 3 ?
 #endif
 constexpr int kG32sAhead = XT_G32S_AHEAD;
 
-// XT_G32S_TRACE (0 in the library): a tuning build records, per workgroup,
-// s_memrealtime (100 MHz) at entry (0), chunk 0 landed (1), MFMA loop done
-// (2), halves exchanged (3), outputs issued (4); loader wave 8 at all its
-// loads issued (5) and landed (6).  xt_debug_g32s_trace copies them out.
-#ifndef XT_G32S_TRACE
-#define XT_G32S_TRACE 0
-#endif
-#if XT_G32S_TRACE
-__device__ unsigned long long xt_g32s_trace[1024][8];
-#define XT_G32S_STAMP(k, who)                                                    \
-    do {                                                                         \
-        if ((who) && lin < 1024) xt_g32s_trace[lin][k] = wall_clock64();         \
-    } while (0)
-#else
-#define XT_G32S_STAMP(k, who) \
-    do {                      \
-    } while (0)
-#endif
-
 template <int NCMAX>
 __global__ __launch_bounds__(768) void gemm32s_kernel(const MMArgs a) {
     constexpr int CH = 256;
@@ -1775,7 +1752,6 @@ __global__ __launch_bounds__(768) void gemm32s_kernel(const MMArgs a) {
     asm volatile("" ::"s"(pb.np), "s"(pb.t0), "s"(pb.t1), "s"(pb.t2), "s"(pb.t3), "s"(gx), "s"(gy), "s"(gz));
     __builtin_amdgcn_sched_barrier(0);  // one round of argument loads
     const int lin = blockIdx.x + gx * (blockIdx.y + gy * blockIdx.z);
-    XT_G32S_STAMP(0, threadIdx.x == 0);
     const int t = xcd_remap(lin, gx * gy * gz);
     const int by = t % gy;
     const int bx = (t / gy) % gx;
@@ -1821,13 +1797,11 @@ __global__ __launch_bounds__(768) void gemm32s_kernel(const MMArgs a) {
                 __builtin_amdgcn_s_barrier();
             }
         }
-        XT_G32S_STAMP(5, threadIdx.x == 512);
 #pragma unroll
         for (int c = NCMAX - D + 1; c < NCMAX; ++c) {
             wait_vmcnt(2 * (NCMAX - 1 - c));
             __builtin_amdgcn_s_barrier();
         }
-        XT_G32S_STAMP(6, threadIdx.x == 512);
         __builtin_amdgcn_s_barrier();  // the MFMA waves' exchange
         __builtin_amdgcn_s_barrier();  // and output staging barriers
         return;
@@ -1880,7 +1854,6 @@ __global__ __launch_bounds__(768) void gemm32s_kernel(const MMArgs a) {
         for (int k = 0; k < 16; ++k) acc[s][k] = 0;
     v4i acur[4];
     __syncthreads();  // chunk 0 has landed
-    XT_G32S_STAMP(1, threadIdx.x == 0);
     read_a(0, acur);
 #pragma unroll
     for (int c = 0; c < NCMAX; ++c) {
@@ -1902,7 +1875,6 @@ __global__ __launch_bounds__(768) void gemm32s_kernel(const MMArgs a) {
     }
 #pragma unroll
     for (int k = 0; k < 16; ++k) acc[0][k] += acc[1][k] + acc[2][k] + acc[3][k];
-    XT_G32S_STAMP(2, threadIdx.x == 0);
 
     // Add the halves L through LDS, in slots 0-1 when every wave is past
     // their reads (their chunks completed before the last chunk's barrier),
@@ -1924,7 +1896,6 @@ __global__ __launch_bounds__(768) void gemm32s_kernel(const MMArgs a) {
         }
     }
     __syncthreads();
-    XT_G32S_STAMP(3, threadIdx.x == 0);
     // Code-domain sums of the 32 x 128 tile -> LDS (slot 1), then whole rows.
     int32_t* dtile = reinterpret_cast<int32_t*>(xch + 4096);  // [32][128], two slots on
 #pragma unroll
@@ -1968,7 +1939,6 @@ __global__ __launch_bounds__(768) void gemm32s_kernel(const MMArgs a) {
             }
         }
     }
-    XT_G32S_STAMP(4, threadIdx.x == 0);
 }
 
 int gemm32s_ncmax() { return 18; }
@@ -2254,30 +2224,6 @@ hipError_t launch_hf_tiles(int fmt, const uint8_t* stored, int64_t K, int64_t N,
 
 }  // namespace xt
 
-// XT_MID_STATS (0 in the library) makes the MLP middle kernel record, for
-// its first row, phase timestamps and piece counts into xt_mid_stats, read
-// with xt_debug_mid_stats(); for timing harnesses only.
-#ifndef XT_MID_STATS
-#define XT_MID_STATS 0
-#endif
-#if XT_MID_STATS
-__device__ unsigned long long xt_mid_stats[16];
-#define XT_STAMP(k)                                                             \
-    do {                                                                        \
-        if (blockIdx.x == 0 && threadIdx.x == 0) xt_mid_stats[k] = wall_clock64(); \
-    } while (0)
-#define XT_COUNT(k, v)                                                          \
-    do {                                                                        \
-        if (blockIdx.x == 0 && threadIdx.x == 0) xt_mid_stats[k] = (v);         \
-    } while (0)
-#else
-#define XT_STAMP(k) \
-    do {            \
-    } while (0)
-#define XT_COUNT(k, v) \
-    do {               \
-    } while (0)
-#endif
 
 namespace xt {
 
@@ -2607,7 +2553,6 @@ __device__ __forceinline__ float exact_seq_sum(int n, const float* lt, SeqSumLds
     const float excl_next = __uint_as_float(dpp32<0x130, 0xf>(__float_as_uint(excl)));  // wave_shl:1
     if (lane == 63) sl.wtot[w] = incl;
     __syncthreads();
-    XT_STAMP(3);
     float woff = 0.0f;
     for (int j = 0; j < w; ++j) woff = __fadd_rn(woff, sl.wtot[j]);
     const float woff_next = __fadd_rn(woff, sl.wtot[w]);
@@ -2652,7 +2597,6 @@ __device__ __forceinline__ float exact_seq_sum(int n, const float* lt, SeqSumLds
         sl.wcnt[w] = (int)cincl;
     }
     __syncthreads();
-    XT_STAMP(4);
     uint64_t gp = gincl - dsum;
     int rank = (int)(cincl - ends);
     int total_ends = 0;
@@ -2679,7 +2623,6 @@ __device__ __forceinline__ float exact_seq_sum(int n, const float* lt, SeqSumLds
         }
     }
     __syncthreads();
-    XT_STAMP(5);
 
     // 3. walk the pieces (wave 0).  Records are loaded 64 at a time, one per
     // lane, with everything that does not depend on the running sum: the
@@ -2689,9 +2632,6 @@ __device__ __forceinline__ float exact_seq_sum(int n, const float* lt, SeqSumLds
     // b = -126, so "sum in binade b and sum + P below 2^(b+1)" is
     // lo <= bits < hi - P).  The sequential part reads them with readlane.
     if (w == 0) {
-#if XT_MID_STATS
-        int n_fb = 0;
-#endif
         // (uniform values read from LDS are made scalar, so that the walk
         // runs on the scalar unit instead of under exec masks)
         total_ends = __builtin_amdgcn_readfirstlane(total_ends);
@@ -2733,9 +2673,6 @@ __device__ __forceinline__ float exact_seq_sum(int n, const float* lt, SeqSumLds
                     const bool inr = sbits >= klo && sbits < klim;
                     sbits = inr ? sbits + kp : sbits;
                     if (__builtin_expect(!inr, 0)) {
-#if XT_MID_STATS
-                        ++n_fb;
-#endif
                         sbits = __float_as_uint(seq_advance(__uint_as_float(sbits), lt,
                                                             lane_read(start, kk), lane_read(idx, kk)));
                     }
@@ -2745,12 +2682,7 @@ __device__ __forceinline__ float exact_seq_sum(int n, const float* lt, SeqSumLds
             s = __uint_as_float(sbits);
         }
         if (lane == 0) sl.res = s;
-#if XT_MID_STATS
-        XT_COUNT(8, total_ends);
-        XT_COUNT(9, n_fb);
-#endif
     }
-    XT_STAMP(6);
     __syncthreads();
     return sl.res;
 }
@@ -2769,7 +2701,6 @@ __global__ __launch_bounds__(kMidThreads) void mlp_mid_kernel(MidArgs a) {
     const int nmain = (n / 16) * 16;
     const float* gr = a.gate + (size_t)m * a.ldg;
     const float* ur = a.up + (size_t)m * a.ldg;
-    XT_STAMP(0);
     float v[CM], nwv[CM];
 #pragma unroll
     for (int c = 0; c < CM; ++c) {
@@ -2778,7 +2709,6 @@ __global__ __launch_bounds__(kMidThreads) void mlp_mid_kernel(MidArgs a) {
                                 : 0.0f;
         nwv[c] = (a.norm_w && c < C && i < n) ? a.norm_w[i] : 0.0f;  // fetched early
     }
-    XT_STAMP(1);
     if (a.norm_w) {
         float* lt = reinterpret_cast<float*>(lds);
         int* rec_idx = reinterpret_cast<int*>(lds + (size_t)C * kMidThreads * 4);
@@ -2801,7 +2731,6 @@ __global__ __launch_bounds__(kMidThreads) void mlp_mid_kernel(MidArgs a) {
         int flags = 0;
 #pragma unroll
         for (int j = 0; j < kMidWaves; ++j) flags |= sm_i[j];
-        XT_STAMP(2);
         float sum;
         if (flags & 1) sum = __builtin_nanf("");
         else if (flags & 2) sum = __builtin_inff();
@@ -2818,7 +2747,6 @@ __global__ __launch_bounds__(kMidThreads) void mlp_mid_kernel(MidArgs a) {
             if (c < C && i < n) v[c] = __fmul_rn(__fmul_rn(v[c], invr), nwv[c]);
         }
     }
-    XT_STAMP(11);
     if (a.out) {
         float* orow = a.out + (size_t)m * a.ldo;
 #pragma unroll
@@ -2859,7 +2787,6 @@ __global__ __launch_bounds__(kMidThreads) void mlp_mid_kernel(MidArgs a) {
     for (int i = n + tid; i < a.ldq; i += kMidThreads) qr[i] = 0;
     if (!a.rowsum) {  // the product decodes signed weights or sums the row itself
         if (tid == 0) a.inv[m] = invs;
-        XT_STAMP(7);
         return;
     }
     sum = wave_sum_int(sum);
@@ -2872,7 +2799,6 @@ __global__ __launch_bounds__(kMidThreads) void mlp_mid_kernel(MidArgs a) {
         a.inv[m] = invs;
         if (a.rowsum) a.rowsum[m] = tot;
     }
-    XT_STAMP(7);
 }
 
 int mid_max_cols() { return kMidCmax * kMidThreads; }
@@ -2913,20 +2839,4 @@ hipError_t launch_mlp_mid(const MidArgs& a0, int M, hipStream_t s) {
 
 }  // namespace xt
 
-#if XT_G32S_TRACE
-extern "C" int xt_debug_g32s_trace(unsigned long long* out) {
-    return hipMemcpyFromSymbol(out, HIP_SYMBOL(xt::xt_g32s_trace), sizeof(unsigned long long) * 1024 * 8) ==
-                   hipSuccess
-               ? 0
-               : -2;
-}
-#endif
 
-#if XT_MID_STATS
-extern "C" int xt_debug_mid_stats(unsigned long long* out) {
-    return hipMemcpyFromSymbol(out, HIP_SYMBOL(xt_mid_stats), sizeof(unsigned long long) * 16) ==
-                   hipSuccess
-               ? 0
-               : -2;
-}
-#endif

@@ -46,16 +46,6 @@
 #include "xtern_device.h"
 #include "xtern_internal.h"
 
-// XT_STACK_TRACE (0 in the library) compiles per-item timestamps for a
-// tuning build: thread 0 of the workgroup records s_memrealtime (100 MHz) at
-// the item's phase boundaries into StackArgs::trace[item * 8 + k].
-#ifndef XT_STACK_TRACE
-#define XT_STACK_TRACE 0
-#endif
-#ifndef XT_STACK_PIPE3
-#define XT_STACK_PIPE3 0
-#endif
-
 namespace xt {
 
 namespace {
@@ -69,18 +59,6 @@ static_assert(kDescWords <= 64 && sizeof(StackOpDev) % 4 == 0, "a descriptor is 
 // GEMV completions of every op, then the quantiser completions.
 __device__ __forceinline__ unsigned* ctr_at(unsigned* c, int slot) { return c + slot * 32; }
 constexpr int kCtrExit = 1, kCtrError = 2, kCtrDone0 = 4;
-
-__device__ __forceinline__ void stamp(const StackArgs& a, int pos, int k, unsigned tag) {
-#if XT_STACK_TRACE
-    if (a.trace && threadIdx.x == 0) {
-        uint64_t* t = a.trace + (size_t)pos * 8;
-        t[k] = __builtin_amdgcn_s_memrealtime();
-        if (k == 0) t[7] = tag;
-    }
-#else
-    (void)a, (void)pos, (void)k, (void)tag;
-#endif
-}
 
 // Buffer resources (uniform).  num_records bounds every access whose vector
 // offset (plus instruction offset) is past it: such a load returns zeros and
@@ -105,9 +83,6 @@ __device__ __forceinline__ v4i ld_w16(__amdgpu_buffer_rsrc_t r, unsigned voff, u
 __device__ __forceinline__ void st_buf(__amdgpu_buffer_rsrc_t r, unsigned off, unsigned v, bool coh) {
     if (coh) __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, kAuxCoh);
     else __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, 0);
-}
-__device__ __forceinline__ void st_coh(float* p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 __device__ __forceinline__ void st_coh(unsigned* p, unsigned v) {
     __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -325,7 +300,6 @@ __device__ void gemv_item(const StackArgs& a, Shared& sh, const OpRef& d, int op
             wv[t][r] = ld_w16(wr, voff, c < nch ? (unsigned)(((G0 + r) * nch + c) * 1024) : kOutOfRange);
     }
     __builtin_amdgcn_sched_barrier(0);
-    stamp(a, pos, 1, 0);
     const int o = (G0 + min(wave, RG - 1)) * 16 + j;
     const float wscale = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(
         rsrc(d.ptr<const float>(OPF(ws) + 8 * p), (unsigned)(N * 4)), (unsigned)min(o, N - 1) * 4u, 0, 0));
@@ -338,7 +312,6 @@ __device__ void gemv_item(const StackArgs& a, Shared& sh, const OpRef& d, int op
     } else {
         wave_wait(a, sh, a.nops + opi, (unsigned)M);
     }
-    stamp(a, pos, 2, 0);
 
     const int ntb = ONE ? 1 : (M + 15) >> 4;
     for (int tb = 0; tb < ntb; ++tb) {
@@ -360,7 +333,6 @@ __device__ void gemv_item(const StackArgs& a, Shared& sh, const OpRef& d, int op
             });
             if (lane == 0) sh.wmax[wave] = __int_as_float(wm);
             __syncthreads();
-            stamp(a, pos, 3, 0);
             float rmx = sh.wmax[0];
 #pragma unroll
             for (int w = 1; w < kSW; ++w) rmx = fmaxf(rmx, sh.wmax[w]);
@@ -456,7 +428,6 @@ __device__ void gemv_item(const StackArgs& a, Shared& sh, const OpRef& d, int op
 #pragma unroll
         for (int r = 0; r < RG; ++r) sh.red[wave][r][lane] = acc[r];
         __syncthreads();
-        stamp(a, pos, 4, 0);
         if (wave < RG && G0 + wave < NG && o < N) {
             v4i sum = sh.red[0][wave][lane];
 #pragma unroll
@@ -472,7 +443,6 @@ __device__ void gemv_item(const StackArgs& a, Shared& sh, const OpRef& d, int op
             }
         }
     }
-    stamp(a, pos, 5, 0);
     if (pub) {  // another op reads these outputs inside the launch
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
@@ -481,358 +451,8 @@ __device__ void gemv_item(const StackArgs& a, Shared& sh, const OpRef& d, int op
     } else {
         __syncthreads();  // the reduction stage is read before the next item writes it
     }
-    stamp(a, pos, 6, 0);
 }
 
-// XT_STACK_PIPE3 (0 in the library): the three-deep M = 1 pipeline below.
-// Off: its first GPU runs faulted (a descriptor read the compiler sank into
-// a 16-lane branch; fixed since, in load_op and at the output pointer, but
-// not yet run again).  The two-deep pipeline after #else is the one built.
-#if XT_STACK_PIPE3
-// ---------------------------------------------------------------------------
-// M = 1: software-pipelined items over rows quantised once per op.
-//
-// The op's quantiser item writes its input row as i8 plus the sum of each
-// 256-column chunk.  A GEMV item covers rg row groups (8, 4 or 2, so that no
-// wave holds more than NS weight tiles): wave w multiplies row group w % rg
-// and the chunks c with c % (8 / rg) == w / rg, so every wave holds one
-// accumulator and all waves carry the same load.  Weights enter the MFMA as
-// codes (w + 1) and each wave subtracts the chunk sums of the chunks it
-// multiplied: the decode is 3 shifts and 4 ANDs per 16 weights.  The i8 row
-// goes through LDS (double-buffered by item parity); the A fragment of a
-// k-step is one ds_read_b128 that the 16 token lanes share.
-//
-// Three items are in flight per workgroup.  Step s issues, in this order:
-// item s + 1's row (when its quantiser is known to be done), item s + 2's
-// quantiser count (when not yet known) and item s + 2's weight tiles and
-// w_scale; then it computes item s.  Vector memory operations complete in
-// issue order, so waiting for item s's row (issued at step s - 1) also
-// covers its weights (step s - 2) and leaves items s + 1 and s + 2 in flight
-// while s computes.  Every step issues the same number of loads (the ones it
-// does not need at an out-of-range offset: zeros, no memory access), so the
-// compiler's wait counts stay exact.  A row not known ready a step ahead is
-// loaded late (after a wait that drains the loads in flight): rare, since an
-// op's quantiser item is listed long before its GEMV items.
-//
-// Completion counts are bumped per wave (eight per item): a wave's output
-// stores of item s have completed once item s + 2's row loads (issued after
-// them) have returned, so the wave bumps then, without a barrier and without
-// waiting for the weights in flight.  Before any wait of its own a wave
-// drains and bumps whatever it still holds, so no workgroup waits for a
-// completion it is itself holding back.
-// ---------------------------------------------------------------------------
-template <int NS>
-struct OneBuf {
-    v4i w[NS];     // weight tiles of this wave's chunk slots
-    v4i q;         // 16 bytes of the i8 input row (thread t: bytes 16 t ..)
-    v4i cs;        // threads 0..7: chunk sums 4 t .. 4 t + 3
-    float inv;     // the row's inverse scale
-    float wsc;     // w_scale of this lane's output row
-    unsigned cnt;  // the op's quantiser count (when asked; else zero)
-};
-
-struct OneGeo {
-    int opi, p, G0, N, NG, nch, rg, pub;
-    int quant;  // a quantiser item (runs in the compute stage; its loads are empty)
-    int row;    // needs the op's quantised row (a GEMV item)
-    int rdy;    // the row was known ready when the item was looked up
-    int qiss;   // the row's loads have been issued (or none are needed)
-    // resources as base + size (built where used: resources kept in the
-    // struct would be copied through scratch memory)
-    const void* wp;
-    const void* qp;
-    const void* cp;
-    const void* ip;
-    const void* sp;
-    unsigned wn, qn, cn, in_, sn;
-    __device__ __forceinline__ __amdgpu_buffer_rsrc_t wr() const { return rsrc(wp, wn); }
-    __device__ __forceinline__ __amdgpu_buffer_rsrc_t qr() const { return rsrc(qp, qn); }
-    __device__ __forceinline__ __amdgpu_buffer_rsrc_t cr() const { return rsrc(cp, cn); }
-    __device__ __forceinline__ __amdgpu_buffer_rsrc_t ir() const { return rsrc(ip, in_); }
-    __device__ __forceinline__ __amdgpu_buffer_rsrc_t sr() const { return rsrc(sp, sn); }
-};
-
-// k >= n gives an empty item (no chunks, empty resources).
-__device__ __forceinline__ OneGeo one_geo(const Shared& sh, int k, int n, int nops) {
-    OneGeo g;
-    g.opi = g.p = g.G0 = 0;
-    g.N = g.NG = 1;
-    g.nch = 0;
-    g.rg = 8;
-    g.pub = 0;
-    g.quant = 0;
-    g.row = 0;
-    g.rdy = 1;
-    g.qiss = 1;
-    g.wp = g.qp = g.cp = g.ip = g.sp = nullptr;
-    g.wn = g.qn = g.cn = g.in_ = g.sn = 0u;
-    if (k >= n) return g;
-    const unsigned it = __builtin_amdgcn_readfirstlane(sh.items[k]);
-    g.opi = (int)(it >> 20);
-    const OpRef d = load_op(sh, g.opi);
-    const int blk = (int)(it & 0xfffff) - d.i(OPF(nq));
-    if (blk < 0) {  // quantiser item
-        g.quant = 1;
-        return g;
-    }
-    const int np = d.i(OPF(nproj));
-    const int ge0 = d.i(OPF(gend)), ge1 = d.i(OPF(gend) + 4), ge2 = d.i(OPF(gend) + 8);
-    g.p = (np > 1 && blk >= ge0) + (np > 2 && blk >= ge1) + (np > 3 && blk >= ge2);
-    const int b0 = g.p == 0 ? 0 : d.i(OPF(gend) + 4 * (g.p - 1));
-    g.rg = d.i(OPF(rg));
-    g.G0 = (blk - b0) * g.rg;
-    g.N = d.i(OPF(N) + 4 * g.p);
-    g.NG = (g.N + 15) >> 4;
-    g.nch = d.i(OPF(nch));
-    g.pub = d.i(OPF(pub));
-    g.row = 1;
-    g.rdy = known(sh, nops + g.opi);
-    g.qiss = 0;
-    g.wp = d.ptr<const uint8_t>(OPF(tiles) + 8 * g.p);
-    g.wn = (unsigned)(g.NG * g.nch * 1024);
-    g.qp = d.ptr<const int8_t>(OPF(q));
-    g.qn = (unsigned)d.i(OPF(ldq));
-    g.cp = d.ptr<const int32_t>(OPF(csum));
-    g.cn = 128u;
-    g.ip = d.ptr<const float>(OPF(inv));
-    g.in_ = 4u;
-    g.sp = d.ptr<const float>(OPF(ws) + 8 * g.p);
-    g.sn = (unsigned)(g.N * 4);
-    return g;
-}
-
-// chunk of slot i for this wave, or -1
-__device__ __forceinline__ int one_chunk(const OneGeo& g, int wave, int i) {
-    const int per = kSW / g.rg;  // waves per row group: 1, 2 or 4
-    const int c = (wave / g.rg) + per * i;
-    return c < g.nch ? c : -1;
-}
-
-// The item's weight tiles and this lane's w_scale.
-template <int NS>
-__device__ __forceinline__ void one_issue_w(const OneGeo& g, OneBuf<NS>& B) {
-    const int wave = wave_id();
-    const unsigned voff = (unsigned)(threadIdx.x & 63) * 16u;
-    const int r = wave % g.rg;
-#pragma unroll
-    for (int i = 0; i < NS; ++i) {
-        const int c = one_chunk(g, wave, i);
-        B.w[i] = ld_w16(g.wr(), voff, c >= 0 ? (unsigned)(((g.G0 + r) * g.nch + c) * 1024) : kOutOfRange);
-    }
-    const int o = (g.G0 + r) * 16 + (int)(threadIdx.x & 15);
-    B.wsc = __int_as_float(
-        __builtin_amdgcn_raw_buffer_load_b32(g.sr(), (unsigned)min(o, g.N - 1) * 4u, 0u, 0));
-}
-// The i8 row, chunk sums and scale (device scope: written in this launch);
-// out of range (zeros) when `now` is false.
-template <int NS>
-__device__ __forceinline__ void one_issue_q(const OneGeo& g, OneBuf<NS>& B, bool now) {
-    const unsigned t = threadIdx.x;
-    // (uniform by construction; said explicitly, or a value merged from the
-    // wait paths turns these loads into loops over lanes)
-    const unsigned so = __builtin_amdgcn_readfirstlane(now ? 0u : kOutOfRange);
-    B.q = ld_coh16(rsrc(sgpr_ptr(g.qp), __builtin_amdgcn_readfirstlane(g.qn)), t * 16u, so);
-    B.cs = ld_coh16(rsrc(sgpr_ptr(g.cp), __builtin_amdgcn_readfirstlane(g.cn)), (t & 7u) * 16u, so);
-    B.inv = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(
-        rsrc(sgpr_ptr(g.ip), __builtin_amdgcn_readfirstlane(g.in_)), so, 0, kAuxCoh));
-}
-// The op's quantiser count, when the row is not known ready (every lane
-// reads the same word).
-template <int NS>
-__device__ __forceinline__ void one_issue_cnt(const StackArgs& a, const OneGeo& g, OneBuf<NS>& B) {
-    const __amdgpu_buffer_rsrc_t cr = rsrc(a.ctr, (unsigned)((kCtrDone0 + 2 * a.nops) * 128));
-    const unsigned off = (unsigned)((kCtrDone0 + a.nops + g.opi) * 128);
-    B.cnt = __builtin_amdgcn_raw_buffer_load_b32(cr, (g.row && !g.rdy) ? off : kOutOfRange, 0, kAuxCoh);
-}
-
-// Waits (compiler-inserted) until the loads that wrote `v` have returned.
-__device__ __forceinline__ void await_loaded(const v4i& v) { asm volatile("" ::"v"(v) : "memory"); }
-
-// This wave's completion bump for op `p` (none when p < 0); its stores for
-// the item have completed.
-__device__ __forceinline__ void one_bump(const StackArgs& a, int p) {
-    if (p >= 0 && (threadIdx.x & 63) == 0)
-        __hip_atomic_fetch_add(done_ctr(a, p), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void one_mark_known(Shared& sh, int slot) {
-    if ((threadIdx.x & 63) == 0) atomicOr(&sh.known[slot >> 5], 1u << (slot & 31));
-}
-
-template <int NS>
-__device__ __forceinline__ void one_compute(const StackArgs& a, Shared& sh, const OneGeo& g,
-                                            const OneBuf<NS>& B, const unsigned* qb, const unsigned* cb,
-                                            int pos) {
-    const int lane = threadIdx.x & 63, wave = wave_id();
-    const int gq = lane >> 4, j = lane & 15;
-    __syncthreads();  // the row is in LDS
-    stamp(a, pos, 3, 0);
-    v4i acc = v4i{0, 0, 0, 0};
-    int xsum = 0;
-#pragma unroll
-    for (int i = 0; i < NS; ++i) {
-        const int c = one_chunk(g, wave, i);
-        if (c >= 0) {  // (uniform)
-            xsum += (int)cb[c];
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const v4i av = *reinterpret_cast<const v4i*>(qb + (c * 256 + s * 64 + gq * 16) / 4);
-                acc = mfma(av, decode4(B.w[i][s]), acc);
-            }
-        }
-    }
-    acc[0] -= xsum;  // codes are w + 1 (token 0: element 0 of the lanes with gq == 0)
-    const int per = kSW / g.rg;  // waves per row group: partial sums through LDS
-    int* red = reinterpret_cast<int*>(&sh.red[0][0][0]);
-    if (per > 1) {
-        if (gq == 0) red[wave * 16 + j] = acc[0];
-        __syncthreads();  // (the next write is after the next item's first barrier)
-    }
-    stamp(a, pos, 4, 0);
-    const int r = wave % g.rg;
-    const int o = (g.G0 + r) * 16 + j;
-    // (read here, with every lane active: see load_op)
-    float* const yp = load_op(sh, g.opi).ptr<float>(OPF(y) + 8 * g.p);
-    if (wave < g.rg && gq == 0 && g.G0 + r < g.NG && o < g.N) {
-        int sum = acc[0];
-        if (per > 1) {
-            sum = 0;
-            for (int t = 0; t < per; ++t) sum += red[(wave + t * g.rg) * 16 + j];
-        }
-        // layers.rs:294 -- (dot as f32 * inv_scale) * w_scale; device-scope
-        // stores only where another op of the launch reads the output
-        const float v = __fmul_rn(__fmul_rn((float)sum, B.inv), B.wsc);
-        const __amdgpu_buffer_rsrc_t yr = rsrc(yp, (unsigned)(g.N * 4));
-        st_buf(yr, (unsigned)o * 4u, __float_as_uint(v), g.pub != 0);
-    }
-    stamp(a, pos, 5, 0);
-}
-
-// Step s: X holds item s, Y item s + 1, Z receives item s + 2.  p1 / p2:
-// the ops whose completions this wave still holds for items s - 1 / s - 2.
-template <int NS>
-__device__ __forceinline__ void one_step(const StackArgs& a, Shared& sh, int s, int n, int i0,
-                                         OneGeo& gX, OneBuf<NS>& X, OneGeo& gY, OneBuf<NS>& Y,
-                                         OneGeo& gZ, OneBuf<NS>& Z, int& p1, int& p2) {
-    const int pos = i0 + s;
-    stamp(a, pos, 0, blockIdx.x | ((unsigned)gX.opi << 16));
-    // item s's row loads (step s - 1) have returned, and with them item
-    // s - 2's output stores, issued before them
-    await_loaded(X.q);
-    one_bump(a, p2);
-    p2 = p1;
-    p1 = -1;
-    unsigned* qb = sh.qrow[s & 1];
-    unsigned* cb = sh.csum[s & 1];
-    if (!gX.qiss) {  // (uniform per wave) the row was not known ready a step ahead
-        __builtin_amdgcn_s_waitcnt(0);
-        one_bump(a, p2);
-        p2 = -1;
-        if (!gX.rdy && __builtin_amdgcn_readfirstlane(X.cnt) >= 1u) one_mark_known(sh, a.nops + gX.opi);
-        else wave_wait(a, sh, a.nops + gX.opi, 1u);
-        OneBuf<NS> L;
-        one_issue_q<NS>(gX, L, true);
-        *reinterpret_cast<v4i*>(qb + threadIdx.x * 4) = L.q;
-        if (threadIdx.x < 8) *reinterpret_cast<v4i*>(cb + threadIdx.x * 4) = L.cs;
-        // (waited for here: a value still in flight at the join would make
-        // the normal path wait for the loads issued after it)
-        X.inv = L.inv;
-        asm volatile("" ::"v"(X.inv) : "memory");
-    } else if (gX.row) {
-        *reinterpret_cast<v4i*>(qb + threadIdx.x * 4) = X.q;
-        if (threadIdx.x < 8) *reinterpret_cast<v4i*>(cb + threadIdx.x * 4) = X.cs;
-    }
-    stamp(a, pos, 1, 0);
-    // issue: item s + 1's row, item s + 2's count and weights
-    bool yok = gY.qiss || gY.rdy;
-    if (!yok && __builtin_amdgcn_readfirstlane(Y.cnt) >= 1u) {
-        yok = true;
-        one_mark_known(sh, a.nops + gY.opi);
-    }
-    gZ = one_geo(sh, s + 2, n, a.nops);
-    __builtin_amdgcn_sched_barrier(0);  // (issue order: row, count, weights)
-    one_issue_q<NS>(gY, Y, gY.row && yok);
-    gY.qiss = yok;
-    __builtin_amdgcn_sched_barrier(0);
-    one_issue_cnt<NS>(a, gZ, Z);
-    __builtin_amdgcn_sched_barrier(0);
-    one_issue_w<NS>(gZ, Z);
-    __builtin_amdgcn_sched_barrier(0);
-    stamp(a, pos, 2, 0);
-    if (gX.quant) {  // (uniform) drain first: the quantiser may wait
-        __builtin_amdgcn_s_waitcnt(0);
-        one_bump(a, p2);
-        p2 = -1;
-        quant_item(a, sh, load_op(sh, gX.opi), gX.opi, 0, (unsigned)kSW);
-    } else if (gX.row) {  // (an empty item past the end computes nothing)
-        one_compute<NS>(a, sh, gX, X, qb, cb, pos);
-        if (gX.pub) p1 = gX.opi;
-    }
-    // the stores above stay ahead of the next step's loads
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_sched_barrier(0);
-    stamp(a, pos, 6, 0);
-}
-
-template <int NS>
-__global__ __launch_bounds__(kSNT, 2) void stack_one_kernel(const StackArgs a) {
-    __shared__ Shared sh;
-    const int i0 = a.sched_off[blockIdx.x], n = a.sched_off[blockIdx.x + 1] - i0;
-    for (int i = threadIdx.x; i < n; i += kSNT) sh.items[i] = a.sched[i0 + i];
-    for (int i = threadIdx.x; i < a.nops * kDescWords; i += kSNT)
-        sh.desc[i] = reinterpret_cast<const unsigned*>(a.ops)[i];
-    for (int i = threadIdx.x; i < kKnownWords; i += kSNT) sh.known[i] = 0u;
-    __syncthreads();
-    OneBuf<NS> A, B, C;
-    OneGeo ga, gb, gc;
-    // The loads of steps -2 and -1, in a step's order (so the wait counts
-    // of the first step match the loop's): an empty row, item 0's count and
-    // weights; item 0's row empty too (it takes the late path), item 1's
-    // count and weights.
-    gc = one_geo(sh, n, n, a.nops);
-    ga = one_geo(sh, 0, n, a.nops);
-    gb = one_geo(sh, 1, n, a.nops);
-    one_issue_q<NS>(gc, C, false);
-    __builtin_amdgcn_sched_barrier(0);
-    one_issue_cnt<NS>(a, ga, A);
-    __builtin_amdgcn_sched_barrier(0);
-    one_issue_w<NS>(ga, A);
-    __builtin_amdgcn_sched_barrier(0);
-    one_issue_q<NS>(ga, A, false);
-    __builtin_amdgcn_sched_barrier(0);
-    one_issue_cnt<NS>(a, gb, B);
-    __builtin_amdgcn_sched_barrier(0);
-    one_issue_w<NS>(gb, B);
-    __builtin_amdgcn_sched_barrier(0);
-    int p1 = -1, p2 = -1;
-    // whole trips only (steps past the end run empty items): an exit in the
-    // middle of a trip would join the loop's back edge, and the compiler's
-    // wait counts would then allow for a path that never runs
-    for (int s = 0; s < n; s += 3) {
-        one_step<NS>(a, sh, s, n, i0, ga, A, gb, B, gc, C, p1, p2);
-        one_step<NS>(a, sh, s + 1, n, i0, gb, B, gc, C, ga, A, p1, p2);
-        one_step<NS>(a, sh, s + 2, n, i0, gc, C, ga, A, gb, B, p1, p2);
-    }
-    __builtin_amdgcn_s_waitcnt(0);
-    one_bump(a, p1);
-    one_bump(a, p2);
-    __builtin_amdgcn_s_waitcnt(0);  // every wave's bumps are performed before the exit count
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const unsigned old = __hip_atomic_fetch_add(ctr_at(a.ctr, kCtrExit), 1u, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT);
-        sh.last = old == gridDim.x - 1;
-    }
-    __syncthreads();
-    if (sh.last) {
-        for (int i = threadIdx.x; i < a.nops; i += kSNT) {
-            st_coh(done_ctr(a, i), 0u);
-            st_coh(qdone_ctr(a, i), 0u);
-        }
-        if (threadIdx.x == 0) st_coh(ctr_at(a.ctr, kCtrExit), 0u);
-    }
-}
-
-#else  // XT_STACK_PIPE3
 // ---------------------------------------------------------------------------
 // M = 1: software-pipelined items over rows quantised once per op.
 //
@@ -970,7 +590,6 @@ __device__ __forceinline__ void one_issue_q(const OneGeo& g, OneBuf<NS>& B, bool
 template <int NS>
 __device__ __forceinline__ void one_pre(const StackArgs& a, Shared& sh, const OneGeo& g, OneBuf<NS>& B,
                                         int pos) {
-    stamp(a, pos, 1, 0);
     const bool now = g.dep_ready != 0;  // (quantiser and empty items: ready)
     if (!now) wave_wait(a, sh, a.nops + g.opi, 1u);
     OneBuf<NS> L;
@@ -989,7 +608,6 @@ __device__ __forceinline__ void one_compute(const StackArgs& a, Shared& sh, cons
     }
     const int lane = threadIdx.x & 63, wave = wave_id();
     const int gq = lane >> 4, j = lane & 15;
-    stamp(a, pos, 2, 0);
     unsigned* qb = sh.qrow[parity];
     *reinterpret_cast<v4i*>(qb + threadIdx.x * 4) = B.q;
     if (threadIdx.x < 8) *reinterpret_cast<v4i*>(sh.csum[parity] + threadIdx.x * 4) = B.cs;
@@ -998,7 +616,6 @@ __device__ __forceinline__ void one_compute(const StackArgs& a, Shared& sh, cons
     // (read here, with every lane active: see load_op)
     float* const yp = load_op(sh, g.opi).ptr<float>(OPF(y) + 8 * g.p);
     __syncthreads();
-    stamp(a, pos, 3, 0);
     v4i acc = v4i{0, 0, 0, 0};
     int xsum = 0;
 #pragma unroll
@@ -1019,7 +636,6 @@ __device__ __forceinline__ void one_compute(const StackArgs& a, Shared& sh, cons
         sh.red[wave][0][lane] = acc;
         __syncthreads();
     }
-    stamp(a, pos, 4, 0);
     if (wave < g.rg && gq == 0 && g.G0 + r < g.NG && o < g.N) {
         const int sum = split ? sh.red[wave][0][lane][0] + sh.red[wave + 4][0][lane][0] : acc[0];
         // layers.rs:294 -- (dot as f32 * inv_scale) * w_scale; device-scope
@@ -1028,7 +644,6 @@ __device__ __forceinline__ void one_compute(const StackArgs& a, Shared& sh, cons
         const __amdgpu_buffer_rsrc_t yr = rsrc(yp, (unsigned)(g.N * 4));
         st_buf(yr, (unsigned)o * 4u, __float_as_uint(v), g.pub != 0);
     }
-    stamp(a, pos, 5, 0);
     if (g.pub) {  // another op reads these outputs inside the launch
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
@@ -1037,7 +652,6 @@ __device__ __forceinline__ void one_compute(const StackArgs& a, Shared& sh, cons
     } else if (split) {
         __syncthreads();  // the reduction stage is read before the next item writes it
     }
-    stamp(a, pos, 6, 0);
 }
 
 // (A quantiser item -- one per op, listed early -- runs in its compute slot.)
@@ -1060,14 +674,12 @@ __global__ __launch_bounds__(kSNT, 2) void stack_one_kernel(const StackArgs a) {
     // two items per trip: A holds item k, B item k + 1 (the next item's loads
     // are issued on every trip, empty past the end)
     for (int k = 0; k < m; k += 2) {
-        stamp(a, i0 + item(k), 0, blockIdx.x | ((unsigned)ga.opi << 16));
         one_pre<NS>(a, sh, ga, A, i0 + item(k));
         gb = one_geo(sh, item(k + 1), n, a.nops);
         one_issue_q<NS>(gb, B, gb.dep_ready != 0);
         one_issue_w<NS>(sh, gb, B);
         one_compute<NS>(a, sh, ga, A, 0, i0 + item(k));
         if (k + 1 >= m) break;
-        stamp(a, i0 + item(k + 1), 0, blockIdx.x | ((unsigned)gb.opi << 16));
         one_pre<NS>(a, sh, gb, B, i0 + item(k + 1));
         ga = one_geo(sh, item(k + 2), n, a.nops);
         one_issue_q<NS>(ga, A, ga.dep_ready != 0);
@@ -1090,7 +702,6 @@ __global__ __launch_bounds__(kSNT, 2) void stack_one_kernel(const StackArgs a) {
     }
 }
 
-#endif  // XT_STACK_PIPE3
 
 // ONE: the M = 1 launch (every GEMV item quantises its row).  WPE: waves per
 // SIMD the register budget allows (4: two workgroups per CU).
@@ -1107,7 +718,6 @@ __global__ __launch_bounds__(kSNT, WPE) void stack_kernel(const StackArgs a) {
     for (int k = 0; k < n; ++k) {
         const unsigned it = __builtin_amdgcn_readfirstlane(sh.items[k]);
         const int opi = (int)(it >> 20), local = (int)(it & 0xfffff);
-        stamp(a, i0 + k, 0, blockIdx.x | ((unsigned)opi << 16));
         const OpRef op = load_op(sh, opi);
         const int nq = op.i(OPF(nq));
         if (!ONE && local < nq) {
@@ -1147,19 +757,6 @@ int stack_gemv_rg(int nch) { return (nch + kSW - 1) / kSW <= 2 ? 8 : 4; }
 // M = 1 launches take the pipelined kernel whose chunk slots per wave (NS)
 // cover every op of the stack; M > 1 the general one (which reads rows its
 // quantiser items wrote: the host lists those items for every op).
-#if XT_STACK_PIPE3
-static const void* stack_fn(int M, int ns) {
-    if (M != 1) return reinterpret_cast<const void*>(stack_kernel<false, 2>);
-    if (ns <= 8) return reinterpret_cast<const void*>(stack_one_kernel<8>);
-    return reinterpret_cast<const void*>(stack_one_kernel<10>);
-}
-// Row groups per M = 1 item: as many as keep a wave at 10 weight tiles or
-// fewer (three items' tiles live in registers).
-int stack_one_slots(int nch, int* rg) {
-    *rg = nch <= 10 ? 8 : nch <= 20 ? 4 : 2;
-    return (nch * *rg + kSW - 1) / kSW;
-}
-#else
 static const void* stack_fn(int M, int ns) {
     if (M != 1) return reinterpret_cast<const void*>(stack_kernel<false, 2>);
     if (ns <= 8) return reinterpret_cast<const void*>(stack_one_kernel<8>);
@@ -1171,7 +768,6 @@ int stack_one_slots(int nch, int* rg) {
     *rg = nch <= 16 ? 8 : 4;
     return *rg == 8 ? nch : (nch + 1) / 2;
 }
-#endif
 bool stack_pipelined(int M) { return M == 1; }
 
 hipError_t launch_stack(const StackArgs& a, int blocks, hipStream_t s) {
