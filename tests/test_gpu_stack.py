@@ -40,21 +40,22 @@ def pack4(t):
 
 
 class Mat:
-    def __init__(self, rng, K, N, sparse=False):
+    def __init__(self, rng, K, N, sparse=False, pack5=False, ws_scale=1.0):
         p0 = rng.uniform(0.3, 0.7)
         u = rng.random((N, K))
         t = np.where(u < p0, 0, np.where(rng.random((N, K)) < 0.5, -1, 1)).astype(np.int8)
         self.K, self.N, self.t = K, N, t
-        self.wb = pack4(t)
-        self.ws = rng.uniform(0.02, 0.1, N).astype(np.float32)
+        self.fmt = 1 if pack5 else 0
+        self.wb = np.concatenate([xtern.pack_ternary5(r) for r in t]) if pack5 else pack4(t)
+        self.ws = (rng.uniform(0.02, 0.1, N) * ws_scale).astype(np.float32)
         if sparse:
             blob = np.frombuffer(xtern.encode_sparse_tensor(t, K, N)[0], np.uint8)
             self.w = xtern.DeviceWeights(xtern.XT_XORSPARSE, K, N, blob, self.ws)
         else:
-            self.w = xtern.DeviceWeights(xtern.XT_PACK4, K, N, self.wb, self.ws)
+            self.w = xtern.DeviceWeights(xtern.XT_PACK5 if pack5 else xtern.XT_PACK4, K, N, self.wb, self.ws)
 
     def ref(self, x, mode):
-        return oracle.linear_forward(0, self.K, self.N, x, self.ws, wbytes=self.wb, quant_mode=mode)[0]
+        return oracle.linear_forward(self.fmt, self.K, self.N, x, self.ws, wbytes=self.wb, quant_mode=mode)[0]
 
 
 def build(rng, shapes, layers, M, order, sparse_down=False):
@@ -178,5 +179,106 @@ def test_stack_rejects_bad_ops():
         xtern.Stack([([m.w], x, [y], None)], 33)      # M above 32
     p5 = xtern.DeviceWeights(xtern.XT_PACK5, 256, 32,
                              np.concatenate([xtern.pack_ternary5(r) for r in m.t]), m.ws)
+    x2 = torch.zeros((2, 256), device="cuda")
+    y2 = torch.zeros((2, 32), device="cuda")
     with pytest.raises(xtern.XternError):
-        xtern.Stack([([p5], x, [y], None)], 1)        # Pack5 not on the stack
+        xtern.Stack([([p5], x2, [y2], None)], 2)      # Pack5 only on the M = 1 stack
+    with pytest.raises(xtern.XternError):
+        xtern.Stack([([m.w], x, [y], None), ([m.w], x, [y], 0)], 1)  # x not an output of dep
+    with pytest.raises(xtern.XternError):
+        xtern.Stack([([m.w, p5], x, [y, y], None)], 1)  # Pack4 and Pack5 in one op
+
+
+def build_chain(rng, mats, M, x0):
+    """The strict projection chain: q/k/v read the previous down output, o
+    reads q, gate/up read o, down reads up (every op waits for the one
+    before it).  mats: per layer {name: Mat}."""
+    dev = "cuda"
+    ops, checks = [], []
+    h_prev, dep_prev = x0, None
+    for m in mats:
+        outs = {n: torch.full((M, m[n].N), float("nan"), dtype=torch.float32, device=dev) for n in m}
+        seq = [(["q", "k", "v"], h_prev, dep_prev), (["o"], outs["q"], "last"),
+               (["gate", "up"], outs["o"], "last"), (["down"], outs["up"], "last")]
+        for names, x, dep in seq:
+            d = len(ops) - 1 if dep == "last" else dep
+            ys = [outs[n] for n in names]
+            ops.append(([m[n].w for n in names], x, ys, d))
+            checks.append((len(ops) - 1, names, ys, x, m))
+        h_prev, dep_prev = outs["down"], len(ops) - 1
+    return ops, checks
+
+
+def run_and_compare(ops, checks, M, mode, reps=2):
+    exp = expected(checks, mode)
+    st = xtern.Stack(ops, M, mode)
+    for rep in range(reps):
+        for _, _, ys, _, _ in checks:
+            for y in ys:
+                y.fill_(float("nan"))
+        st.run()
+        torch.cuda.synchronize()
+        assert not st.gave_up()
+        compare(checks, exp, f"run {rep}")
+
+
+def test_stack_m1_strict_chain_bitnet():
+    """Two BitNet-2B layers as the strict chain q/k/v -> o -> gate/up -> down."""
+    log("stack strict chain, bitnet, M=1")
+    rng = np.random.default_rng(zlib.crc32(b"strict_chain") & 0xffff)
+    mats = [{n: Mat(rng, K, N, ws_scale=0.3) for n, (K, N) in BITNET.items()} for _ in range(2)]
+    x0 = torch.from_numpy(rng.standard_normal((1, 2560)).astype(np.float32)).cuda()
+    ops, checks = build_chain(rng, mats, 1, x0)
+    run_and_compare(ops, checks, 1, xtern.XT_QUANT_AVX512, reps=3)
+
+
+def test_stack_m1_bitnet_30_layers():
+    """The full 30-layer BitNet-2B projection chain at M = 1 (120 ops, 210
+    projections) against the oracle.  Layers share one set of 7 matrices (the
+    device weights are the same handles; the host builds 7 matrices, not
+    210); every layer still reads the previous layer's output from inside the
+    launch."""
+    log("stack 30-layer bitnet chain, M=1")
+    rng = np.random.default_rng(zlib.crc32(b"bitnet30") & 0xffff)
+    shared = {n: Mat(rng, K, N, ws_scale=0.3) for n, (K, N) in BITNET.items()}
+    x0 = torch.from_numpy(rng.standard_normal((1, 2560)).astype(np.float32)).cuda()
+    ops, checks = build_chain(rng, [shared] * 30, 1, x0)
+    assert len(ops) == 120
+    run_and_compare(ops, checks, 1, xtern.XT_QUANT_SCALAR)
+
+
+PACK5_3B = {"q": (3200, 3200), "k": (3200, 320), "v": (3200, 320), "o": (3200, 3200),
+            "gate": (3200, 8640), "up": (3200, 8640), "down": (8640, 3200)}
+
+
+@pytest.mark.parametrize("mode", [xtern.XT_QUANT_AVX512, xtern.XT_QUANT_SCALAR])
+def test_stack_m1_pack5_chain(mode):
+    """Pack5 weights (BitNet-3B shapes) on the M = 1 stack,
+    strict chain, two layers."""
+    log(f"stack pack5 chain M=1 mode={mode}")
+    rng = np.random.default_rng(zlib.crc32(b"pack5_chain") & 0xffff + mode)
+    mats = [{n: Mat(rng, K, N, pack5=True, ws_scale=0.3) for n, (K, N) in PACK5_3B.items()} for _ in range(2)]
+    x0 = torch.from_numpy(rng.standard_normal((1, 3200)).astype(np.float32)).cuda()
+    ops, checks = build_chain(rng, mats, 1, x0)
+    run_and_compare(ops, checks, 1, mode)
+
+
+def test_stack_m1_ragged_mixed_formats():
+    """Ragged shapes (N not a multiple of 16, K not of 256), XorSparse and
+    Pack4 projections, and a Pack5 op in one M = 1 stack."""
+    log("stack ragged mixed formats M=1")
+    rng = np.random.default_rng(zlib.crc32(b"ragged_mixed") & 0xffff)
+    a = Mat(rng, 300, 76)
+    b = Mat(rng, 300, 45, sparse=True)
+    c = Mat(rng, 76, 132, pack5=True)
+    d = Mat(rng, 132, 300, sparse=True)
+    x0 = torch.from_numpy(rng.standard_normal((1, 300)).astype(np.float32)).cuda()
+    ya = torch.full((1, 76), float("nan"), device="cuda")
+    yb = torch.full((1, 45), float("nan"), device="cuda")
+    yc = torch.full((1, 132), float("nan"), device="cuda")
+    yd = torch.full((1, 300), float("nan"), device="cuda")
+    ops = [([a.w, b.w], x0, [ya, yb], None), ([c.w], ya, [yc], 0), ([d.w], yc, [yd], 1),
+           ([a.w], yd, [torch.full((1, 76), float("nan"), device="cuda")], 2)]
+    checks = [(0, ["a", "b"], [ya, yb], x0, {"a": a, "b": b}), (1, ["c"], [yc], ya, {"c": c}),
+              (2, ["d"], [yd], yc, {"d": d}), (3, ["a"], ops[3][2], yd, {"a": a})]
+    run_and_compare(ops, checks, 1, xtern.XT_QUANT_AVX512, reps=3)

@@ -228,6 +228,23 @@ int run_product_xs(const xt_weights* const* ws, int n, const int8_t* q, int ldq,
     return XT_OK;
 }
 
+// Row groups from which a single decode product takes the streaming GEMV.
+constexpr int kGStreamMinGroups = 16384;
+
+// Compute units of the current device (cached per device).
+int device_cus(int* cus) {
+    static std::mutex mu;
+    static std::vector<int> cache;
+    int dev = 0;
+    XT_HIP(hipGetDevice(&dev));
+    std::lock_guard<std::mutex> lk(mu);
+    if ((int)cache.size() <= dev) cache.resize((size_t)dev + 1, 0);
+    if (cache[(size_t)dev] == 0)
+        XT_HIP(hipDeviceGetAttribute(&cache[(size_t)dev], hipDeviceAttributeMultiprocessorCount, dev));
+    *cus = cache[(size_t)dev];
+    return XT_OK;
+}
+
 int run_product(const xt_weights* const* ws, int n, const int8_t* q, int ldq, const float* inv,
                 const int32_t* rowsum, int64_t M, float* const* ys, int32_t* acc,
                 hipStream_t s, Scratch* sc = nullptr) {
@@ -236,6 +253,32 @@ int run_product(const xt_weights* const* ws, int n, const int8_t* q, int ldq, co
     if (fmt == XT_XORSPARSE_STREAM) return run_product_xs(ws, n, q, ldq, inv, M, ys, acc, s);
     int ng_total = 0;
     for (int p = 0; p < n; ++p) ng_total += (int)((ws[p]->N + 15) / 16);
+    // Tall matrices at decode sizes: the streaming GEMV (every wave walks its
+    // own row groups; xtern_gstream.hip).  Measured on MI355X: 121 stacked C0
+    // matrices (52272 row groups) at M = 1 6.5 TB/s against 4.7 TB/s on the
+    // one-shot GEMV; 17280 row groups at M = 2 / 4 / 8 5.9 / 5.4 / 5.2 TB/s.
+    if (n == 1 && M >= 1 && M <= 16 && (fmt == XT_PACK4 || fmt == XT_XORSPARSE) &&
+        ng_total >= kGStreamMinGroups && xt::gstream_fits(fmt, (int)M, (int)ws[0]->nch) &&
+        (reinterpret_cast<uintptr_t>(q) & 15) == 0 && ldq % 16 == 0) {
+        int cus = 0;
+        if (int rc = device_cus(&cus)) return rc;
+        xt::GStreamArgs g;
+        memset(&g, 0, sizeof g);
+        g.tiles = ws[0]->tiles;
+        g.ws = ws[0]->ws;
+        g.y = ys[0];
+        g.acc = acc;
+        g.q = q;
+        g.inv = inv;
+        g.M = (int)M;
+        g.ldq = ldq;
+        g.nch = (int)ws[0]->nch;
+        g.NG = ng_total;
+        g.N = (int)ws[0]->N;
+        hipError_t e = xt::launch_gstream(fmt, g, 4 * cus, M == 1 ? 2 : 4, s);
+        if (e != hipSuccess) return hip_fail(e, "streaming GEMV launch");
+        return XT_OK;
+    }
     const xt::MMConfig cfg =
         xt::choose_config(fmt, (int)M, ng_total, (int)ws[0]->nch, rowsum != nullptr);
     xt::MMArgs a;
@@ -899,11 +942,173 @@ int xt_workspace_release(void) {
 }
 
 struct xt_stack {
-    xt::StackArgs args;
+    xt::StackArgs args;    // M > 1: the persistent item kernel (xtern_stack.hip)
+    xt::SStackArgs sargs;  // M = 1: the streaming kernel (xtern_sstack.hip)
+    bool stream;
     int blocks;
     int device;
     void* dev_mem;  // ops, items, counters, scratch (one allocation)
 };
+
+namespace {
+
+// Op order shared by both stack forms: ops that others wait for go as early
+// as their own inputs allow, the rest keep the caller's order.  (Ops with no
+// dependency path between them may run in any order: they share no buffers,
+// per the contract in xtern.h.)  Every op still follows the op it depends on.
+std::vector<int> stack_order(const xt_stack_op* ops, int nops, const std::vector<char>& pub) {
+    std::vector<int> order;
+    std::vector<char> placed((size_t)nops, 0);
+    while ((int)order.size() < nops) {
+        int pick = -1;
+        for (int i = 0; i < nops && pick < 0; ++i)
+            if (!placed[(size_t)i] && (ops[i].dep < 0 || placed[(size_t)ops[i].dep]) && pub[(size_t)i]) pick = i;
+        for (int i = 0; i < nops && pick < 0; ++i)
+            if (!placed[(size_t)i] && (ops[i].dep < 0 || placed[(size_t)ops[i].dep])) pick = i;
+        placed[(size_t)pick] = 1;
+        order.push_back(pick);
+    }
+    return order;
+}
+
+// M = 1: the streaming stack.  Tasks in list order: the quantiser tasks of
+// ops without a dependency, then per op (in stack_order) its 16-row groups
+// followed by the quantiser tasks of the ops that read its outputs.
+int create_sstack(const xt_stack_op* ops, int nops, int mode, xt_stack** out) {
+    if (nops > xt::kSStackMaxOps)
+        return fail(XT_ERR_UNSUPPORTED, "at most " + std::to_string(xt::kSStackMaxOps) + " ops per M = 1 stack");
+    struct OpInfo {
+        int fmt, nch, ldq, K, ngroups;
+        size_t qoff;
+    };
+    std::vector<OpInfo> info((size_t)nops);
+    std::vector<char> pub((size_t)nops, 0);
+    size_t scratch = 0, ntasks = 0;
+    for (int i = 0; i < nops; ++i) {
+        const xt_stack_op& op = ops[i];
+        const std::string at = "op " + std::to_string(i) + ": ";
+        const int fmt = op.w[0]->fmt;
+        const int ch = fmt == XT_PACK5 ? 320 : 256;
+        OpInfo& f = info[(size_t)i];
+        f.ngroups = 0;
+        for (int p = 0; p < op.n; ++p) {
+            const xt_weights* w = op.w[p];
+            if (w->fmt != XT_PACK4 && w->fmt != XT_XORSPARSE && w->fmt != XT_PACK5)
+                return fail(XT_ERR_UNSUPPORTED, at + "stack weights must be Pack4, Pack5 or XorSparse");
+            if ((w->fmt == XT_PACK5) != (fmt == XT_PACK5))
+                return fail(XT_ERR_UNSUPPORTED, at + "projections of one op must share the tile format");
+            if (w->K != op.w[0]->K) return fail(XT_ERR_INVALID, at + "projections must share in_dim");
+            if (w->K % 4 != 0 || w->nch * ch > xt::kSStackMaxRowBytes)
+                return fail(XT_ERR_UNSUPPORTED, at + "in_dim must be a multiple of 4 and at most " +
+                                                    std::to_string(xt::kSStackMaxRowBytes / ch * ch));
+            f.ngroups += (int)((w->N + 15) / 16);
+        }
+        f.fmt = fmt == XT_PACK5 ? XT_PACK5 : XT_PACK4;
+        f.K = (int)op.w[0]->K;
+        f.nch = (int)op.w[0]->nch;
+        f.ldq = f.nch * ch;
+        f.qoff = scratch;
+        scratch += align_up((size_t)f.ldq + 8, 256);  // row, then its sum and scale
+        ntasks += 1 + (size_t)f.ngroups;
+        if (op.dep >= 0) pub[(size_t)op.dep] = 1;
+    }
+    // 16-row groups per task: as many as keep about four tasks per wave of
+    // a full grid (a task's row load and start are paid once per task)
+    int dev0 = 0, cus0 = 0;
+    XT_HIP(hipGetDevice(&dev0));
+    XT_HIP(hipDeviceGetAttribute(&cus0, hipDeviceAttributeMultiprocessorCount, dev0));
+    size_t all_groups = 0;
+    for (const OpInfo& f : info) all_groups += (size_t)f.ngroups;
+    const int rg = (int)std::max<size_t>(1, std::min<size_t>(8, all_groups / ((size_t)cus0 * 16 * 4)));
+    ntasks = nops;
+    for (int i = 0; i < nops; ++i)
+        for (int p = 0; p < ops[i].n; ++p) ntasks += (size_t)(((ops[i].w[p]->N + 15) / 16 + rg - 1) / rg);
+    if (ntasks > (size_t)1 << 30) return fail(XT_ERR_UNSUPPORTED, "stack too large");
+    const size_t tasks_b = align_up(ntasks * sizeof(xt::SStackTask), 256);
+    const size_t ctr_b = (size_t)(4 + 2 * nops) * 128;
+    char* mem = nullptr;
+    hipError_t e = hipMalloc(reinterpret_cast<void**>(&mem), tasks_b + ctr_b + scratch);
+    if (e != hipSuccess) return fail(XT_ERR_NOMEM, std::string("stack allocation: ") + hipGetErrorString(e));
+    char* sc = mem + tasks_b + ctr_b;
+
+    std::vector<xt::SStackTask> tasks;
+    tasks.reserve(ntasks);
+    auto base = [&](int i) {
+        const OpInfo& f = info[(size_t)i];
+        xt::SStackTask t;
+        memset(&t, 0, sizeof t);
+        t.q = reinterpret_cast<int8_t*>(sc + f.qoff);
+        t.opi = i;
+        t.nch = f.nch;
+        t.K = f.K;
+        t.ldq = f.ldq;
+        t.dep = ops[i].dep;
+        t.dep_groups = ops[i].dep >= 0 ? info[(size_t)ops[i].dep].ngroups : 0;
+        return t;
+    };
+    auto quant_task = [&](int i) {
+        xt::SStackTask t = base(i);
+        t.tiles = ops[i].x;
+        t.flags = 1;
+        tasks.push_back(t);
+    };
+    for (int i = 0; i < nops; ++i)
+        if (ops[i].dep < 0) quant_task(i);
+    for (int i : stack_order(ops, nops, pub)) {
+        const xt_stack_op& op = ops[i];
+        for (int p = 0; p < op.n; ++p) {
+            const xt_weights* w = op.w[p];
+            const int64_t ng = (w->N + 15) / 16;
+            for (int64_t G = 0; G < ng; G += rg) {
+                const int n_g = (int)std::min<int64_t>(rg, ng - G);
+                xt::SStackTask t = base(i);
+                t.tiles = w->tiles + (size_t)G * w->nch * xt::kTileBytes;
+                t.ws = w->ws + G * 16;
+                t.y = op.y[p] + G * 16;
+                t.flags = (pub[(size_t)i] ? 2 : 0) | (info[(size_t)i].fmt == XT_PACK5 ? 4 : 0) | (n_g << 16);
+                t.nrows = (int)std::min<int64_t>(16, w->N - (G + n_g - 1) * 16);
+                tasks.push_back(t);
+            }
+        }
+        for (int k = i + 1; k < nops; ++k)
+            if (ops[k].dep == i) quant_task(k);
+    }
+    int dev = 0, cus = 0, per_cu = 0;
+    e = hipGetDevice(&dev);
+    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e == hipSuccess) e = xt::sstack_blocks_per_cu(&per_cu);
+    if (e == hipSuccess && per_cu < 1) e = hipErrorInvalidConfiguration;
+    if (e == hipSuccess) e = hipMemcpy(mem, tasks.data(), tasks.size() * sizeof(xt::SStackTask), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemset(mem + tasks_b, 0, ctr_b + scratch);
+    if (e == hipSuccess) e = hipDeviceSynchronize();
+    if (e != hipSuccess) {
+        (void)hipFree(mem);
+        return hip_fail(e, "stack setup");
+    }
+    xt_stack* st = new (std::nothrow) xt_stack();
+    if (!st) {
+        (void)hipFree(mem);
+        return fail(XT_ERR_NOMEM, "stack handle");
+    }
+    // Every wave resident at once (see xtern_sstack.hip): at most the
+    // occupancy, and four workgroups per CU (16 waves) stream best.
+    const int wpb = xt::sstack_waves_per_block();
+    st->stream = true;
+    st->sargs.tasks = reinterpret_cast<const xt::SStackTask*>(mem);
+    st->sargs.ctr = reinterpret_cast<unsigned*>(mem + tasks_b);
+    st->sargs.ntasks = (int)tasks.size();
+    st->sargs.nops = nops;
+    st->sargs.mode = mode;
+    st->sargs.spin_limit = 1 << 20;  // polls (about a microsecond each) before a wait gives up
+    st->args.ctr = st->sargs.ctr;    // (the error slot, read by xt_stack_check)
+    st->blocks = std::max(1, std::min(cus * std::min(per_cu, 4), ((int)tasks.size() + wpb - 1) / wpb));
+    st->device = dev;
+    st->dev_mem = mem;
+    *out = st;
+    return XT_OK;
+}
+
+}  // namespace
 
 int xt_stack_create(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stack** out) {
     if (!out) return fail(XT_ERR_INVALID, "out is NULL");
@@ -916,6 +1121,24 @@ int xt_stack_create(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_st
     if (M < 1 || M > 32) return fail(XT_ERR_UNSUPPORTED, "stack M must be 1..32");
     if (mode != XT_QUANT_AVX512 && mode != XT_QUANT_SCALAR)
         return fail(XT_ERR_INVALID, "unknown quantisation mode");
+    for (int i = 0; i < nops; ++i) {
+        const xt_stack_op& op = ops[i];
+        const std::string at = "op " + std::to_string(i) + ": ";
+        if (op.n < 1 || op.n > 4) return fail(XT_ERR_INVALID, at + "n must be 1..4");
+        if (!op.x) return fail(XT_ERR_INVALID, at + "x is NULL");
+        if (op.dep < -1 || op.dep >= i) return fail(XT_ERR_INVALID, at + "dep must be -1 or an earlier op");
+        for (int p = 0; p < op.n; ++p)
+            if (!op.w[p] || !op.y[p]) return fail(XT_ERR_INVALID, at + "NULL weights or output");
+        if (op.dep >= 0) {
+            int src = -1;
+            for (int p = 0; p < ops[op.dep].n; ++p)
+                if (ops[op.dep].y[p] == op.x) src = p;
+            if (src < 0) return fail(XT_ERR_INVALID, at + "x must be one of the dep op's outputs");
+            if (ops[op.dep].w[src]->N != op.w[0]->K)
+                return fail(XT_ERR_INVALID, at + "x (an output of the dep op) differs in length from in_dim");
+        }
+    }
+    if (M == 1) return create_sstack(ops, nops, mode, out);
     const int rq = xt::stack_rows_per_quant_item();
     const bool one = xt::stack_pipelined((int)M);  // M = 1: rows quantised once per op
     int slots = 0;
@@ -1112,7 +1335,8 @@ int xt_stack_create(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_st
 
 int xt_stack_run(const xt_stack* st, void* stream) {
     if (!st) return fail(XT_ERR_INVALID, "stack is NULL");
-    hipError_t e = xt::launch_stack(st->args, st->blocks, static_cast<hipStream_t>(stream));
+    hipError_t e = st->stream ? xt::launch_sstack(st->sargs, st->blocks, static_cast<hipStream_t>(stream))
+                              : xt::launch_stack(st->args, st->blocks, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "stack launch");
     return XT_OK;
 }

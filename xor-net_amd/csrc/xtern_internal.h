@@ -71,6 +71,23 @@ struct MMArgs {
 constexpr int kGemvFusedQuantMax = 8192;
 constexpr int kGemv2FusedQuantMax = 16384;
 
+// Streaming decode GEMV (xtern_gstream.hip): one projection, M <= 16 rows
+// of i8 activations given.
+struct GStreamArgs {
+    const uint8_t* tiles;  // [NG][nch][64][16]
+    const float* ws;       // [N]
+    float* y;              // [M][N]
+    int32_t* acc;          // optional [M][N]
+    const int8_t* q;       // [M][ldq], zero beyond in_dim up to nch * CH
+    const float* inv;      // [M]
+    int M, ldq, nch, NG, N;
+    // set by the launcher: LDS row stride, row groups [G0, G1) of this
+    // launch, the most groups of one wave, the sums' LDS offset
+    int lda, G0, G1, rg_max, sums_off;
+};
+bool gstream_fits(int fmt, int M, int nch);
+hipError_t launch_gstream(int fmt, const GStreamArgs& a, int grid, int d, hipStream_t s);
+
 struct MMConfig {
     int mb, nb, waves, pf;  // tokens per WG = 16*mb, rows per WG = 16*nb
     int splitk;             // workgroups along K (blockIdx.z)
@@ -155,6 +172,30 @@ int xs_max_rows();
 // Address (on the current device) and size of the static device scratch used
 // by the allocation-free entry point; resolved once per device.
 hipError_t scratch_region(void** ptr, size_t* bytes);
+// Streaming decode stack, M = 1 (xtern_sstack.hip).
+constexpr int kSStackMaxOps = 8191;          // op index: 13 bits of a task
+constexpr int kSStackMaxRowBytes = 9216;     // i8 row (nch * chunk columns) of one op, at most
+// One task, 64 bytes: everything a wave needs to start it, loaded one task
+// ahead.  flags bits 0-15: 1 quantiser task, 2 other ops read the outputs
+// (count the groups' completion), 4 Pack5 tiles; bits 16-31: the task's
+// consecutive 16-row groups (one projection), nrows: rows of the last one.
+struct alignas(16) SStackTask {
+    const void* tiles;        // group: its first tile; quantiser: the op's f32 input row
+    const float* ws;          // group: w_scales of its rows
+    float* y;                 // group: outputs of its rows
+    int8_t* q;                // the op's i8 row [ldq], then its i32 sum and f32 inverse scale
+    int opi, flags, nch, nrows;
+    int K, ldq, dep, dep_groups;  // dep: op whose outputs x reads, or -1; its group count
+};
+static_assert(sizeof(SStackTask) == 64, "a task record is four 16-byte loads");
+struct SStackArgs {
+    const SStackTask* tasks;
+    unsigned* ctr;            // (4 + 2 * nops) slots of 128 bytes, zero between launches
+    int ntasks, nops, mode, spin_limit;
+};
+hipError_t launch_sstack(const SStackArgs& a, int blocks, hipStream_t s);
+hipError_t sstack_blocks_per_cu(int* n);
+int sstack_waves_per_block();
 // Persistent decode stack (xtern_stack.hip): one launch over a list of ops.
 constexpr int kStackRowGroupsMax = 8;       // 16-row groups per GEMV item (M > 1): stack_gemv_rg
 constexpr int kStackMaxOps = 4095;

@@ -1,0 +1,374 @@
+// Streaming decode stack (M = 1): a whole list of ternary projections in one
+// launch, every wave walking its own sequence of 16-row groups.
+//
+// Reference behaviour: the layer loop of the BitNet decode step
+// (src/models/llama/mod.rs:420-470) calls TernaryLinear::forward /
+// fused_forward_qkv / fused_forward_mlp per projection, each bit-exact with
+// TernaryLinear::forward (src/bit1_58/layers.rs:262-313): per-token absmax
+// quantisation (quantization.rs:95-195), the exact i32 dot of `dot_row`
+// (:216-231) over pack4 / pack5 / sparse weights, (f32)dot * inv * w_scale.
+//
+// Work list.  The host flattens the ops into tasks: one quantiser task per op
+// (the op's f32 input row -> i8 row, its exact sum and inverse scale) and one
+// task per 16-row group of each of the op's projections.  Every task follows
+// the tasks it waits for: an op's quantiser task comes after the last group
+// of the op its input comes from, its groups after its quantiser task.  Wave
+// gw of the grid (TW waves) takes tasks gw, gw + TW, gw + 2 TW, ... in that
+// order; the grid is no larger than what is resident at once, so the wave
+// holding the earliest unfinished task is running and has its inputs, and
+// the launch always finishes.  Waits are bounded anyway: one that gives up
+// sets a flag for the host, and all later waits of the launch return at once.
+//
+// A group task streams its nch weight tiles (1 KiB each) D at a time with the
+// row's i8 pieces in the wave's own LDS region (no barrier: a wave's LDS
+// accesses complete in order).  The loads that start a group -- the
+// quantiser-done count, the i8 row, its sum and scale, the w_scales and the
+// first D tiles -- are issued together; if the count shows the row not yet
+// written, the wave waits for it and loads the row again.  This is the
+// streaming GEMV's walk (xtern_gstream.hip) with the dependency checks added:
+// every wave keeps its own loads in flight, no workgroup-wide phases.
+//
+// Coherence across the eight XCDs (each has its own L2): data one task writes
+// for another (quantised rows, outputs other ops read) is written and read
+// with device-scope accesses, and a count is bumped only after the writer's
+// stores have completed.  The last wave out resets the counts, so the next
+// launch starts from zero without a memset.
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <type_traits>
+
+#include "xtern_device.h"
+#include "xtern_internal.h"
+
+namespace xt {
+
+namespace {
+
+constexpr int kSsW = 4;   // waves per workgroup
+constexpr int kSsD = 2;   // tiles per batch
+constexpr int kSsKnownWords = kSStackMaxOps / 32 + 1;
+
+__device__ __forceinline__ unsigned* ss_ctr(unsigned* c, int slot) { return c + slot * 32; }
+constexpr int kSsExit = 1, kSsError = 2, kSsDone0 = 4;
+constexpr int kSsQuant = 1, kSsPub = 2, kSsPack5 = 4;  // SStackTask::flags
+
+__device__ __forceinline__ unsigned ss_ld_coh(const unsigned* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void ss_st_coh(unsigned* p, unsigned v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Device-scope 16-byte loads and 4-byte stores through buffer resources
+// (cache policy 16: coherent across the XCDs' L2s).  Offsets past the
+// resource read zeros without a memory access.
+constexpr int kSsCoh = 16;
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t ss_rsrc(const void* base, unsigned bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+__device__ __forceinline__ v4i ss_ld_coh16(__amdgpu_buffer_rsrc_t r, unsigned off) {
+    return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kSsCoh);
+}
+__device__ __forceinline__ void ss_st_coh4(__amdgpu_buffer_rsrc_t r, unsigned off, unsigned v) {
+    __builtin_amdgcn_raw_buffer_store_b32(v, r, off, 0, kSsCoh);
+}
+
+// Lane 0 waits until *c >= target (bounded; see the file comment).
+__device__ __forceinline__ void ss_wait(unsigned* c, unsigned target, unsigned* err, int limit) {
+    for (int n = 0; ss_ld_coh(c) < target; ++n) {
+        if (n >= limit) {
+            ss_st_coh(err, 1u);
+            break;
+        }
+        if ((n & 63) == 63 && ss_ld_coh(err)) break;
+        __builtin_amdgcn_s_sleep(2);
+    }
+}
+
+__device__ __forceinline__ v4i ss_lds16(uint32_t addr) {
+    return *reinterpret_cast<const __attribute__((address_space(3))) v4i*>((uintptr_t)addr);
+}
+
+// A task record, as uniform values (see SStackTask).
+struct Rec {
+    const uint8_t* tiles;  // group: the group's first tile; quantiser: the f32 input row
+    const float* ws;       // group: w_scales of its 16 rows
+    float* y;              // group: outputs of its 16 rows
+    int8_t* q;             // the op's i8 row, then its sum and inverse scale
+    int opi, flags, nch, nrows, K, ldq, dep, dep_groups, ngroups;
+};
+__device__ __forceinline__ Rec ss_rec(const SStackTask* t) {
+    const v4i* v = reinterpret_cast<const v4i*>(t);
+    const v4i a = v[0], b = v[1], c = v[2], d = v[3];
+    auto u = [](int x) { return (uint32_t)__builtin_amdgcn_readfirstlane(x); };
+    auto ptr = [&](int lo, int hi) { return (uint64_t)u(lo) | ((uint64_t)u(hi) << 32); };
+    Rec r;
+    r.tiles = reinterpret_cast<const uint8_t*>(ptr(a[0], a[1]));
+    r.ws = reinterpret_cast<const float*>(ptr(a[2], a[3]));
+    r.y = reinterpret_cast<float*>(ptr(b[0], b[1]));
+    r.q = reinterpret_cast<int8_t*>(ptr(b[2], b[3]));
+    r.opi = (int)u(c[0]);
+    r.flags = (int)u(c[1]) & 0xffff;
+    r.ngroups = (int)(u(c[1]) >> 16);
+    r.nch = (int)u(c[2]);
+    r.nrows = (int)u(c[3]);
+    r.K = (int)u(d[0]);
+    r.ldq = (int)u(d[1]);
+    r.dep = (int)u(d[2]);
+    r.dep_groups = (int)u(d[3]);
+    return r;
+}
+
+// The quantiser task of an op (one wave): quantization.rs:95-195 on the f32
+// row -> i8 row (zero from K to ldq), its exact sum and its inverse scale.
+template <int MODE>
+__device__ void ss_quant(const SStackArgs& a, const Rec& r) {
+    const int lane = threadIdx.x & 63;
+    const int K = r.K, n4 = K >> 2;
+    const bool coh = r.dep >= 0;  // the input is written inside the launch
+    if (coh && lane == 0)
+        ss_wait(ss_ctr(a.ctr, kSsDone0 + r.dep), (unsigned)r.dep_groups, ss_ctr(a.ctr, kSsError), a.spin_limit);
+    __builtin_amdgcn_wave_barrier();
+    // pieces past K read as zero; an input written before the launch takes
+    // ordinary cached loads
+    const __amdgpu_buffer_rsrc_t xr = ss_rsrc(r.tiles, (unsigned)(K * 4));
+    auto load4 = [&](int f) -> float4 {
+        const v4i v = coh ? ss_ld_coh16(xr, (unsigned)f * 16u)
+                          : __builtin_amdgcn_raw_buffer_load_b128(xr, (unsigned)f * 16u, 0, 0);
+        return make_float4(__int_as_float(v[0]), __int_as_float(v[1]), __int_as_float(v[2]),
+                           __int_as_float(v[3]));
+    };
+    // the row in rounds of kSsQ pieces per lane, all of a round's loads in
+    // flight at once; a row of at most one round stays in
+    // registers for the second pass (12: K <= 3072 in one round, and the
+    // kernel stays within 128 VGPRs, four waves per SIMD)
+    constexpr int kSsQ = 12;
+    const int rounds = (n4 + 64 * kSsQ - 1) / (64 * kSsQ);
+    float4 v[kSsQ];
+    float mx = 0.0f;
+    for (int rd = 0; rd < rounds; ++rd) {
+#pragma unroll
+        for (int u = 0; u < kSsQ; ++u) v[u] = load4((rd * kSsQ + u) * 64 + lane);
+#pragma unroll
+        for (int u = 0; u < kSsQ; ++u)
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(v[u].x), fabsf(v[u].y)), fmaxf(fabsf(v[u].z), fabsf(v[u].w))));
+    }
+    const float rmx = __int_as_float(wave_reduce_bits(__float_as_int(mx), [](int p, int q) {
+        return __float_as_int(fmaxf(__int_as_float(p), __int_as_float(q)));
+    }));
+    const float scale = (rmx > 0.0f) ? __fdiv_rn(127.0f, rmx) : 1.0f;
+    const float invs = (rmx > 0.0f) ? __fdiv_rn(rmx, 127.0f) : 1.0f;
+    const int kmain = (K / 16) * 16;
+    int rs = 0;
+    const __amdgpu_buffer_rsrc_t qr = ss_rsrc(r.q, (unsigned)(r.ldq + 8));
+    const int n4q = r.ldq / 4;  // (ldq >= K: the i8 row is zero from K on)
+    const int qrounds = (n4q + 64 * kSsQ - 1) / (64 * kSsQ);
+    for (int rd = 0; rd < qrounds; ++rd) {
+        if (rounds > 1 || rd > 0) {  // (uniform) reload: the registers hold one round only
+#pragma unroll
+            for (int u = 0; u < kSsQ; ++u) v[u] = load4((rd * kSsQ + u) * 64 + lane);
+        }
+#pragma unroll
+        for (int u = 0; u < kSsQ; ++u) {
+            const int f = (rd * kSsQ + u) * 64 + lane;
+            const float e4[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+            unsigned w = 0;
+#pragma unroll
+            for (int t = 0; t < 4; ++t)
+                w |= (unsigned)(quant_one(e4[t], scale, MODE, 4 * f + t < kmain) & 255) << (8 * t);
+            rs = __builtin_amdgcn_sdot4((int)w, 0x01010101, rs, false);
+            // (pieces past ldq land out of the resource: no store)
+            ss_st_coh4(qr, f < n4q ? (unsigned)f * 4u : 0x80000000u, w);
+        }
+    }
+    rs = wave_reduce_bits(rs, [](int p, int q) { return p + q; });
+    if (lane == 0) {
+        ss_st_coh4(qr, (unsigned)r.ldq, (unsigned)rs);
+        ss_st_coh4(qr, (unsigned)r.ldq + 4u, __float_as_uint(invs));
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // (vmcnt and lgkmcnt 0: every store has completed)
+    if (lane == 0)
+        __hip_atomic_fetch_add(ss_ctr(a.ctr, kSsDone0 + a.nops + r.opi), 1u, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// A block of r.ngroups consecutive 16-row groups of one projection, each over
+// all of K; areg: this wave's LDS region for the i8 row (loaded once per
+// block).
+template <int FMT>
+__device__ void ss_block(const SStackArgs& a, const Rec& r, uint32_t areg, unsigned* known) {
+    constexpr int STEPS = (FMT == XT_PACK5) ? 5 : 4;
+    constexpr int CH = STEPS * 64;
+    constexpr int kPieces = kSStackMaxRowBytes / 1024;  // 16-byte row pieces per lane, at most
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, j = lane & 15;
+    const int nch = r.nch, opi = r.opi;
+    const int npieces = r.ldq / 16;
+    const uint8_t* const tl = r.tiles + lane * 16;
+    unsigned* const qdone = ss_ctr(a.ctr, kSsDone0 + a.nops + opi);
+    const bool seen = (known[opi >> 5] >> (opi & 31)) & 1u;
+
+    // the loads that start the block, issued together (the count first)
+    const unsigned ready = seen ? 1u : ss_ld_coh(qdone);
+    const __amdgpu_buffer_rsrc_t qr = ss_rsrc(r.q, (unsigned)(r.ldq + 8));
+    v4i pc[kPieces];
+    int rsum;
+    float inv;
+    auto load_row = [&]() {
+#pragma unroll
+        for (int u = 0; u < kPieces; ++u) {
+            const int i = lane + 64 * u;
+            if (64 * u < npieces)  // (uniform)
+                pc[u] = ss_ld_coh16(qr, i < npieces ? (unsigned)i * 16u : 0x80000000u);
+        }
+        rsum = (int)__builtin_amdgcn_raw_buffer_load_b32(qr, (unsigned)r.ldq, 0, kSsCoh);
+        inv = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(qr, (unsigned)r.ldq + 4u, 0, kSsCoh));
+    };
+    load_row();
+    float wsc = r.ws[j];
+    v4i wb[kSsD];
+#pragma unroll
+    for (int s = 0; s < kSsD; ++s)
+        wb[s] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(tl + (size_t)min(s, nch - 1) * kTileBytes));
+    if (!seen) {
+        if (ready < 1u) {  // (uniform) not quantised yet: wait, then load the row again
+            if (lane == 0) ss_wait(qdone, 1u, ss_ctr(a.ctr, kSsError), a.spin_limit);
+            __builtin_amdgcn_wave_barrier();
+            load_row();
+        }
+        if (lane == 0) atomicOr(&known[opi >> 5], 1u << (opi & 31));
+    }
+    // the row into this wave's LDS region (its own LDS accesses complete in
+    // order: the reads below see these stores, and the previous task's reads
+    // came before them)
+#pragma unroll
+    for (int u = 0; u < kPieces; ++u) {
+        const int i = lane + 64 * u;
+        if (i < npieces)
+            *reinterpret_cast<__attribute__((address_space(3))) v4i*>((uintptr_t)(areg + (uint32_t)i * 16u)) = pc[u];
+    }
+    const uint32_t abase = areg + (uint32_t)(g * 16);
+    const bool pub = (r.flags & kSsPub) != 0;
+
+    for (int gi = 0; gi < r.ngroups; ++gi) {
+        const uint8_t* const tg = tl + (size_t)gi * nch * kTileBytes;
+        if (gi > 0) {  // (the first group's scale and first tiles came with the row)
+            wsc = r.ws[gi * 16 + j];
+#pragma unroll
+            for (int s = 0; s < kSsD; ++s)
+                wb[s] = __builtin_nontemporal_load(
+                    reinterpret_cast<const v4i*>(tg + (size_t)min(s, nch - 1) * kTileBytes));
+        }
+        v4i acc[STEPS];
+#pragma unroll
+        for (int st = 0; st < STEPS; ++st) acc[st] = v4i{0, 0, 0, 0};
+        for (int t0 = 0; t0 < nch; t0 += kSsD) {
+            if (t0 > 0) {
+#pragma unroll
+                for (int s = 0; s < kSsD; ++s)
+                    wb[s] = __builtin_nontemporal_load(
+                        reinterpret_cast<const v4i*>(tg + (size_t)min(t0 + s, nch - 1) * kTileBytes));
+            }
+#pragma unroll
+            for (int s = 0; s < kSsD; ++s) {
+                if (t0 + s >= nch) break;  // (uniform)
+                const uint32_t ab = abase + (uint32_t)((t0 + s) * CH);
+                if constexpr (FMT == XT_PACK5) {
+                    int E[4], O[4];
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        E[q] = wb[s][q] & 0x00ff00ff;
+                        O[q] = ((unsigned)wb[s][q] >> 8) & 0x00ff00ff;
+                    }
+#pragma unroll
+                    for (int st = 0; st < STEPS; ++st) {
+                        v4i b;
+#pragma unroll
+                        for (int q = 0; q < 4; ++q) {
+                            const int pE = E[q] * 3, pO = O[q] * 3;
+                            b[q] = (int)__builtin_amdgcn_perm((unsigned)pO, (unsigned)pE, 0x07030501u);
+                            E[q] = pE & 0x00ff00ff;
+                            O[q] = pO & 0x00ff00ff;
+                        }
+                        acc[st] = mfma(ss_lds16(ab + st * 64), b, acc[st]);
+                    }
+                } else {
+#pragma unroll
+                    for (int st = 0; st < STEPS; ++st)
+                        acc[st] = mfma(ss_lds16(ab + st * 64), decode4(wb[s][st]), acc[st]);
+                }
+            }
+        }
+        int sum = acc[0][0];
+#pragma unroll
+        for (int st = 1; st < STEPS; ++st) sum += acc[st][0];
+        // token 0 sits in element 0 of the lanes with g == 0; the MFMAs took
+        // codes w + 1, so the row's sum comes off (layers.rs:340:
+        // (dot as f32 * inv) * w_scale)
+        const int nrows = gi + 1 == r.ngroups ? r.nrows : 16;
+        if (g == 0 && j < nrows) {
+            const float v = __fmul_rn(__fmul_rn((float)(sum - rsum), inv), wsc);
+            if (pub) ss_st_coh4(ss_rsrc(r.y, (unsigned)r.ngroups * 64u), (unsigned)(gi * 16 + j) * 4u, __float_as_uint(v));
+            else r.y[gi * 16 + j] = v;
+        }
+    }
+    if (pub) {  // another op reads these outputs inside the launch
+        __builtin_amdgcn_s_waitcnt(0);
+        if (lane == 0)
+            __hip_atomic_fetch_add(ss_ctr(a.ctr, kSsDone0 + opi), (unsigned)r.ngroups, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+__global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) void sstack_kernel(const SStackArgs a) {
+    __shared__ unsigned known[kSsKnownWords];  // ops this workgroup has seen quantised
+    __shared__ __align__(16) uint8_t rows[kSsW][kSStackMaxRowBytes];
+    for (int i = threadIdx.x; i < kSsKnownWords; i += kSsW * 64) known[i] = 0u;
+    __syncthreads();
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int TW = gridDim.x * kSsW;
+    const int gw = blockIdx.x * kSsW + wave;
+    const uint32_t areg = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)rows[wave];
+    // each task's record is loaded one task ahead
+    Rec nxt;
+    if (gw < a.ntasks) nxt = ss_rec(a.tasks + gw);
+    for (int t = gw; t < a.ntasks; t += TW) {
+        const Rec cur = nxt;
+        if (t + TW < a.ntasks) nxt = ss_rec(a.tasks + t + TW);
+        if (cur.flags & kSsQuant) {
+            if (a.mode == XT_QUANT_AVX512) ss_quant<XT_QUANT_AVX512>(a, cur);
+            else ss_quant<XT_QUANT_SCALAR>(a, cur);
+        } else if (cur.flags & kSsPack5) {
+            ss_block<XT_PACK5>(a, cur, areg, known);
+        } else {
+            ss_block<XT_PACK4>(a, cur, areg, known);
+        }
+    }
+    // the last wave out resets the counts for the next launch (its own
+    // bumps, like everyone's, were performed before its exit is counted)
+    __builtin_amdgcn_s_waitcnt(0);
+    unsigned old = 0;
+    if ((threadIdx.x & 63) == 0)
+        old = __hip_atomic_fetch_add(ss_ctr(a.ctr, kSsExit), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    old = __builtin_amdgcn_readfirstlane(old);
+    if (old == (unsigned)TW - 1) {
+        for (int i = threadIdx.x & 63; i < 2 * a.nops; i += 64) ss_st_coh(ss_ctr(a.ctr, kSsDone0 + i), 0u);
+        if ((threadIdx.x & 63) == 0) ss_st_coh(ss_ctr(a.ctr, kSsExit), 0u);
+    }
+}
+
+}  // namespace
+
+hipError_t launch_sstack(const SStackArgs& a, int blocks, hipStream_t s) {
+    hipLaunchKernelGGL(sstack_kernel, dim3(blocks), dim3(kSsW * 64), 0, s, a);
+    return hipGetLastError();
+}
+
+hipError_t sstack_blocks_per_cu(int* n) {
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(n, reinterpret_cast<const void*>(sstack_kernel),
+                                                        kSsW * 64, 0);
+}
+
+int sstack_waves_per_block() { return kSsW; }
+
+}  // namespace xt
