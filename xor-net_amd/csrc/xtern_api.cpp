@@ -1027,7 +1027,8 @@ int create_sstack(const xt_stack_op* ops, int nops, int mode, xt_stack** out) {
     const size_t tasks_b = align_up(ntasks * sizeof(xt::SStackTask), 256);
     const size_t ctr_b = (size_t)(4 + 2 * nops) * 128;
     char* mem = nullptr;
-    hipError_t e = hipMalloc(reinterpret_cast<void**>(&mem), tasks_b + ctr_b + scratch);
+    const size_t woff_b = align_up(((size_t)cus0 * 64 + 1) * 4, 256);  // (at most 64 waves per CU)
+    hipError_t e = hipMalloc(reinterpret_cast<void**>(&mem), tasks_b + ctr_b + scratch + woff_b);
     if (e != hipSuccess) return fail(XT_ERR_NOMEM, std::string("stack allocation: ") + hipGetErrorString(e));
     char* sc = mem + tasks_b + ctr_b;
 
@@ -1073,12 +1074,43 @@ int create_sstack(const xt_stack_op* ops, int nops, int mode, xt_stack** out) {
         for (int k = i + 1; k < nops; ++k)
             if (ops[k].dep == i) quant_task(k);
     }
-    int dev = 0, cus = 0, per_cu = 0;
-    e = hipGetDevice(&dev);
-    if (e == hipSuccess) e = hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    if (e == hipSuccess) e = xt::sstack_blocks_per_cu(&per_cu);
+    // Every wave resident at once (see xtern_sstack.hip): at most the
+    // occupancy, and four workgroups per CU (16 waves) stream best.
+    const int wpb = xt::sstack_waves_per_block();
+    int per_cu = 0;
+    int row_bytes = 1024;
+    for (const OpInfo& f : info) row_bytes = std::max(row_bytes, (int)align_up((size_t)f.ldq, 1024));
+    e = xt::sstack_blocks_per_cu(row_bytes, &per_cu);
     if (e == hipSuccess && per_cu < 1) e = hipErrorInvalidConfiguration;
-    if (e == hipSuccess) e = hipMemcpy(mem, tasks.data(), tasks.size() * sizeof(xt::SStackTask), hipMemcpyHostToDevice);
+    const int grid = std::max(1, std::min(cus0 * std::min(per_cu, 4), ((int)tasks.size() + wpb - 1) / wpb));
+    const int nw = grid * wpb;
+    // deal the list out: each task, in list order, to the wave with the least
+    // weight bytes so far (a task's start costs about 4 KiB of streaming)
+    std::vector<std::vector<int>> per((size_t)nw);
+    {
+        typedef std::pair<double, int> Slot;
+        std::vector<Slot> heap;
+        for (int w = 0; w < nw; ++w) heap.push_back(Slot(0.0, w));
+        auto later = [](const Slot& x, const Slot& y) { return x > y; };
+        std::make_heap(heap.begin(), heap.end(), later);
+        for (size_t t = 0; t < tasks.size(); ++t) {
+            const xt::SStackTask& k = tasks[t];
+            const double cost = 4096.0 + ((k.flags & 1) ? 8.0 * k.K : 1024.0 * k.nch * (k.flags >> 16));
+            std::pop_heap(heap.begin(), heap.end(), later);
+            per[(size_t)heap.back().second].push_back((int)t);
+            heap.back().first += cost;
+            std::push_heap(heap.begin(), heap.end(), later);
+        }
+    }
+    std::vector<xt::SStackTask> dealt;
+    dealt.reserve(tasks.size());
+    std::vector<int> woff((size_t)nw + 1, 0);
+    for (int w = 0; w < nw; ++w) {
+        for (int t : per[(size_t)w]) dealt.push_back(tasks[(size_t)t]);
+        woff[(size_t)w + 1] = (int)dealt.size();
+    }
+    if (e == hipSuccess) e = hipMemcpy(mem, dealt.data(), dealt.size() * sizeof(xt::SStackTask), hipMemcpyHostToDevice);
+    if (e == hipSuccess) e = hipMemcpy(mem + tasks_b + ctr_b + scratch, woff.data(), woff.size() * 4, hipMemcpyHostToDevice);
     if (e == hipSuccess) e = hipMemset(mem + tasks_b, 0, ctr_b + scratch);
     if (e == hipSuccess) e = hipDeviceSynchronize();
     if (e != hipSuccess) {
@@ -1090,9 +1122,6 @@ int create_sstack(const xt_stack_op* ops, int nops, int mode, xt_stack** out) {
         (void)hipFree(mem);
         return fail(XT_ERR_NOMEM, "stack handle");
     }
-    // Every wave resident at once (see xtern_sstack.hip): at most the
-    // occupancy, and four workgroups per CU (16 waves) stream best.
-    const int wpb = xt::sstack_waves_per_block();
     st->stream = true;
     st->sargs.tasks = reinterpret_cast<const xt::SStackTask*>(mem);
     st->sargs.ctr = reinterpret_cast<unsigned*>(mem + tasks_b);
@@ -1101,8 +1130,10 @@ int create_sstack(const xt_stack_op* ops, int nops, int mode, xt_stack** out) {
     st->sargs.mode = mode;
     st->sargs.spin_limit = 1 << 20;  // polls (about a microsecond each) before a wait gives up
     st->args.ctr = st->sargs.ctr;    // (the error slot, read by xt_stack_check)
-    st->blocks = std::max(1, std::min(cus * std::min(per_cu, 4), ((int)tasks.size() + wpb - 1) / wpb));
-    st->device = dev;
+    st->sargs.woff = reinterpret_cast<const int*>(mem + tasks_b + ctr_b + scratch);
+    st->sargs.row_bytes = row_bytes;
+    st->blocks = grid;
+    st->device = dev0;
     st->dev_mem = mem;
     *out = st;
     return XT_OK;

@@ -189,12 +189,14 @@ struct alignas(16) SStackTask {
 };
 static_assert(sizeof(SStackTask) == 64, "a task record is four 16-byte loads");
 struct SStackArgs {
-    const SStackTask* tasks;
+    const SStackTask* tasks;  // wave w runs tasks[woff[w] .. woff[w + 1]) in order
+    const int* woff;          // [waves + 1]
     unsigned* ctr;            // (4 + 2 * nops) slots of 128 bytes, zero between launches
     int ntasks, nops, mode, spin_limit;
+    int row_bytes;            // LDS per wave for the i8 row: the longest ldq, rounded to 1 KiB
 };
 hipError_t launch_sstack(const SStackArgs& a, int blocks, hipStream_t s);
-hipError_t sstack_blocks_per_cu(int* n);
+hipError_t sstack_blocks_per_cu(int row_bytes, int* n);
 int sstack_waves_per_block();
 // Persistent decode stack (xtern_stack.hip): one launch over a list of ops.
 constexpr int kStackRowGroupsMax = 8;       // 16-row groups per GEMV item (M > 1): stack_gemv_rg

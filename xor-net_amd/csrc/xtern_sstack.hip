@@ -10,14 +10,16 @@
 //
 // Work list.  The host flattens the ops into tasks: one quantiser task per op
 // (the op's f32 input row -> i8 row, its exact sum and inverse scale) and one
-// task per 16-row group of each of the op's projections.  Every task follows
-// the tasks it waits for: an op's quantiser task comes after the last group
-// of the op its input comes from, its groups after its quantiser task.  Wave
-// gw of the grid (TW waves) takes tasks gw, gw + TW, gw + 2 TW, ... in that
-// order; the grid is no larger than what is resident at once, so the wave
-// holding the earliest unfinished task is running and has its inputs, and
-// the launch always finishes.  Waits are bounded anyway: one that gives up
-// sets a flag for the host, and all later waits of the launch return at once.
+// task per block of consecutive 16-row groups of one projection.  Every task
+// follows the tasks it waits for: an op's quantiser task comes after the last
+// group of the op its input comes from, its groups after its quantiser task.
+// The host deals the list out to the waves in list order, each task to the
+// wave with the least work so far (weight bytes), and every wave runs its
+// tasks in list order.  The grid is no larger than what is resident at once,
+// so the wave holding the earliest unfinished task is running and has its
+// inputs, and the launch always finishes.  Waits are bounded anyway: one that
+// gives up sets a flag for the host, and all later waits of the launch return
+// at once.
 //
 // A group task streams its nch weight tiles (1 KiB each) D at a time with the
 // row's i8 pieces in the wave's own LDS region (no barrier: a wave's LDS
@@ -97,25 +99,30 @@ struct Rec {
     int8_t* q;             // the op's i8 row, then its sum and inverse scale
     int opi, flags, nch, nrows, K, ldq, dep, dep_groups, ngroups;
 };
-__device__ __forceinline__ Rec ss_rec(const SStackTask* t) {
-    const v4i* v = reinterpret_cast<const v4i*>(t);
-    const v4i a = v[0], b = v[1], c = v[2], d = v[3];
-    auto u = [](int x) { return (uint32_t)__builtin_amdgcn_readfirstlane(x); };
-    auto ptr = [&](int lo, int hi) { return (uint64_t)u(lo) | ((uint64_t)u(hi) << 32); };
+// A record is loaded one task ahead, dword k into lane k (one register),
+// and its fields are read out with readlane when its task starts (reading
+// them right after the load would wait for it there).
+__device__ __forceinline__ unsigned ss_rec_load(const SStackTask* t) {
+    const int lane = threadIdx.x & 63;
+    return reinterpret_cast<const unsigned*>(t)[lane & 15];
+}
+__device__ __forceinline__ Rec ss_rec(unsigned w) {
+    auto u = [&](int k) { return (uint32_t)__builtin_amdgcn_readlane((int)w, k); };
+    auto ptr = [&](int k) { return (uint64_t)u(k) | ((uint64_t)u(k + 1) << 32); };
     Rec r;
-    r.tiles = reinterpret_cast<const uint8_t*>(ptr(a[0], a[1]));
-    r.ws = reinterpret_cast<const float*>(ptr(a[2], a[3]));
-    r.y = reinterpret_cast<float*>(ptr(b[0], b[1]));
-    r.q = reinterpret_cast<int8_t*>(ptr(b[2], b[3]));
-    r.opi = (int)u(c[0]);
-    r.flags = (int)u(c[1]) & 0xffff;
-    r.ngroups = (int)(u(c[1]) >> 16);
-    r.nch = (int)u(c[2]);
-    r.nrows = (int)u(c[3]);
-    r.K = (int)u(d[0]);
-    r.ldq = (int)u(d[1]);
-    r.dep = (int)u(d[2]);
-    r.dep_groups = (int)u(d[3]);
+    r.tiles = reinterpret_cast<const uint8_t*>(ptr(0));
+    r.ws = reinterpret_cast<const float*>(ptr(2));
+    r.y = reinterpret_cast<float*>(ptr(4));
+    r.q = reinterpret_cast<int8_t*>(ptr(6));
+    r.opi = (int)u(8);
+    r.flags = (int)u(9) & 0xffff;
+    r.ngroups = (int)(u(9) >> 16);
+    r.nch = (int)u(10);
+    r.nrows = (int)u(11);
+    r.K = (int)u(12);
+    r.ldq = (int)u(13);
+    r.dep = (int)u(14);
+    r.dep_groups = (int)u(15);
     return r;
 }
 
@@ -322,19 +329,20 @@ __device__ void ss_block(const SStackArgs& a, const Rec& r, uint32_t areg, unsig
 
 __global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) void sstack_kernel(const SStackArgs a) {
     __shared__ unsigned known[kSsKnownWords];  // ops this workgroup has seen quantised
-    __shared__ __align__(16) uint8_t rows[kSsW][kSStackMaxRowBytes];
+    extern __shared__ __align__(16) uint8_t rows[];  // [kSsW][a.row_bytes]: each wave's i8 row
     for (int i = threadIdx.x; i < kSsKnownWords; i += kSsW * 64) known[i] = 0u;
     __syncthreads();
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int TW = gridDim.x * kSsW;
     const int gw = blockIdx.x * kSsW + wave;
-    const uint32_t areg = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)rows[wave];
+    const uint32_t areg = (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) void*)(rows + wave * a.row_bytes);
     // each task's record is loaded one task ahead
-    Rec nxt;
-    if (gw < a.ntasks) nxt = ss_rec(a.tasks + gw);
-    for (int t = gw; t < a.ntasks; t += TW) {
-        const Rec cur = nxt;
-        if (t + TW < a.ntasks) nxt = ss_rec(a.tasks + t + TW);
+    const int t0 = a.woff[gw], t1 = a.woff[gw + 1];
+    unsigned nxt = 0;
+    if (t0 < t1) nxt = ss_rec_load(a.tasks + t0);
+    for (int t = t0; t < t1; ++t) {
+        const Rec cur = ss_rec(nxt);
+        if (t + 1 < t1) nxt = ss_rec_load(a.tasks + t + 1);
         if (cur.flags & kSsQuant) {
             if (a.mode == XT_QUANT_AVX512) ss_quant<XT_QUANT_AVX512>(a, cur);
             else ss_quant<XT_QUANT_SCALAR>(a, cur);
@@ -359,14 +367,18 @@ __global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(4, 4)
 
 }  // namespace
 
+// LDS beyond the static part: every wave's i8 row region (the stack's
+// longest row, rounded to 1 KiB).
+static size_t ss_dyn_lds(int row_bytes) { return (size_t)kSsW * row_bytes; }
+
 hipError_t launch_sstack(const SStackArgs& a, int blocks, hipStream_t s) {
-    hipLaunchKernelGGL(sstack_kernel, dim3(blocks), dim3(kSsW * 64), 0, s, a);
+    hipLaunchKernelGGL(sstack_kernel, dim3(blocks), dim3(kSsW * 64), ss_dyn_lds(a.row_bytes), s, a);
     return hipGetLastError();
 }
 
-hipError_t sstack_blocks_per_cu(int* n) {
+hipError_t sstack_blocks_per_cu(int row_bytes, int* n) {
     return hipOccupancyMaxActiveBlocksPerMultiprocessor(n, reinterpret_cast<const void*>(sstack_kernel),
-                                                        kSsW * 64, 0);
+                                                        kSsW * 64, ss_dyn_lds(row_bytes));
 }
 
 int sstack_waves_per_block() { return kSsW; }
