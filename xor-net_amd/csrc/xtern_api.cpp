@@ -1019,7 +1019,8 @@ int create_sstack(const xt_stack_op* ops, int nops, int mode, xt_stack** out) {
     XT_HIP(hipDeviceGetAttribute(&cus0, hipDeviceAttributeMultiprocessorCount, dev0));
     size_t all_groups = 0;
     for (const OpInfo& f : info) all_groups += (size_t)f.ngroups;
-    const int rg = (int)std::max<size_t>(1, std::min<size_t>(8, all_groups / ((size_t)cus0 * 16 * 4)));
+    // (at most 4: a task's rows are one per lane of a wave)
+    const int rg = (int)std::max<size_t>(1, std::min<size_t>(4, all_groups / ((size_t)cus0 * 16 * 4)));
     ntasks = nops;
     for (int i = 0; i < nops; ++i)
         for (int p = 0; p < ops[i].n; ++p) ntasks += (size_t)(((ops[i].w[p]->N + 15) / 16 + rg - 1) / rg);

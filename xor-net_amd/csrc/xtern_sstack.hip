@@ -87,6 +87,17 @@ __device__ __forceinline__ void ss_wait(unsigned* c, unsigned target, unsigned* 
     }
 }
 
+// Pointers read from a task record are generic; loads and stores through
+// them are given the global address space explicitly, so they are not flat
+// accesses (a flat access counts against the LDS wait counter too, and every
+// LDS read of the wave would then wait for the weight loads in flight).
+typedef __attribute__((address_space(1))) const v4i gv4i;
+typedef __attribute__((address_space(1))) const float gfloat;
+typedef __attribute__((address_space(1))) float gfloat_w;
+__device__ __forceinline__ v4i ss_ld_tile(const uint8_t* p) {
+    return __builtin_nontemporal_load((gv4i*)(uintptr_t)p);
+}
+
 __device__ __forceinline__ v4i ss_lds16(uint32_t addr) {
     return *reinterpret_cast<const __attribute__((address_space(3))) v4i*>((uintptr_t)addr);
 }
@@ -232,11 +243,15 @@ __device__ void ss_block(const SStackArgs& a, const Rec& r, uint32_t areg, unsig
         inv = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(qr, (unsigned)r.ldq + 4u, 0, kSsCoh));
     };
     load_row();
-    float wsc = r.ws[j];
+    // lane l holds row l of the task (group l / 16): its w_scale now, its dot
+    // once that group is done; the outputs are stored together at the end
+    const int trows = (r.ngroups - 1) * 16 + r.nrows;
+    const float wsc = ((gfloat*)(uintptr_t)r.ws)[min(lane, trows - 1)];
+    int dot = 0;
     v4i wb[kSsD];
 #pragma unroll
     for (int s = 0; s < kSsD; ++s)
-        wb[s] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(tl + (size_t)min(s, nch - 1) * kTileBytes));
+        wb[s] = ss_ld_tile(tl + (size_t)min(s, nch - 1) * kTileBytes);
     if (!seen) {
         if (ready < 1u) {  // (uniform) not quantised yet: wait, then load the row again
             if (lane == 0) ss_wait(qdone, 1u, ss_ctr(a.ctr, kSsError), a.spin_limit);
@@ -259,12 +274,10 @@ __device__ void ss_block(const SStackArgs& a, const Rec& r, uint32_t areg, unsig
 
     for (int gi = 0; gi < r.ngroups; ++gi) {
         const uint8_t* const tg = tl + (size_t)gi * nch * kTileBytes;
-        if (gi > 0) {  // (the first group's scale and first tiles came with the row)
-            wsc = r.ws[gi * 16 + j];
+        if (gi > 0) {  // (the first group's tiles came with the row)
 #pragma unroll
             for (int s = 0; s < kSsD; ++s)
-                wb[s] = __builtin_nontemporal_load(
-                    reinterpret_cast<const v4i*>(tg + (size_t)min(s, nch - 1) * kTileBytes));
+                wb[s] = ss_ld_tile(tg + (size_t)min(s, nch - 1) * kTileBytes);
         }
         v4i acc[STEPS];
 #pragma unroll
@@ -273,8 +286,7 @@ __device__ void ss_block(const SStackArgs& a, const Rec& r, uint32_t areg, unsig
             if (t0 > 0) {
 #pragma unroll
                 for (int s = 0; s < kSsD; ++s)
-                    wb[s] = __builtin_nontemporal_load(
-                        reinterpret_cast<const v4i*>(tg + (size_t)min(t0 + s, nch - 1) * kTileBytes));
+                    wb[s] = ss_ld_tile(tg + (size_t)min(t0 + s, nch - 1) * kTileBytes);
             }
 #pragma unroll
             for (int s = 0; s < kSsD; ++s) {
@@ -309,15 +321,17 @@ __device__ void ss_block(const SStackArgs& a, const Rec& r, uint32_t areg, unsig
         int sum = acc[0][0];
 #pragma unroll
         for (int st = 1; st < STEPS; ++st) sum += acc[st][0];
-        // token 0 sits in element 0 of the lanes with g == 0; the MFMAs took
-        // codes w + 1, so the row's sum comes off (layers.rs:340:
-        // (dot as f32 * inv) * w_scale)
-        const int nrows = gi + 1 == r.ngroups ? r.nrows : 16;
-        if (g == 0 && j < nrows) {
-            const float v = __fmul_rn(__fmul_rn((float)(sum - rsum), inv), wsc);
-            if (pub) ss_st_coh4(ss_rsrc(r.y, (unsigned)r.ngroups * 64u), (unsigned)(gi * 16 + j) * 4u, __float_as_uint(v));
-            else r.y[gi * 16 + j] = v;
-        }
+        // token 0 sits in element 0 of lanes 0-15 (row j); lane l takes row
+        // l % 16 of group l / 16
+        const int v = __builtin_amdgcn_ds_bpermute((lane & 15) << 2, sum);
+        if ((lane >> 4) == gi) dot = v;
+    }
+    // the MFMAs took codes w + 1, so the row's sum comes off
+    // (layers.rs:340: (dot as f32 * inv) * w_scale)
+    if (lane < trows) {
+        const float v = __fmul_rn(__fmul_rn((float)(dot - rsum), inv), wsc);
+        if (pub) ss_st_coh4(ss_rsrc(r.y, (unsigned)trows * 4u), (unsigned)lane * 4u, __float_as_uint(v));
+        else ((gfloat_w*)(uintptr_t)r.y)[lane] = v;
     }
     if (pub) {  // another op reads these outputs inside the launch
         __builtin_amdgcn_s_waitcnt(0);
