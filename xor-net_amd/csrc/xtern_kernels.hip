@@ -18,13 +18,7 @@
 #include "xtern_internal.h"
 #include "xtern_device.h"
 
-// XT_ABLATE (0 in the library) lets a timing harness compile the prefill
-// GEMM with parts removed: 1 = no weight loads, 2 = no activation loads,
-// 4 = no MFMA phase, 8 = no output stores, 16 = no LDS staging stores.
-// Outputs are meaningless when it is non-zero.
-#ifndef XT_ABLATE
-#define XT_ABLATE 0
-#endif
+
 
 namespace xt {
 
@@ -1420,7 +1414,7 @@ __global__ __launch_bounds__(256 * KG) void gemm_kernel(const MMArgs a) {
         for (int nb = 0; nb < NBW; ++nb) {
             const int cc = kgrp + KG * u;
             const int G = gbase + nb;
-            wv[u][nb] = (!(XT_ABLATE & 1) && cc < nc && G < NG)
+            wv[u][nb] = (cc < nc && G < NG)
                             ? *reinterpret_cast<const v4i*>(tiles + ((size_t)(G * nch + cbeg + cc) * 64 + lane) * 16)
                             : v4i{0, 0, 0, 0};
         }
@@ -1462,13 +1456,13 @@ __global__ __launch_bounds__(256 * KG) void gemm_kernel(const MMArgs a) {
         const int cs = blk / MB;                // cc * STEPS + st
         const int row = mbase + mb * 16 + (ln & 15);
         stage[r] = v4i{0, 0, 0, 0};
-        if (!(XT_ABLATE & 2) && p < pieces && row < M)
+        if (p < pieces && row < M)
             stage[r] = ld_cached(a.q + (size_t)row * a.ldq + (size_t)cbeg * CH + cs * 64 + (ln >> 4) * 16);
     }
 #pragma unroll
     for (int r = 0; r < PPT; ++r) {
         const int p = threadIdx.x + r * NT;
-        if (!(XT_ABLATE & 16) && p < pieces) *reinterpret_cast<v4i*>(lds_a + ((size_t)p << 4)) = stage[r];
+        if (p < pieces) *reinterpret_cast<v4i*>(lds_a + ((size_t)p << 4)) = stage[r];
     }
     __syncthreads();
 
@@ -1489,7 +1483,7 @@ __global__ __launch_bounds__(256 * KG) void gemm_kernel(const MMArgs a) {
 
 #pragma unroll
     for (int u = 0; u < NCW; ++u) {
-        if (!(XT_ABLATE & 4) && kgrp + KG * u < nc) {
+        if (kgrp + KG * u < nc) {
             int E[NBW][4], O[NBW][4];
             if constexpr (FMT == XT_PACK5) {
 #pragma unroll
@@ -1571,7 +1565,6 @@ __global__ __launch_bounds__(256 * KG) void gemm_kernel(const MMArgs a) {
         }
     }
     __syncthreads();
-    if (XT_ABLATE & 8) return;
     const int obase = (bx - tile0) * 128;
     int32_t* plane = a.part + (size_t)bz * a.M * a.ldp;
     const bool vec = (N & 3) == 0;

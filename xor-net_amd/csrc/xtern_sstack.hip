@@ -226,12 +226,16 @@ __device__ void ss_block(const SStackArgs& a, const Rec& r, uint32_t areg, unsig
     unsigned* const qdone = ss_ctr(a.ctr, kSsDone0 + a.nops + opi);
     const bool seen = (known[opi >> 5] >> (opi & 31)) & 1u;
 
-    // the loads that start the block, issued together (the count first)
-    const unsigned ready = seen ? 1u : ss_ld_coh(qdone);
+    // the loads that start the block, issued together (the count first).
+    // Values every lane needs (the count, the row's sum and scale) are loaded
+    // by one or two lanes and broadcast: device-scope loads bypass the
+    // per-CU cache, so 64 lanes loading one word would send 64 requests
+    // to one L2 line.
     const __amdgpu_buffer_rsrc_t qr = ss_rsrc(r.q, (unsigned)(r.ldq + 8));
+    unsigned ready = 1u;
+    if (!seen && lane == 0) ready = ss_ld_coh(qdone);
     v4i pc[kPieces];
-    int rsum;
-    float inv;
+    unsigned ri = 0;  // lane 0: the row's sum, lane 1: its inverse scale
     auto load_row = [&]() {
 #pragma unroll
         for (int u = 0; u < kPieces; ++u) {
@@ -239,8 +243,7 @@ __device__ void ss_block(const SStackArgs& a, const Rec& r, uint32_t areg, unsig
             if (64 * u < npieces)  // (uniform)
                 pc[u] = ss_ld_coh16(qr, i < npieces ? (unsigned)i * 16u : 0x80000000u);
         }
-        rsum = (int)__builtin_amdgcn_raw_buffer_load_b32(qr, (unsigned)r.ldq, 0, kSsCoh);
-        inv = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(qr, (unsigned)r.ldq + 4u, 0, kSsCoh));
+        if (lane < 2) ri = (unsigned)__builtin_amdgcn_raw_buffer_load_b32(qr, (unsigned)(r.ldq + 4 * lane), 0, kSsCoh);
     };
     load_row();
     // lane l holds row l of the task (group l / 16): its w_scale now, its dot
@@ -253,6 +256,7 @@ __device__ void ss_block(const SStackArgs& a, const Rec& r, uint32_t areg, unsig
     for (int s = 0; s < kSsD; ++s)
         wb[s] = ss_ld_tile(tl + (size_t)min(s, nch - 1) * kTileBytes);
     if (!seen) {
+        ready = __builtin_amdgcn_readfirstlane(ready);
         if (ready < 1u) {  // (uniform) not quantised yet: wait, then load the row again
             if (lane == 0) ss_wait(qdone, 1u, ss_ctr(a.ctr, kSsError), a.spin_limit);
             __builtin_amdgcn_wave_barrier();
@@ -260,6 +264,8 @@ __device__ void ss_block(const SStackArgs& a, const Rec& r, uint32_t areg, unsig
         }
         if (lane == 0) atomicOr(&known[opi >> 5], 1u << (opi & 31));
     }
+    const int rsum = __builtin_amdgcn_readlane((int)ri, 0);
+    const float inv = __int_as_float(__builtin_amdgcn_readlane((int)ri, 1));
     // the row into this wave's LDS region (its own LDS accesses complete in
     // order: the reads below see these stores, and the previous task's reads
     // came before them)
@@ -341,7 +347,7 @@ __device__ void ss_block(const SStackArgs& a, const Rec& r, uint32_t areg, unsig
     }
 }
 
-__global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(4, 4))) void sstack_kernel(const SStackArgs a) {
+__global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(4))) void sstack_kernel(const SStackArgs a) {
     __shared__ unsigned known[kSsKnownWords];  // ops this workgroup has seen quantised
     extern __shared__ __align__(16) uint8_t rows[];  // [kSsW][a.row_bytes]: each wave's i8 row
     for (int i = threadIdx.x; i < kSsKnownWords; i += kSsW * 64) known[i] = 0u;
