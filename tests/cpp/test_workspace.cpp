@@ -208,7 +208,60 @@ static void test_stress_ownership() {
     CHECK(!g_double_free, "no double free");
 }
 
+// A thread that ends hands its buffers on: the next new thread adopts them
+// (after one device synchronize) instead of allocating, so threads started
+// and ended one after another hold one buffer per kind in all.
+static void test_ended_threads_hand_buffers_on() {
+    xt::WorkspaceTable t(backend());
+    void* s = (void*)0x70;
+    const int a0 = g_allocs, s0 = g_syncs;
+    for (int i = 0; i < 20; ++i) {
+        std::thread th([&, i] {
+            std::string e;
+            void *p = nullptr, *q = nullptr;
+            CHECK(t.get(s, 1000 + i, 0, false, &p, &e) == 0, "get kind 0");
+            CHECK(t.get(s, 2000, 2, false, &q, &e) == 0, "get kind 2");
+            CHECK(p != q, "kinds differ");
+            t.thread_exit(std::this_thread::get_id());  // (the library's thread_local guard)
+        });
+        th.join();
+        CHECK(t.live_count() == 0 && t.pooled_count() == 2, "pooled after exit (round %d)", i);
+    }
+    CHECK(g_allocs == a0 + 2, "two allocations for 20 threads (got %d)", (int)(g_allocs - a0));
+    CHECK(g_syncs >= s0 + 38, "each adoption synchronised");
+    // a larger request does not take a pooled buffer that is too small
+    std::thread th([&] {
+        std::string e;
+        void* p = nullptr;
+        CHECK(t.get(s, 8u << 20, 0, false, &p, &e) == 0 && size_of(p) >= (8u << 20), "large");
+        t.thread_exit(std::this_thread::get_id());
+    });
+    th.join();
+    CHECK(t.pooled_count() == 3, "both sizes pooled");
+    // stale kind-1 buffers are never adopted
+    std::thread th1([&] {
+        std::string e;
+        void* p = nullptr;
+        CHECK(t.get(s, 1000, 1, true, &p, &e) == 0, "kind 1");
+        t.thread_exit(std::this_thread::get_id());
+    });
+    th1.join();
+    t.mark_stale(1);
+    const int a1 = g_allocs;
+    std::thread th2([&] {
+        std::string e;
+        void* p = nullptr;
+        CHECK(t.get(s, 1000, 1, true, &p, &e) == 0, "kind 1 again");
+    });
+    th2.join();
+    CHECK(g_allocs == a1 + 1, "stale pooled kind-1 buffer not adopted");
+    std::string e;
+    CHECK(t.release_all(&e) == 0 && t.pooled_count() == 0, "release frees the pool");
+    CHECK(!g_double_free, "no double free");
+}
+
 int main() {
+    test_ended_threads_hand_buffers_on();
     test_two_threads_one_stream();
     test_growth_retires();
     test_capture_never_allocates();

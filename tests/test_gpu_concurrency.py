@@ -81,3 +81,39 @@ def test_threads_share_one_stream(name, fmt, K, N, M):
             if not np.array_equal(y.view(np.int32), want[i].view(np.int32)):
                 bad.append((i, r, int((y != want[i]).sum())))
     assert not bad, f"(thread, round, differing outputs): {bad[:8]}"
+
+
+def test_short_lived_threads_one_after_another():
+    """A server that starts a thread per request (server/main.rs:589-676):
+    30 short-lived threads, each making calls of growing size on a shared
+    stream and ending.  Every output equals the oracle's; the library hands
+    an ended thread's workspace to the next thread (xtern_workspace.h)."""
+    log("short-lived threads")
+    rng = np.random.default_rng(7)
+    K, N = 2560, 640
+    t = tern(rng, N, K)
+    wb = np.concatenate([xtern.pack_ternary4(r) for r in t])
+    ws = rng.uniform(0.5, 1.5, N).astype(np.float32)
+    w = xtern.DeviceWeights(xtern.XT_PACK4, K, N, wb, ws)
+    stream = torch.cuda.Stream()
+    errors = []
+    for i in range(30):
+        M = 2 + (i % 7) * 5
+        x = rng.standard_normal((M, K)).astype(np.float32)
+        want = oracle.linear_forward(0, K, N, x, ws, wbytes=wb)[0]
+        xd = torch.from_numpy(x).cuda()
+        torch.cuda.synchronize()
+        out = {}
+
+        def body():
+            with torch.cuda.stream(stream):
+                out["y"] = xtern.linear_f32(w, xd, stream=stream)
+            stream.synchronize()
+
+        th = threading.Thread(target=body)
+        th.start()
+        th.join()
+        got = out["y"].cpu().numpy()
+        if not np.array_equal(got.view(np.int32), want.view(np.int32)):
+            errors.append(i)
+    assert not errors, f"threads {errors} produced wrong outputs"

@@ -13,6 +13,7 @@
 #include <map>
 #include <mutex>
 #include <string>
+#include <thread>
 #include <tuple>
 #include <utility>
 #include <vector>
@@ -84,6 +85,13 @@ xt::WorkspaceTable& ws_table() {
     return *t;  // (left to process teardown: HIP may be gone by static destruction)
 }
 
+// Hands the calling thread's buffers to the table's pool when the thread
+// ends (constructed on a thread's first workspace request).
+struct WsThreadGuard {
+    ~WsThreadGuard() { ws_table().thread_exit(std::this_thread::get_id()); }
+};
+thread_local WsThreadGuard g_ws_thread_guard;
+
 int ws_status(int st, const std::string& err) {
     switch (st) {
         case xt::WorkspaceTable::kOk: return XT_OK;
@@ -116,6 +124,7 @@ int workspace(hipStream_t s, size_t bytes, void** out, int kind = 0, Scratch* sc
         sc->used += need;
         return XT_OK;
     }
+    (void)&g_ws_thread_guard;  // (constructs this thread's guard)
     std::string err;
     const int st = ws_table().get(s, bytes, kind, kind == 1, out, &err);
     return ws_status(st, err);

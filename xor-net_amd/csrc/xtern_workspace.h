@@ -16,6 +16,14 @@
 // doubles the capacity, so the retired buffers together stay below the live
 // one.
 //
+// A host thread that ends hands its buffers to a pool (thread_exit, called
+// from a thread_local guard in the library).  A (device, stream, thread,
+// kind) that needs its first buffer adopts a pooled one of the same device
+// and kind that is large enough, after one device synchronize (the ended
+// thread's launches may still be queued), instead of allocating.  So a host
+// that spawns short-lived threads holds at most as many buffers per kind as
+// it has threads calling at the same time, not one per thread ever started.
+//
 // While the stream is being captured into a graph the table never allocates
 // (no allocation, memset or synchronisation may enter a capture): a request
 // that fits the existing buffer is served, one that would grow it fails with
@@ -73,6 +81,19 @@ public:
                    "of the largest shape on this stream and thread before capturing";
             return kCapture;
         }
+        if (!w.ptr) {  // a first buffer for this key: adopt a pooled one
+            for (size_t i = 0; i < pool_.size(); ++i) {
+                const Pooled& pb = pool_[i];
+                if (pb.dev != dev || pb.kind != kind || pb.stale || pb.cap < bytes) continue;
+                if (int e = b_.device_sync()) return backend_fail(e, "device synchronize", err);
+                w.ptr = pb.ptr;
+                w.cap = pb.cap;
+                w.stale = false;
+                pool_.erase(pool_.begin() + (ptrdiff_t)i);
+                *out = w.ptr;
+                return kOk;
+            }
+        }
         size_t cap = w.cap * 2;
         if (cap < bytes) cap = bytes;
         if (cap < kMinBytes) cap = kMinBytes;
@@ -103,6 +124,23 @@ public:
         std::lock_guard<std::mutex> lk(mu_);
         for (auto& kv : table_)
             if (std::get<3>(kv.first) == kind) kv.second.stale = true;
+        for (Pooled& pb : pool_)
+            if (pb.kind == kind) pb.stale = true;
+    }
+
+    // The calling thread `id` ends: its buffers go to the pool.
+    void thread_exit(std::thread::id id) {
+        std::lock_guard<std::mutex> lk(mu_);
+        for (auto it = table_.begin(); it != table_.end();) {
+            if (std::get<2>(it->first) == id) {
+                if (it->second.ptr)
+                    pool_.push_back(Pooled{std::get<0>(it->first), std::get<3>(it->first), it->second.ptr,
+                                           it->second.cap, it->second.stale});
+                it = table_.erase(it);
+            } else {
+                ++it;
+            }
+        }
     }
 
     // Wait for the device, then free every buffer (live and retired).  The
@@ -115,8 +153,11 @@ public:
             if (kv.second.ptr && b_.free_(kv.second.ptr)) rc = kBackend;
         for (void* p : retired_)
             if (b_.free_(p)) rc = kBackend;
+        for (const Pooled& pb : pool_)
+            if (b_.free_(pb.ptr)) rc = kBackend;
         table_.clear();
         retired_.clear();
+        pool_.clear();
         if (rc) *err = "workspace free failed";
         return rc;
     }
@@ -131,6 +172,10 @@ public:
         std::lock_guard<std::mutex> lk(mu_);
         return retired_.size();
     }
+    size_t pooled_count() {
+        std::lock_guard<std::mutex> lk(mu_);
+        return pool_.size();
+    }
 
     static constexpr size_t kMinBytes = (size_t)1 << 20;
 
@@ -141,6 +186,12 @@ private:
         bool stale = false;
     };
     typedef std::tuple<int, void*, std::thread::id, int> Key;
+    struct Pooled {
+        int dev, kind;
+        void* ptr;
+        size_t cap;
+        bool stale;
+    };
 
     int backend_fail(int e, const char* what, std::string* err) {
         *err = std::string(what) + ": " + b_.error_string(e);
@@ -151,6 +202,7 @@ private:
     std::mutex mu_;
     std::map<Key, Entry> table_;
     std::vector<void*> retired_;
+    std::vector<Pooled> pool_;  // buffers of threads that have ended
 };
 
 }  // namespace xt
