@@ -35,8 +35,6 @@ namespace xt {
 
 namespace {
 
-constexpr int kXsWaves = 16;
-constexpr int kXsThreads = kXsWaves * 64;
 constexpr unsigned kXsOOR = 0x80000000u;  // an offset past every section
 
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t xs_rsrc(const void* p, unsigned bytes) {
@@ -49,11 +47,17 @@ __device__ __forceinline__ v4i xs_ld128(__amdgpu_buffer_rsrc_t r, unsigned off) 
     return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
 }
 
-// MT: token rows per launch (1, 4 or 16; M <= MT); NIT: block quads per wave.
-template <int MT, int NIT>
-__global__ __launch_bounds__(kXsThreads) void xs_gemv_kernel(const XsArgs a) {
+// MT: token rows per launch (1, 4 or 16; M <= MT); NIT: block quads per
+// wave; W: waves per workgroup.
+template <int MT, int NIT, int W>
+__global__ __launch_bounds__(W * 64) void xs_gemv_kernel(const XsArgs a) {
+    constexpr int kXsWaves = W;
     __shared__ unsigned table[256];
     __shared__ int red[kXsWaves][MT][16];
+    // MT > 1: per wave, the quad's expanded weights [block][row][16-byte
+    // piece] and activation rows [token][piece] (one piece of padding per row)
+    __shared__ v4i wsl[MT > 1 ? kXsWaves : 1][4][16][4];
+    __shared__ v4i asl[MT > 1 ? kXsWaves : 1][16][17];
     const int t = threadIdx.x, lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int j = lane & 15, bq = lane >> 4;
@@ -122,9 +126,10 @@ __global__ __launch_bounds__(kXsThreads) void xs_gemv_kernel(const XsArgs a) {
     __syncthreads();  // the table
 
     // phase 3: expand and multiply
-    int acc[MT];
-#pragma unroll
-    for (int m = 0; m < MT; ++m) acc[m] = 0;
+    int acc[MT == 1 ? 1 : 1];
+    acc[0] = 0;
+    v4i macc = v4i{0, 0, 0, 0};  // MT > 1: tokens 4g..4g+3 of row (lane & 15)
+    const int g = lane >> 4;
 #pragma unroll
     for (int it = 0; it < NIT; ++it) {
         const unsigned S0 = __builtin_amdgcn_alignbit(w1[it], w0[it], sh[it]);
@@ -147,32 +152,44 @@ __global__ __launch_bounds__(kXsThreads) void xs_gemv_kernel(const XsArgs a) {
                 for (int d = 0; d < 4; ++d)
                     acc[0] = __builtin_amdgcn_sdot4((int)wd[4 * u + d], x1[it][u][d], acc[0], false);
         } else {
+            // The quad's 4 x 64 columns: the expanded weights (lane order,
+            // row j of block bq) and the activation rows (4-row loads:
+            // token 4u + lane / 16, piece lane % 16) go through the wave's
+            // LDS slices, then one MFMA per block takes 16 tokens x 16 rows
+            // x 64 columns.  (A wave's LDS accesses complete in order: no
+            // barrier.)
+            const int q0 = wave + it * kXsWaves;  // the quad
+            const bool qlive = 4 * q0 < nb;
+            v4i xa[4];
 #pragma unroll
-            for (int m = 0; m < MT; ++m) {
-                if (m < M) {  // (uniform)
-                    const unsigned xo = live[it] ? (unsigned)m * (unsigned)a.ldq + (unsigned)blk[it] * 64u
-                                                 : kXsOOR;
-                    v4i x[4];
-#pragma unroll
-                    for (int u = 0; u < 4; ++u) x[u] = xs_ld128(qr, xo + 16u * u);
-                    int s = acc[m];
-#pragma unroll
-                    for (int u = 0; u < 4; ++u)
-#pragma unroll
-                        for (int d = 0; d < 4; ++d)
-                            s = __builtin_amdgcn_sdot4((int)wd[4 * u + d], x[u][d], s, false);
-                    acc[m] = s;
-                }
+            for (int u = 0; u < 4; ++u) {
+                const int m = 4 * u + (lane >> 4);
+                xa[u] = xs_ld128(qr, (qlive && m < M) ? (unsigned)m * (unsigned)a.ldq + (unsigned)q0 * 256u +
+                                                            (unsigned)(lane & 15) * 16u
+                                                      : kXsOOR);
             }
+#pragma unroll
+            for (int p = 0; p < 4; ++p)
+                wsl[wave][bq][j][p] = v4i{(int)wd[4 * p], (int)wd[4 * p + 1], (int)wd[4 * p + 2], (int)wd[4 * p + 3]};
+#pragma unroll
+            for (int u = 0; u < 4; ++u) asl[wave][4 * u + (lane >> 4)][lane & 15] = xa[u];
+            __asm__ volatile("" ::: "memory");
+#pragma unroll
+            for (int b = 0; b < 4; ++b)
+                macc = mfma(asl[wave][j][4 * b + g], wsl[wave][b][j][g], macc);
+            __asm__ volatile("" ::: "memory");
         }
     }
-    // rows: the wave's 4 block lanes, then the waves
-#pragma unroll
-    for (int m = 0; m < MT; ++m) {
-        int v = acc[m];
+    if constexpr (MT == 1) {
+        // rows: the wave's 4 block lanes, then the waves
+        int v = acc[0];
         v += __shfl_xor(v, 16);
         v += __shfl_xor(v, 32);
-        if (bq == 0) red[wave][m][j] = v;
+        if (bq == 0) red[wave][0][j] = v;
+    } else {
+        // lane (g, j): tokens 4g + r of row j
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) red[wave][4 * g + rr][j] = macc[rr];
     }
     __syncthreads();
     if (t < 16 * MT) {
@@ -190,25 +207,34 @@ __global__ __launch_bounds__(kXsThreads) void xs_gemv_kernel(const XsArgs a) {
 }
 
 template <int MT>
-hipError_t launch_mt(const XsArgs& a, int nit, hipStream_t s) {
-    const dim3 grid((unsigned)((a.N + 15) / 16)), block(kXsThreads);
-    if (nit <= 1) hipLaunchKernelGGL((xs_gemv_kernel<MT, 1>), grid, block, 0, s, a);
-    else if (nit <= 2) hipLaunchKernelGGL((xs_gemv_kernel<MT, 2>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((xs_gemv_kernel<MT, 4>), grid, block, 0, s, a);
+hipError_t launch_mt(const XsArgs& a, hipStream_t s) {
+    const dim3 grid((unsigned)((a.N + 15) / 16));
+    const int nq = (a.nb + 3) / 4;  // block quads of a row group
+    if constexpr (MT == 1) {
+        // W waves of NIT quads each: four waves while they cover the row at
+        // four quads per lane (independent items interleave in a lane), else 16
+        if (nq <= 4 * 4) hipLaunchKernelGGL((xs_gemv_kernel<1, 4, 4>), grid, dim3(256), 0, s, a);
+        else if (nq <= 16) hipLaunchKernelGGL((xs_gemv_kernel<1, 1, 16>), grid, dim3(1024), 0, s, a);
+        else if (nq <= 32) hipLaunchKernelGGL((xs_gemv_kernel<1, 2, 16>), grid, dim3(1024), 0, s, a);
+        else hipLaunchKernelGGL((xs_gemv_kernel<1, 4, 16>), grid, dim3(1024), 0, s, a);
+    } else {
+        // 8 waves (LDS slices of 8.3 KiB each)
+        if (nq <= 8) hipLaunchKernelGGL((xs_gemv_kernel<MT, 1, 8>), grid, dim3(512), 0, s, a);
+        else if (nq <= 16) hipLaunchKernelGGL((xs_gemv_kernel<MT, 2, 8>), grid, dim3(512), 0, s, a);
+        else if (nq <= 32) hipLaunchKernelGGL((xs_gemv_kernel<MT, 4, 8>), grid, dim3(512), 0, s, a);
+        else hipLaunchKernelGGL((xs_gemv_kernel<MT, 8, 8>), grid, dim3(512), 0, s, a);
+    }
     return hipGetLastError();
 }
 
 }  // namespace
 
-int xs_max_blocks() { return 4 * 4 * kXsWaves; }
+int xs_max_blocks() { return 4 * 4 * 16; }  // (M > 1: 8 waves x 8 quads x 4)
 int xs_max_rows() { return 16; }
 
 hipError_t launch_xs_gemv(const XsArgs& a, hipStream_t s) {
-    const int nq = (a.nb + 3) / 4;
-    const int nit = (nq + kXsWaves - 1) / kXsWaves;
-    if (a.M <= 1) return launch_mt<1>(a, nit, s);
-    if (a.M <= 4) return launch_mt<4>(a, nit, s);
-    return launch_mt<16>(a, nit, s);
+    if (a.M <= 1) return launch_mt<1>(a, s);
+    return launch_mt<16>(a, s);
 }
 
 }  // namespace xt
