@@ -376,16 +376,18 @@ def stack_c4(np, torch, xtern, rng, Ms=(1, 8, 32), layers=30):
     """the BitNet-2B decode-step linear stack, 30 layers
     x {q, k, v, o, gate, up, down}, f32 activations (q/k/v and gate/up share
     one quantised input, as fused_forward_qkv / _mlp).  Weights are distinct
-    device buffers (521 MB, > 2x the MALL).  Three ways, same weights:
+    device buffers (521 MB, > 2x the MALL).  Four ways, same weights:
       per_call       one library call per op (120 calls), one HIP graph per stack;
-      residual_only  the projection stack (xt_stack_*) as ONE launch with only
-                     the residual dependency: layer L's q/k/v and gate/up read
-                     layer L-1's down output; o and down read inputs that are
-                     ready before the launch;
-      chain          ONE launch of the strict chain q/k/v -> o -> gate/up ->
-                     down -> next layer, each op reading the previous op's
-                     raw output (no norm / attention / activation in between:
-                     the library runs none of those inside a launch).
+      residual_only  the projection stack (xt_stack_*) with only the residual
+                     dependency: layer L's q/k/v and gate/up read layer
+                     L-1's down output; o and down read inputs that are
+                     ready before the run (the library runs it in one launch);
+      chain          the strict chain q/k/v -> o -> gate/up -> down -> next
+                     layer, each op reading the previous op's raw output (no
+                     norm / attention / activation in between: the library
+                     runs none of those), in the plan the library picks (one
+                     call per op: 120 dependency levels);
+      chain_one_launch  the same chain forced into one persistent launch.
     The persistent outputs are checked bit-exact against the per-call ones."""
     shapes = {"q": (2560, 2560), "k": (2560, 640), "v": (2560, 640), "o": (2560, 2560),
               "gate": (2560, 6912), "up": (2560, 6912), "down": (6912, 2560)}
@@ -460,8 +462,13 @@ def stack_c4(np, torch, xtern, rng, Ms=(1, 8, 32), layers=30):
                 prev_h, prev_dep = o["down"], len(ops) - 1
             return ops
 
-        for tag, ops in (("residual_only", ops_residual_only()), ("chain", ops_chain())):
-            st = xtern.Stack(ops, M)
+        # plan None: the library's choice (the chain runs per op, the
+        # residual-only list in one launch); chain_one_launch forces the
+        # chain into one launch, to show what its dependencies cost there
+        for tag, ops, plan in (("residual_only", ops_residual_only(), None), ("chain", ops_chain(), None),
+                               ("chain_one_launch", ops_chain(), "one_launch")):
+            st = xtern.Stack(ops, M, plan=plan)
+            row[f"{tag}_plan"] = st.plan_name
             gs = Graph(torch, lambda _i: st.run(), 1)
             us_p = gs.time_ms(10) * 1e3
             if st.gave_up():
@@ -484,7 +491,7 @@ def stack_c4(np, torch, xtern, rng, Ms=(1, 8, 32), layers=30):
                         f"{tag}_hbm_frac": round(wbytes / (us_p * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                         f"{tag}_TOPS": round(ops1 * M / (us_p * 1e-6) / 1e12, 2)})
             del gs, st
-        row["persistent_checked"] = "bit-exact vs per-call outputs (both dependency shapes)"
+        row["persistent_checked"] = "bit-exact vs per-call outputs (every dependency shape and plan)"
         res.append(row)
         del outs, xo, xdl
         torch.cuda.empty_cache()

@@ -338,26 +338,38 @@ int xt_ternary_mlp_f32(const xt_weights* gate, const xt_weights* up, const xt_we
                        const float* norm_weight, float eps, int use_silu, const float* x,
                        int64_t M, float* y, int mode, void* stream);
 
-/* ---- Decode stack: a whole list of projections in one launch ----
+/* ---- Decode stack: a whole list of projections, planned once ----
  * The decode step of the reference runs its layers' projections one call
  * after the other (src/models/llama/mod.rs:420-470: per layer
  * fused_forward_qkv, o, fused_forward_mlp / gate+up, down; the next block's
  * weights prefetched while the current one computes, :446-453).  A stack
- * holds such a list and runs it as ONE persistent launch in which workgroups
- * stream the weights of the next projections while earlier ones finish.
- * Every output is bit-identical to xt_ternary_linear_f32 /
- * xt_ternary_linear_multi_f32 of the same op.
+ * holds such a list and runs it in one of two plans:
+ *   XT_STACK_ONE_LAUNCH  ONE persistent launch in which the waves stream the
+ *                        weights of later projections while earlier ones
+ *                        finish (dependencies are kept inside the launch);
+ *   XT_STACK_PER_OP      one library call per op in dependency order (a
+ *                        dependency is then a kernel boundary).
+ * xt_stack_create picks the faster plan for the list unless mode carries one
+ * of the flags: a dependency kept inside a launch costs about 20 us here
+ * against a few us for a kernel boundary, so long chains run per op and
+ * wide lists (many ops per dependency level) in one launch.  Every output is
+ * bit-identical to xt_ternary_linear_f32 / xt_ternary_linear_multi_f32 of
+ * the same op in both plans.
  *
  * One op: n (1..4) projections that share one f32 input x [M][in_dim]
- * (same in_dim, Pack4 or XorSparse weights, in_dim a multiple of 4, at most
- * 8192), outputs y[p] [M][out_dim(p)].  dep: index of an EARLIER op whose
- * outputs this op's x reads (x is then one of that op's y buffers, written
- * inside the launch), or -1 when x is ready before the launch.  Ops without
- * a dep path between them may run concurrently: no op may write a buffer
- * that another op reads or writes unless a dep chain orders them.  M is 1..32
- * for the whole stack.  The stack keeps the pointers (x, y, weights): they
- * must stay valid while it is used; change the data in place between runs.
- * No reference counterpart as an API: the reference has no device launches. */
+ * (same in_dim and format), outputs y[p] [M][out_dim(p)].  dep: index of an
+ * EARLIER op whose outputs this op's x reads (x is then one of that op's y
+ * buffers), or -1 when x is ready before the run.  Ops without a dep path
+ * between them may run concurrently: no op may write a buffer that another
+ * op reads or writes unless a dep chain orders them.  M is 1..32 for the
+ * whole stack.  The one-launch plan takes Pack4, Pack5 and XorSparse tile
+ * weights at M = 1 (in_dim a multiple of 4, a padded row of at most 9216
+ * bytes) and Pack4 / XorSparse at M > 1 (in_dim at most 8192); the per-op
+ * plan takes every format, and is what XT_STACK_AUTO picks for a list the
+ * one-launch kernels do not take.  The stack keeps the pointers (x, y,
+ * weights): they must stay valid while it is used; change the data in place
+ * between runs.  No reference counterpart as an API: the reference has no
+ * device launches. */
 typedef struct xt_stack_op {
     const xt_weights* w[4];
     int n;
@@ -367,16 +379,26 @@ typedef struct xt_stack_op {
 } xt_stack_op;
 typedef struct xt_stack xt_stack;
 
-/* Validate the ops and build the device work list (allocates; load time). */
+/* Plan flags, OR'd into xt_stack_create's mode (XT_STACK_AUTO: none). */
+enum { XT_STACK_AUTO = 0, XT_STACK_ONE_LAUNCH = 0x100, XT_STACK_PER_OP = 0x200 };
+
+/* Validate the ops, choose the plan and build the device work list
+ * (allocates; load time).  mode: XT_QUANT_* | optional plan flag. */
 int xt_stack_create(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stack** out);
-/* One launch over the whole list on `stream` (asynchronous; no allocation,
- * no memset, capturable in a HIP graph).  Runs of one stack must not overlap
- * (they share its counters and scratch): order them on one stream. */
+/* The plan of a stack: XT_STACK_ONE_LAUNCH or XT_STACK_PER_OP (negative on
+ * a NULL stack). */
+int xt_stack_plan(const xt_stack* st);
+/* Run the whole list on `stream` (asynchronous).  One launch: no allocation,
+ * no memset, capturable in a HIP graph.  Per op: the calls of
+ * xt_ternary_linear_f32 / _multi_f32, with their workspaces (run once
+ * outside capture first, as for those calls).  Runs of one stack must not
+ * overlap (they share its counters and scratch): order them on one stream. */
 int xt_stack_run(const xt_stack* st, void* stream);
 /* Wait for the device, then report whether any dependency wait of the runs
  * since the last check gave up (*gave_up = 1: outputs of those runs are not
  * valid; a wait gives up after seconds, e.g. if the device is shared with a
- * kernel that never yields), and clear the flag. */
+ * kernel that never yields), and clear the flag.  Per-op stacks have no
+ * such waits: *gave_up = 0. */
 int xt_stack_check(xt_stack* st, int* gave_up);
 int xt_stack_destroy(xt_stack* st);
 

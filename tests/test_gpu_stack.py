@@ -126,13 +126,15 @@ CASES = [("bitnet_m1_down_first", BITNET, 2, 1, "down_first", xtern.XT_QUANT_AVX
          ("mid_m3_down_first", MID, 1, 3, "down_first", xtern.XT_QUANT_SCALAR)]
 
 
+@pytest.mark.parametrize("plan", ["one_launch", "per_op"])
 @pytest.mark.parametrize("name,shapes,layers,M,order,mode", CASES, ids=[c[0] for c in CASES])
-def test_stack_matches_oracle(name, shapes, layers, M, order, mode):
-    log(f"stack {name}: layers={layers} M={M} order={order} mode={mode}")
+def test_stack_matches_oracle(name, shapes, layers, M, order, mode, plan):
+    log(f"stack {name}: layers={layers} M={M} order={order} mode={mode} plan={plan}")
     rng = np.random.default_rng(zlib.crc32(name.encode()) & 0xffff)
     ops, checks = build(rng, shapes, layers, M, order, sparse_down=(M == 3))
     exp = expected(checks, mode)
-    st = xtern.Stack(ops, M, mode)
+    st = xtern.Stack(ops, M, mode, plan=plan)
+    assert st.plan_name == plan
     for rep in range(3):  # repeated launches: the counters reset themselves
         for _, _, ys, _, _ in checks:
             for y in ys:
@@ -143,12 +145,13 @@ def test_stack_matches_oracle(name, shapes, layers, M, order, mode):
         compare(checks, exp, f"run {rep}")
 
 
-def test_stack_in_graph_replays():
-    log("stack graph replay")
+@pytest.mark.parametrize("plan", ["one_launch", "per_op"])
+def test_stack_in_graph_replays(plan):
+    log(f"stack graph replay plan={plan}")
     rng = np.random.default_rng(5)
     ops, checks = build(rng, SMALL, 3, 2, "chain")
     exp = expected(checks, xtern.XT_QUANT_AVX512)
-    st = xtern.Stack(ops, 2)
+    st = xtern.Stack(ops, 2, plan=plan)
     s = torch.cuda.Stream()
     with torch.cuda.stream(s):
         st.run(stream=s)
@@ -182,7 +185,9 @@ def test_stack_rejects_bad_ops():
     x2 = torch.zeros((2, 256), device="cuda")
     y2 = torch.zeros((2, 32), device="cuda")
     with pytest.raises(xtern.XternError):
-        xtern.Stack([([p5], x2, [y2], None)], 2)      # Pack5 only on the M = 1 stack
+        xtern.Stack([([p5], x2, [y2], None)], 2, plan="one_launch")  # Pack5: M = 1 launch only
+    with pytest.raises(xtern.XternError):
+        xtern.Stack([([m.w], x, [y], None)], 1, plan="fastest")      # unknown plan
     with pytest.raises(xtern.XternError):
         xtern.Stack([([m.w], x, [y], None), ([m.w], x, [y], 0)], 1)  # x not an output of dep
     with pytest.raises(xtern.XternError):
@@ -209,9 +214,11 @@ def build_chain(rng, mats, M, x0):
     return ops, checks
 
 
-def run_and_compare(ops, checks, M, mode, reps=2):
+def run_and_compare(ops, checks, M, mode, reps=2, plan="one_launch"):
     exp = expected(checks, mode)
-    st = xtern.Stack(ops, M, mode)
+    st = xtern.Stack(ops, M, mode, plan=plan)
+    if plan is not None:
+        assert st.plan_name == plan
     for rep in range(reps):
         for _, _, ys, _, _ in checks:
             for y in ys:
@@ -282,3 +289,46 @@ def test_stack_m1_ragged_mixed_formats():
     checks = [(0, ["a", "b"], [ya, yb], x0, {"a": a, "b": b}), (1, ["c"], [yc], ya, {"c": c}),
               (2, ["d"], [yd], yc, {"d": d}), (3, ["a"], ops[3][2], yd, {"a": a})]
     run_and_compare(ops, checks, 1, xtern.XT_QUANT_AVX512, reps=3)
+
+
+def test_stack_auto_plan_choice():
+    """XT_STACK_AUTO: the strict 8-layer chain (32 dependency levels) runs
+    per op; the residual-only list (two levels, 32 ops) in one launch; a
+    Pack5 list at M = 2 (not taken by the M > 1 launch) per op.  Each is
+    checked against the oracle in the plan it got."""
+    log("stack auto plan choice")
+    rng = np.random.default_rng(zlib.crc32(b"auto_plan") & 0xffff)
+    shared = {n: Mat(rng, K, N, ws_scale=0.3) for n, (K, N) in BITNET.items()}
+    x0 = torch.from_numpy(rng.standard_normal((1, 2560)).astype(np.float32)).cuda()
+    ops, checks = build_chain(rng, [shared] * 8, 1, x0)
+    st = xtern.Stack(ops, 1)
+    assert st.plan_name == "per_op"
+    run_and_compare(ops, checks, 1, xtern.XT_QUANT_AVX512, reps=1, plan=None)
+
+    # residual only: layer L's q/k/v and gate/up read layer L-1's down output;
+    # o and down read inputs ready before the run
+    ops, checks = [], []
+    h, dep = x0, None
+    for L in range(8):
+        outs = {n: torch.full((1, shared[n].N), float("nan"), device="cuda") for n in shared}
+        xo = torch.from_numpy(rng.standard_normal((1, 2560)).astype(np.float32)).cuda()
+        xd = torch.from_numpy(rng.standard_normal((1, 6912)).astype(np.float32)).cuda()
+        for names, x, d in ((["down"], xd, None), (["q", "k", "v"], h, dep), (["o"], xo, None),
+                            (["gate", "up"], h, dep)):
+            ys = [outs[n] for n in names]
+            ops.append(([shared[n].w for n in names], x, ys, d))
+            checks.append((len(ops) - 1, names, ys, x, shared))
+            if names == ["down"]:
+                dn = len(ops) - 1
+        h, dep = outs["down"], dn
+    st = xtern.Stack(ops, 1)
+    assert st.plan_name == "one_launch"
+    run_and_compare(ops, checks, 1, xtern.XT_QUANT_SCALAR, reps=1, plan=None)
+
+    m = Mat(rng, 320, 48, pack5=True)
+    x2 = torch.from_numpy(rng.standard_normal((2, 320)).astype(np.float32)).cuda()
+    y2 = torch.full((2, 48), float("nan"), device="cuda")
+    st = xtern.Stack([([m.w], x2, [y2], None)], 2)
+    assert st.plan_name == "per_op"
+    run_and_compare([([m.w], x2, [y2], None)], [(0, ["p"], [y2], x2, {"p": m})], 2,
+                    xtern.XT_QUANT_AVX512, reps=1, plan=None)

@@ -214,3 +214,19 @@ def test_stack_create_rejects_null_weights_on_cpu():
         rc = xtern._lib.xt_stack_create(arr, 1, 1, 0, ctypes.byref(h))
         assert rc == xtern.XT_ERR_INVALID
         assert b"NULL weights or output" in xtern._lib.xt_last_error()
+
+
+def test_stack_plan_flags_on_cpu():
+    """Unknown plan flags in xt_stack_create's mode are an argument error
+    found before any device call; xt_stack_plan of NULL is one too."""
+    arr = (xtern._StackOp * 1)()
+    arr[0].n = 1
+    arr[0].x = 0x1000
+    arr[0].dep = -1
+    arr[0].w[0] = 0x4000
+    arr[0].y[0] = 0x2000
+    h = ctypes.c_void_p()
+    for bad in (xtern.XT_STACK_ONE_LAUNCH | xtern.XT_STACK_PER_OP, 0x400, 0x100 | 7):
+        rc = xtern._lib.xt_stack_create(arr, 1, 1, bad, ctypes.byref(h))
+        assert rc == xtern.XT_ERR_INVALID
+    assert xtern._lib.xt_stack_plan(None) == xtern.XT_ERR_INVALID

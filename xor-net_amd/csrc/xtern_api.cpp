@@ -957,7 +957,14 @@ struct xt_stack {
     int blocks;
     int device;
     void* dev_mem;  // ops, items, counters, scratch (one allocation)
+    // the per-op plan: the ops in dependency order, run as library calls
+    bool per_op = false;
+    int64_t M = 0;
+    int qmode = 0;
+    std::vector<xt_stack_op> seq;
 };
+
+}  // extern "C"
 
 namespace {
 
@@ -979,6 +986,63 @@ std::vector<int> stack_order(const xt_stack_op* ops, int nops, const std::vector
     }
     return order;
 }
+
+// Which plan runs a list faster, from measured figures (BitNet-2B
+// projection shapes, weights streamed from HBM, MI355X):
+//  * one call per op: about 4.6 us per op at M = 1, 6.5 at M <= 8 and 9.2 up
+//    to M = 32 (launch to launch in a HIP graph), or the op's weight bytes at
+//    2.7 TB/s where that is longer;
+//  * one launch: the weights at 3.6 TB/s (M = 1), 2.0 (M <= 8) or 1.2 TB/s,
+//    plus about 20 us per dependency level after the first: a level's ops
+//    start only once the level before has published its outputs (device-
+//    scope stores, a count, polls, the quantiser task and its count), and
+//    each of its waves then walks its share of the op's tiles two at a time
+//    (one memory latency per pair), where a one-op launch loads all of a
+//    workgroup's tiles at once.
+// The 30-layer projection stack with the residual dependency (2 levels) runs
+// in one launch in 143 us against 556 us per op; the strict chain (120
+// levels) took 2440 us in one launch against 556 us per op.
+bool stack_prefers_per_op(const xt_stack_op* ops, int nops, int64_t M) {
+    const double call_us = M == 1 ? 4.6 : (M <= 8 ? 6.5 : 9.2);
+    const double call_bpus = 2.7e6, launch_bpus = M == 1 ? 3.6e6 : (M <= 8 ? 2.0e6 : 1.2e6);
+    const double level_us = 20.0;
+    std::vector<int> lvl((size_t)nops, 0);
+    int depth = 0;
+    double bytes = 0, per_op_us = 0;
+    for (int i = 0; i < nops; ++i) {
+        lvl[(size_t)i] = ops[i].dep < 0 ? 0 : lvl[(size_t)ops[i].dep] + 1;
+        depth = std::max(depth, lvl[(size_t)i] + 1);
+        double b = 0;
+        for (int p = 0; p < ops[i].n; ++p) b += (double)ops[i].w[p]->tile_bytes;
+        bytes += b;
+        per_op_us += std::max(call_us, b / call_bpus);
+    }
+    const double launch_us = bytes / launch_bpus + level_us * (depth - 1);
+    return per_op_us < launch_us;
+}
+
+// The per-op plan: the ops' shapes checked as the calls will check them, the
+// list kept in its given order (every dep points to an earlier op).
+int create_per_op(const xt_stack_op* ops, int nops, int64_t M, int qmode, xt_stack** out) {
+    for (int i = 0; i < nops; ++i) {
+        if (int rc = check_group(ops[i].w, ops[i].n, ops[i].x, M, ops[i].y))
+            return fail(rc, "op " + std::to_string(i) + ": " + g_err);
+    }
+    int dev = 0;
+    XT_HIP(hipGetDevice(&dev));
+    xt_stack* st = new (std::nothrow) xt_stack();
+    if (!st) return fail(XT_ERR_NOMEM, "stack handle");
+    st->per_op = true;
+    st->M = M;
+    st->qmode = qmode;
+    st->seq.assign(ops, ops + nops);
+    st->device = dev;
+    st->dev_mem = nullptr;
+    *out = st;
+    return XT_OK;
+}
+
+int create_stack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stack** out);
 
 // M = 1: the streaming stack.  Tasks in list order: the quantiser tasks of
 // ops without a dependency, then per op (in stack_order) its 16-row groups
@@ -1151,6 +1215,8 @@ int create_sstack(const xt_stack_op* ops, int nops, int mode, xt_stack** out) {
 
 }  // namespace
 
+extern "C" {
+
 int xt_stack_create(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stack** out) {
     if (!out) return fail(XT_ERR_INVALID, "out is NULL");
     *out = nullptr;
@@ -1160,6 +1226,10 @@ int xt_stack_create(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_st
         return fail(XT_ERR_UNSUPPORTED, "at most " + std::to_string(max_ops) +
                                             " ops per stack (split longer lists into several stacks)");
     if (M < 1 || M > 32) return fail(XT_ERR_UNSUPPORTED, "stack M must be 1..32");
+    const int plan = mode & ~0xff;
+    mode &= 0xff;
+    if (plan != XT_STACK_AUTO && plan != XT_STACK_ONE_LAUNCH && plan != XT_STACK_PER_OP)
+        return fail(XT_ERR_INVALID, "unknown stack plan flags");
     if (mode != XT_QUANT_AVX512 && mode != XT_QUANT_SCALAR)
         return fail(XT_ERR_INVALID, "unknown quantisation mode");
     for (int i = 0; i < nops; ++i) {
@@ -1179,7 +1249,26 @@ int xt_stack_create(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_st
                 return fail(XT_ERR_INVALID, at + "x (an output of the dep op) differs in length from in_dim");
         }
     }
-    if (M == 1) return create_sstack(ops, nops, mode, out);
+    if (plan == XT_STACK_PER_OP || (plan == XT_STACK_AUTO && stack_prefers_per_op(ops, nops, M)))
+        return create_per_op(ops, nops, M, mode, out);
+    const int rc = M == 1 ? create_sstack(ops, nops, mode, out) : create_stack(ops, nops, M, mode, out);
+    // (a list the one-launch kernels do not take runs per op unless the
+    // caller asked for one launch)
+    if (rc == XT_ERR_UNSUPPORTED && plan == XT_STACK_AUTO) return create_per_op(ops, nops, M, mode, out);
+    return rc;
+}
+
+int xt_stack_plan(const xt_stack* st) {
+    if (!st) return fail(XT_ERR_INVALID, "stack is NULL");
+    return st->per_op ? XT_STACK_PER_OP : XT_STACK_ONE_LAUNCH;
+}
+
+}  // extern "C"
+
+namespace {
+
+// M > 1: the persistent item kernel's work list.
+int create_stack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stack** out) {
     const int rq = xt::stack_rows_per_quant_item();
     const bool one = xt::stack_pipelined((int)M);  // M = 1: rows quantised once per op
     int slots = 0;
@@ -1374,8 +1463,20 @@ int xt_stack_create(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_st
     return XT_OK;
 }
 
+}  // namespace
+
+extern "C" {
+
 int xt_stack_run(const xt_stack* st, void* stream) {
     if (!st) return fail(XT_ERR_INVALID, "stack is NULL");
+    if (st->per_op) {
+        for (size_t i = 0; i < st->seq.size(); ++i) {
+            const xt_stack_op& op = st->seq[i];
+            if (int rc = linear_f32(op.w, op.n, op.x, st->M, op.y, st->qmode, static_cast<hipStream_t>(stream)))
+                return fail(rc, "stack op " + std::to_string(i) + ": " + g_err);
+        }
+        return XT_OK;
+    }
     hipError_t e = st->stream ? xt::launch_sstack(st->sargs, st->blocks, static_cast<hipStream_t>(stream))
                               : xt::launch_stack(st->args, st->blocks, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "stack launch");
@@ -1385,6 +1486,10 @@ int xt_stack_run(const xt_stack* st, void* stream) {
 int xt_stack_check(xt_stack* st, int* gave_up) {
     if (!st || !gave_up) return fail(XT_ERR_INVALID, "NULL argument");
     XT_HIP(hipDeviceSynchronize());
+    if (st->per_op) {
+        *gave_up = 0;
+        return XT_OK;
+    }
     unsigned flag = 0;
     unsigned* slot = st->args.ctr + 2 * 32;  // the error slot (xtern_stack.hip kCtrError)
     XT_HIP(hipMemcpy(&flag, slot, sizeof flag, hipMemcpyDeviceToHost));
@@ -1396,7 +1501,7 @@ int xt_stack_check(xt_stack* st, int* gave_up) {
 int xt_stack_destroy(xt_stack* st) {
     if (!st) return XT_OK;
     hipError_t e = hipDeviceSynchronize();
-    hipError_t e2 = hipFree(st->dev_mem);
+    hipError_t e2 = st->dev_mem ? hipFree(st->dev_mem) : hipSuccess;
     delete st;
     if (e != hipSuccess) return hip_fail(e, "stack destroy");
     if (e2 != hipSuccess) return hip_fail(e2, "stack destroy");

@@ -219,7 +219,7 @@ __device__ void ss_block(const SStackArgs& a, const Rec& r, uint32_t areg, unsig
     constexpr int CH = STEPS * 64;
     constexpr int kPieces = kSStackMaxRowBytes / 1024;  // 16-byte row pieces per lane, at most
     const int lane = threadIdx.x & 63;
-    const int g = lane >> 4, j = lane & 15;
+    const int g = lane >> 4;
     const int nch = r.nch, opi = r.opi;
     const int npieces = r.ldq / 16;
     const uint8_t* const tl = r.tiles + lane * 16;

@@ -58,6 +58,7 @@ XT_ERR_UNSUPPORTED = -4
 XT_PACK4, XT_PACK5, XT_XORSPARSE = 0, 1, 2
 XT_XORSPARSE_STREAM = 5   # the XorSparse blob kept compact on the device
 XT_QUANT_AVX512, XT_QUANT_SCALAR = 0, 1
+XT_STACK_AUTO, XT_STACK_ONE_LAUNCH, XT_STACK_PER_OP = 0, 0x100, 0x200
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -120,6 +121,7 @@ class _StackOp(ctypes.Structure):
 _lib.xt_stack_create.argtypes = [ctypes.POINTER(_StackOp), ctypes.c_int, _i64, ctypes.c_int,
                                  ctypes.POINTER(_vp)]
 _lib.xt_stack_run.argtypes = [_vp, _vp]
+_lib.xt_stack_plan.argtypes = [_vp]
 _lib.xt_stack_check.argtypes = [_vp, ctypes.POINTER(ctypes.c_int)]
 _lib.xt_stack_destroy.argtypes = [_vp]
 
@@ -741,9 +743,16 @@ from .layers import (TernaryLinear, DynamicLinear, TernaryRep, FastRmsNorm, Mlp,
 class Stack:
     """A decode stack (xt_stack_*): ops = [(weights list, x, ys list, dep)],
     x [M, in_dim] f32 and ys [M, out_dim] f32 device tensors that the stack
-    keeps referencing; run() is one launch over every op."""
+    keeps referencing.  plan: None (the library picks), "one_launch" (every
+    op in one persistent launch) or "per_op" (one library call per op);
+    run() runs the whole list, `plan_name` says which plan it has."""
 
-    def __init__(self, ops, M, mode=XT_QUANT_AVX512):
+    _PLANS = {None: XT_STACK_AUTO, "auto": XT_STACK_AUTO, "one_launch": XT_STACK_ONE_LAUNCH,
+              "per_op": XT_STACK_PER_OP}
+
+    def __init__(self, ops, M, mode=XT_QUANT_AVX512, plan=None):
+        if plan not in self._PLANS:
+            raise XternError(XT_ERR_INVALID, f"unknown stack plan {plan!r}")
         torch = _torch()
         arr = (_StackOp * len(ops))()
         self._keep = []
@@ -759,8 +768,15 @@ class Stack:
                 o.y[p] = _dev_ptr(y, torch.float32, "y").value
             self._keep += [x] + list(ys) + list(ws)
         h = ctypes.c_void_p()
-        _check(_lib.xt_stack_create(arr, len(ops), M, mode, ctypes.byref(h)))
+        _check(_lib.xt_stack_create(arr, len(ops), M, mode | self._PLANS[plan], ctypes.byref(h)))
         self.handle = h
+
+    @property
+    def plan_name(self):
+        p = _lib.xt_stack_plan(self.handle)
+        if p < 0:
+            _check(p)
+        return "per_op" if p == XT_STACK_PER_OP else "one_launch"
 
     def run(self, stream=None):
         _check(_lib.xt_stack_run(self.handle, _stream_ptr(stream)))
