@@ -380,7 +380,7 @@ typedef struct xt_stack_op {
 typedef struct xt_stack xt_stack;
 
 /* Plan flags, OR'd into xt_stack_create's mode (XT_STACK_AUTO: none). */
-enum { XT_STACK_AUTO = 0, XT_STACK_ONE_LAUNCH = 0x100, XT_STACK_PER_OP = 0x200 };
+enum { XT_STACK_AUTO = 0, XT_STACK_ONE_LAUNCH = 256, XT_STACK_PER_OP = 512 };
 
 /* Validate the ops, choose the plan and build the device work list
  * (allocates; load time).  mode: XT_QUANT_* | optional plan flag. */

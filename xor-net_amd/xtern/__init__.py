@@ -58,7 +58,7 @@ XT_ERR_UNSUPPORTED = -4
 XT_PACK4, XT_PACK5, XT_XORSPARSE = 0, 1, 2
 XT_XORSPARSE_STREAM = 5   # the XorSparse blob kept compact on the device
 XT_QUANT_AVX512, XT_QUANT_SCALAR = 0, 1
-XT_STACK_AUTO, XT_STACK_ONE_LAUNCH, XT_STACK_PER_OP = 0, 0x100, 0x200
+XT_STACK_AUTO, XT_STACK_ONE_LAUNCH, XT_STACK_PER_OP = 0, 256, 512
 
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
