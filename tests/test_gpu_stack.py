@@ -123,7 +123,10 @@ CASES = [("bitnet_m1_down_first", BITNET, 2, 1, "down_first", xtern.XT_QUANT_AVX
          ("small_m3", SMALL, 4, 3, "chain", xtern.XT_QUANT_AVX512),
          ("small_m17", SMALL, 3, 17, "down_first", xtern.XT_QUANT_SCALAR),
          ("mid_m1_chain", MID, 2, 1, "chain", xtern.XT_QUANT_AVX512),
-         ("mid_m3_down_first", MID, 1, 3, "down_first", xtern.XT_QUANT_SCALAR)]
+         ("mid_m3_down_first", MID, 1, 3, "down_first", xtern.XT_QUANT_SCALAR),
+         ("bitnet_m16_down_first", BITNET, 1, 16, "down_first", xtern.XT_QUANT_SCALAR),
+         ("small_m16_chain", SMALL, 3, 16, "chain", xtern.XT_QUANT_AVX512),
+         ("mid_m12_chain", MID, 2, 12, "chain", xtern.XT_QUANT_AVX512)]
 
 
 @pytest.mark.parametrize("plan", ["one_launch", "per_op"])
@@ -182,10 +185,10 @@ def test_stack_rejects_bad_ops():
         xtern.Stack([([m.w], x, [y], None)], 33)      # M above 32
     p5 = xtern.DeviceWeights(xtern.XT_PACK5, 256, 32,
                              np.concatenate([xtern.pack_ternary5(r) for r in m.t]), m.ws)
-    x2 = torch.zeros((2, 256), device="cuda")
-    y2 = torch.zeros((2, 32), device="cuda")
+    x17 = torch.zeros((17, 256), device="cuda")
+    y17 = torch.zeros((17, 32), device="cuda")
     with pytest.raises(xtern.XternError):
-        xtern.Stack([([p5], x2, [y2], None)], 2, plan="one_launch")  # Pack5: M = 1 launch only
+        xtern.Stack([([p5], x17, [y17], None)], 17, plan="one_launch")  # Pack5: M <= 16 launch only
     with pytest.raises(xtern.XternError):
         xtern.Stack([([m.w], x, [y], None)], 1, plan="fastest")      # unknown plan
     with pytest.raises(xtern.XternError):
@@ -254,47 +257,64 @@ def test_stack_m1_bitnet_30_layers():
     run_and_compare(ops, checks, 1, xtern.XT_QUANT_SCALAR)
 
 
+def test_stack_m8_bitnet_30_layers():
+    """The 30-layer BitNet-2B projection chain at M = 8 (120 ops) in one
+    launch against the oracle (shared matrices, as at M = 1)."""
+    log("stack 30-layer bitnet chain, M=8")
+    rng = np.random.default_rng(zlib.crc32(b"bitnet30_m8") & 0xffff)
+    shared = {n: Mat(rng, K, N, ws_scale=0.3) for n, (K, N) in BITNET.items()}
+    x0 = torch.from_numpy(rng.standard_normal((8, 2560)).astype(np.float32)).cuda()
+    ops, checks = build_chain(rng, [shared] * 30, 8, x0)
+    run_and_compare(ops, checks, 8, xtern.XT_QUANT_AVX512, reps=1)
+
+
 PACK5_3B = {"q": (3200, 3200), "k": (3200, 320), "v": (3200, 320), "o": (3200, 3200),
             "gate": (3200, 8640), "up": (3200, 8640), "down": (8640, 3200)}
 
 
-@pytest.mark.parametrize("mode", [xtern.XT_QUANT_AVX512, xtern.XT_QUANT_SCALAR])
-def test_stack_m1_pack5_chain(mode):
-    """Pack5 weights (BitNet-3B shapes) on the M = 1 stack,
+@pytest.mark.parametrize("M,mode", [(1, xtern.XT_QUANT_AVX512), (1, xtern.XT_QUANT_SCALAR),
+                                    (8, xtern.XT_QUANT_AVX512), (16, xtern.XT_QUANT_SCALAR)])
+def test_stack_pack5_chain(M, mode):
+    """Pack5 weights (BitNet-3B shapes) in one launch,
     strict chain, two layers."""
-    log(f"stack pack5 chain M=1 mode={mode}")
-    rng = np.random.default_rng(zlib.crc32(b"pack5_chain") & 0xffff + mode)
+    log(f"stack pack5 chain M={M} mode={mode}")
+    rng = np.random.default_rng(zlib.crc32(b"pack5_chain") & 0xffff + mode + M)
     mats = [{n: Mat(rng, K, N, pack5=True, ws_scale=0.3) for n, (K, N) in PACK5_3B.items()} for _ in range(2)]
-    x0 = torch.from_numpy(rng.standard_normal((1, 3200)).astype(np.float32)).cuda()
-    ops, checks = build_chain(rng, mats, 1, x0)
-    run_and_compare(ops, checks, 1, mode)
+    x0 = torch.from_numpy(rng.standard_normal((M, 3200)).astype(np.float32)).cuda()
+    ops, checks = build_chain(rng, mats, M, x0)
+    run_and_compare(ops, checks, M, mode)
 
 
-def test_stack_m1_ragged_mixed_formats():
-    """Ragged shapes (N not a multiple of 16, K not of 256), XorSparse and
-    Pack4 projections, and a Pack5 op in one M = 1 stack."""
-    log("stack ragged mixed formats M=1")
-    rng = np.random.default_rng(zlib.crc32(b"ragged_mixed") & 0xffff)
+@pytest.mark.parametrize("M", [1, 2, 5, 8, 13, 16])
+def test_stack_ragged_mixed_formats(M):
+    """Ragged shapes (N not a multiple of 16, K not of 256, Pack5 rows of an
+    odd number of 320-column chunks), XorSparse and Pack4 projections, and
+    a Pack5 op in one launch."""
+    log(f"stack ragged mixed formats M={M}")
+    rng = np.random.default_rng(zlib.crc32(b"ragged_mixed") & 0xffff + M)
     a = Mat(rng, 300, 76)
     b = Mat(rng, 300, 45, sparse=True)
     c = Mat(rng, 76, 132, pack5=True)
     d = Mat(rng, 132, 300, sparse=True)
-    x0 = torch.from_numpy(rng.standard_normal((1, 300)).astype(np.float32)).cuda()
-    ya = torch.full((1, 76), float("nan"), device="cuda")
-    yb = torch.full((1, 45), float("nan"), device="cuda")
-    yc = torch.full((1, 132), float("nan"), device="cuda")
-    yd = torch.full((1, 300), float("nan"), device="cuda")
+    e = Mat(rng, 300, 37, pack5=True)
+    x0 = torch.from_numpy(rng.standard_normal((M, 300)).astype(np.float32)).cuda()
+    ya = torch.full((M, 76), float("nan"), device="cuda")
+    yb = torch.full((M, 45), float("nan"), device="cuda")
+    yc = torch.full((M, 132), float("nan"), device="cuda")
+    yd = torch.full((M, 300), float("nan"), device="cuda")
+    ye = torch.full((M, 37), float("nan"), device="cuda")
     ops = [([a.w, b.w], x0, [ya, yb], None), ([c.w], ya, [yc], 0), ([d.w], yc, [yd], 1),
-           ([a.w], yd, [torch.full((1, 76), float("nan"), device="cuda")], 2)]
+           ([a.w], yd, [torch.full((M, 76), float("nan"), device="cuda")], 2), ([e.w], yd, [ye], 2)]
     checks = [(0, ["a", "b"], [ya, yb], x0, {"a": a, "b": b}), (1, ["c"], [yc], ya, {"c": c}),
-              (2, ["d"], [yd], yc, {"d": d}), (3, ["a"], ops[3][2], yd, {"a": a})]
-    run_and_compare(ops, checks, 1, xtern.XT_QUANT_AVX512, reps=3)
+              (2, ["d"], [yd], yc, {"d": d}), (3, ["a"], ops[3][2], yd, {"a": a}),
+              (4, ["e"], [ye], yd, {"e": e})]
+    run_and_compare(ops, checks, M, xtern.XT_QUANT_AVX512, reps=3)
 
 
 def test_stack_auto_plan_choice():
     """XT_STACK_AUTO: the strict 8-layer chain (32 dependency levels) runs
     per op; the residual-only list (two levels, 32 ops) in one launch; a
-    Pack5 list at M = 2 (not taken by the M > 1 launch) per op.  Each is
+    Pack5 list at M = 17 (not taken by the M > 16 launch) per op.  Each is
     checked against the oracle in the plan it got."""
     log("stack auto plan choice")
     rng = np.random.default_rng(zlib.crc32(b"auto_plan") & 0xffff)
@@ -326,9 +346,9 @@ def test_stack_auto_plan_choice():
     run_and_compare(ops, checks, 1, xtern.XT_QUANT_SCALAR, reps=1, plan=None)
 
     m = Mat(rng, 320, 48, pack5=True)
-    x2 = torch.from_numpy(rng.standard_normal((2, 320)).astype(np.float32)).cuda()
-    y2 = torch.full((2, 48), float("nan"), device="cuda")
-    st = xtern.Stack([([m.w], x2, [y2], None)], 2)
+    x2 = torch.from_numpy(rng.standard_normal((17, 320)).astype(np.float32)).cuda()
+    y2 = torch.full((17, 48), float("nan"), device="cuda")
+    st = xtern.Stack([([m.w], x2, [y2], None)], 17)
     assert st.plan_name == "per_op"
-    run_and_compare([([m.w], x2, [y2], None)], [(0, ["p"], [y2], x2, {"p": m})], 2,
+    run_and_compare([([m.w], x2, [y2], None)], [(0, ["p"], [y2], x2, {"p": m})], 17,
                     xtern.XT_QUANT_AVX512, reps=1, plan=None)

@@ -1047,7 +1047,7 @@ int create_stack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stack
 // M = 1: the streaming stack.  Tasks in list order: the quantiser tasks of
 // ops without a dependency, then per op (in stack_order) its 16-row groups
 // followed by the quantiser tasks of the ops that read its outputs.
-int create_sstack(const xt_stack_op* ops, int nops, int mode, xt_stack** out) {
+int create_sstack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stack** out) {
     if (nops > xt::kSStackMaxOps)
         return fail(XT_ERR_UNSUPPORTED, "at most " + std::to_string(xt::kSStackMaxOps) + " ops per M = 1 stack");
     struct OpInfo {
@@ -1079,22 +1079,26 @@ int create_sstack(const xt_stack_op* ops, int nops, int mode, xt_stack** out) {
         f.fmt = fmt == XT_PACK5 ? XT_PACK5 : XT_PACK4;
         f.K = (int)op.w[0]->K;
         f.nch = (int)op.w[0]->nch;
-        f.ldq = f.nch * ch;
+        // (M > 1: each token's row fills whole 128-byte lines of its own;
+        // rows written on one XCD are read with ordinary loads on others)
+        f.ldq = M == 1 ? f.nch * ch : (int)align_up((size_t)f.nch * ch, 128);
         f.qoff = scratch;
-        scratch += align_up((size_t)f.ldq + 8, 256);  // row, then its sum and scale
-        ntasks += 1 + (size_t)f.ngroups;
+        scratch += align_up((size_t)M * f.ldq + 8 * (size_t)M, 256);  // rows, then sums and scales
+        ntasks += (size_t)M + (size_t)f.ngroups;
         if (op.dep >= 0) pub[(size_t)op.dep] = 1;
     }
     // 16-row groups per task: as many as keep about four tasks per wave of
-    // a full grid (a task's row load and start are paid once per task)
+    // a full grid (a task's start is paid once per task; M > 1 reads a
+    // chunk's activation pieces once per task)
     int dev0 = 0, cus0 = 0;
     XT_HIP(hipGetDevice(&dev0));
     XT_HIP(hipDeviceGetAttribute(&cus0, hipDeviceAttributeMultiprocessorCount, dev0));
     size_t all_groups = 0;
     for (const OpInfo& f : info) all_groups += (size_t)f.ngroups;
-    // (at most 4: a task's rows are one per lane of a wave)
+    // (at most 4: M = 1 a task's rows are one per lane of a wave; M > 1 its
+    // groups' tiles of one chunk are loaded together)
     const int rg = (int)std::max<size_t>(1, std::min<size_t>(4, all_groups / ((size_t)cus0 * 16 * 4)));
-    ntasks = nops;
+    ntasks = (size_t)nops * (size_t)M;
     for (int i = 0; i < nops; ++i)
         for (int p = 0; p < ops[i].n; ++p) ntasks += (size_t)(((ops[i].w[p]->N + 15) / 16 + rg - 1) / rg);
     if (ntasks > (size_t)1 << 30) return fail(XT_ERR_UNSUPPORTED, "stack too large");
@@ -1121,11 +1125,16 @@ int create_sstack(const xt_stack_op* ops, int nops, int mode, xt_stack** out) {
         t.dep_groups = ops[i].dep >= 0 ? info[(size_t)ops[i].dep].ngroups : 0;
         return t;
     };
-    auto quant_task = [&](int i) {
-        xt::SStackTask t = base(i);
-        t.tiles = ops[i].x;
-        t.flags = 1;
-        tasks.push_back(t);
+    auto quant_task = [&](int i) {  // one per token
+        const OpInfo& f = info[(size_t)i];
+        for (int64_t m = 0; m < M; ++m) {
+            xt::SStackTask t = base(i);
+            t.tiles = ops[i].x + m * f.K;
+            t.q = reinterpret_cast<int8_t*>(sc + f.qoff + (size_t)m * f.ldq);
+            t.ws = reinterpret_cast<const float*>(sc + f.qoff + (size_t)M * f.ldq + 4 * (size_t)m);
+            t.flags = 1;
+            tasks.push_back(t);
+        }
     };
     for (int i = 0; i < nops; ++i)
         if (ops[i].dep < 0) quant_task(i);
@@ -1140,6 +1149,7 @@ int create_sstack(const xt_stack_op* ops, int nops, int mode, xt_stack** out) {
                 t.tiles = w->tiles + (size_t)G * w->nch * xt::kTileBytes;
                 t.ws = w->ws + G * 16;
                 t.y = op.y[p] + G * 16;
+                t.K = (int)w->N;  // (a group task's output row stride)
                 t.flags = (pub[(size_t)i] ? 2 : 0) | (info[(size_t)i].fmt == XT_PACK5 ? 4 : 0) | (n_g << 16);
                 t.nrows = (int)std::min<int64_t>(16, w->N - (G + n_g - 1) * 16);
                 tasks.push_back(t);
@@ -1153,8 +1163,10 @@ int create_sstack(const xt_stack_op* ops, int nops, int mode, xt_stack** out) {
     const int wpb = xt::sstack_waves_per_block();
     int per_cu = 0;
     int row_bytes = 1024;
-    for (const OpInfo& f : info) row_bytes = std::max(row_bytes, (int)align_up((size_t)f.ldq, 1024));
-    e = xt::sstack_blocks_per_cu(row_bytes, &per_cu);
+    for (const OpInfo& f : info)
+        row_bytes = std::max(row_bytes, M == 1 ? (int)align_up((size_t)f.ldq, 1024)
+                                               : 16 * (xt::chunk_cols(f.fmt) + 16));
+    e = xt::sstack_blocks_per_cu((int)M, row_bytes, &per_cu);
     if (e == hipSuccess && per_cu < 1) e = hipErrorInvalidConfiguration;
     const int grid = std::max(1, std::min(cus0 * std::min(per_cu, 4), ((int)tasks.size() + wpb - 1) / wpb));
     const int nw = grid * wpb;
@@ -1206,6 +1218,7 @@ int create_sstack(const xt_stack_op* ops, int nops, int mode, xt_stack** out) {
     st->args.ctr = st->sargs.ctr;    // (the error slot, read by xt_stack_check)
     st->sargs.woff = reinterpret_cast<const int*>(mem + tasks_b + ctr_b + scratch);
     st->sargs.row_bytes = row_bytes;
+    st->sargs.M = (int)M;
     st->blocks = grid;
     st->device = dev0;
     st->dev_mem = mem;
@@ -1251,7 +1264,8 @@ int xt_stack_create(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_st
     }
     if (plan == XT_STACK_PER_OP || (plan == XT_STACK_AUTO && stack_prefers_per_op(ops, nops, M)))
         return create_per_op(ops, nops, M, mode, out);
-    const int rc = M == 1 ? create_sstack(ops, nops, mode, out) : create_stack(ops, nops, M, mode, out);
+    const int rc = M <= xt::kSStackMaxM ? create_sstack(ops, nops, M, mode, out)
+                                        : create_stack(ops, nops, M, mode, out);
     // (a list the one-launch kernels do not take runs per op unless the
     // caller asked for one launch)
     if (rc == XT_ERR_UNSUPPORTED && plan == XT_STACK_AUTO) return create_per_op(ops, nops, M, mode, out);

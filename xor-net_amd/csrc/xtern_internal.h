@@ -175,17 +175,21 @@ hipError_t scratch_region(void** ptr, size_t* bytes);
 // Streaming decode stack, M = 1 (xtern_sstack.hip).
 constexpr int kSStackMaxOps = 8191;          // op index: 13 bits of a task
 constexpr int kSStackMaxRowBytes = 9216;     // i8 row (nch * chunk columns) of one op, at most
+constexpr int kSStackMaxM = 16;              // tokens of the streaming stack (one MFMA block)
 // One task, 64 bytes: everything a wave needs to start it, loaded one task
 // ahead.  flags bits 0-15: 1 quantiser task, 2 other ops read the outputs
 // (count the groups' completion), 4 Pack5 tiles; bits 16-31: the task's
 // consecutive 16-row groups (one projection), nrows: rows of the last one.
+// An op's quantised rows: q [M][ldq] i8, then M i32 row sums, then M f32
+// inverse scales.
 struct alignas(16) SStackTask {
-    const void* tiles;        // group: its first tile; quantiser: the op's f32 input row
-    const float* ws;          // group: w_scales of its rows
-    float* y;                 // group: outputs of its rows
-    int8_t* q;                // the op's i8 row [ldq], then its i32 sum and f32 inverse scale
+    const void* tiles;        // group: its first tile; quantiser: its token's f32 input row
+    const float* ws;          // group: w_scales of its rows; quantiser: its token's sum slot
+    float* y;                 // group: outputs of its rows (token 0; token t at + t * K)
+    int8_t* q;                // group: the op's rows q; quantiser: its token's i8 row
     int opi, flags, nch, nrows;
-    int K, ldq, dep, dep_groups;  // dep: op whose outputs x reads, or -1; its group count
+    int K, ldq, dep, dep_groups;  // K: quantiser: in_dim; group: out_dim (the output row stride).
+                                  // dep: op whose outputs x reads, or -1; its group count
 };
 static_assert(sizeof(SStackTask) == 64, "a task record is four 16-byte loads");
 struct SStackArgs {
@@ -193,10 +197,12 @@ struct SStackArgs {
     const int* woff;          // [waves + 1]
     unsigned* ctr;            // (4 + 2 * nops) slots of 128 bytes, zero between launches
     int ntasks, nops, mode, spin_limit;
-    int row_bytes;            // LDS per wave for the i8 row: the longest ldq, rounded to 1 KiB
+    int row_bytes;            // LDS per wave: M = 1 the i8 row (the longest ldq, rounded to
+                              // 1 KiB); M > 1 one chunk of 16 token rows
+    int M;                    // tokens, 1..kSStackMaxM
 };
 hipError_t launch_sstack(const SStackArgs& a, int blocks, hipStream_t s);
-hipError_t sstack_blocks_per_cu(int row_bytes, int* n);
+hipError_t sstack_blocks_per_cu(int M, int row_bytes, int* n);
 int sstack_waves_per_block();
 // Persistent decode stack (xtern_stack.hip): one launch over a list of ops.
 constexpr int kStackRowGroupsMax = 8;       // 16-row groups per GEMV item (M > 1): stack_gemv_rg

@@ -137,8 +137,9 @@ __device__ __forceinline__ Rec ss_rec(unsigned w) {
     return r;
 }
 
-// The quantiser task of an op (one wave): quantization.rs:95-195 on the f32
-// row -> i8 row (zero from K to ldq), its exact sum and its inverse scale.
+// A quantiser task (one wave, one token of an op): quantization.rs:95-195 on
+// the f32 row -> i8 row (zero from K to ldq), its exact sum and its inverse
+// scale; the op's count of quantised tokens goes up by one.
 template <int MODE>
 __device__ void ss_quant(const SStackArgs& a, const Rec& r) {
     const int lane = threadIdx.x & 63;
@@ -178,7 +179,7 @@ __device__ void ss_quant(const SStackArgs& a, const Rec& r) {
     const float invs = (rmx > 0.0f) ? __fdiv_rn(rmx, 127.0f) : 1.0f;
     const int kmain = (K / 16) * 16;
     int rs = 0;
-    const __amdgpu_buffer_rsrc_t qr = ss_rsrc(r.q, (unsigned)(r.ldq + 8));
+    const __amdgpu_buffer_rsrc_t qr = ss_rsrc(r.q, (unsigned)r.ldq);
     const int n4q = r.ldq / 4;  // (ldq >= K: the i8 row is zero from K on)
     const int qrounds = (n4q + 64 * kSsQ - 1) / (64 * kSsQ);
     for (int rd = 0; rd < qrounds; ++rd) {
@@ -200,9 +201,10 @@ __device__ void ss_quant(const SStackArgs& a, const Rec& r) {
         }
     }
     rs = wave_reduce_bits(rs, [](int p, int q) { return p + q; });
-    if (lane == 0) {
-        ss_st_coh4(qr, (unsigned)r.ldq, (unsigned)rs);
-        ss_st_coh4(qr, (unsigned)r.ldq + 4u, __float_as_uint(invs));
+    if (lane == 0) {  // the token's sum, and its inverse scale M slots later
+        const __amdgpu_buffer_rsrc_t sr = ss_rsrc(r.ws, (unsigned)(4 * a.M + 4));
+        ss_st_coh4(sr, 0u, (unsigned)rs);
+        ss_st_coh4(sr, (unsigned)(4 * a.M), __float_as_uint(invs));
     }
     __builtin_amdgcn_s_waitcnt(0);  // (vmcnt and lgkmcnt 0: every store has completed)
     if (lane == 0)
@@ -347,7 +349,147 @@ __device__ void ss_block(const SStackArgs& a, const Rec& r, uint32_t areg, unsig
     }
 }
 
-__global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(4))) void sstack_kernel(const SStackArgs a) {
+// M > 1 (up to 16 tokens): a block of r.ngroups (<= kSsR) consecutive
+// 16-row groups of one projection, walked chunk by chunk: each step loads
+// the block's tiles of one chunk (one per group) and the chunk's 16-byte
+// pieces of the M quantised rows, puts the pieces in this wave's LDS region
+// (16 token rows of CH bytes, padded) and multiplies every group's tile with
+// the same A fragments, so the activation bytes are read once per block
+// rather than once per group.  The rows are read with ordinary loads, and
+// only after the op's count shows all M tokens quantised: nothing on this
+// XCD has read those lines during the launch before (the L2s start a launch
+// empty of them), every token's row starts on its own 128-byte line (the
+// host pads the row pitch), so its L2 holds no stale copy, and later tasks
+// of the op on the XCD hit in it.
+constexpr int kSsR = 4;  // 16-row groups per task, at most (M > 1)
+template <int FMT>
+__device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsigned* known) {
+    constexpr int STEPS = (FMT == XT_PACK5) ? 5 : 4;
+    constexpr int CH = STEPS * 64;
+    constexpr int LDR = CH + 16;       // LDS bytes per token row of a chunk
+    constexpr int PR = CH / 16;        // 16-byte pieces per token row of a chunk
+    constexpr int kAP = (16 * PR) / 64;  // pieces per lane for 16 token rows
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, j = lane & 15;
+    const int M = a.M, nch = r.nch, opi = r.opi, ldq = r.ldq, N = r.K;
+    const int ng = r.ngroups;
+    unsigned* const qdone = ss_ctr(a.ctr, kSsDone0 + a.nops + opi);
+    // all M tokens quantised before any row load (see above)
+    if (!((known[opi >> 5] >> (opi & 31)) & 1u)) {
+        if (lane == 0) ss_wait(qdone, (unsigned)M, ss_ctr(a.ctr, kSsError), a.spin_limit);
+        __builtin_amdgcn_wave_barrier();
+        if (lane == 0) atomicOr(&known[opi >> 5], 1u << (opi & 31));
+    }
+    // the activation pieces of one chunk: piece p = lane + 64 u is token
+    // p / PR, bytes (p % PR) * 16; tokens >= M read nothing (outside the
+    // resource) and leave rows of the LDS region the outputs never use
+    const __amdgpu_buffer_rsrc_t qr = ss_rsrc(r.q, (unsigned)(M * ldq));
+    auto ptok = [&](int u) { return (lane + 64 * u) / PR; };
+    auto pcol = [&](int u) { return ((lane + 64 * u) % PR) * 16; };
+    const uint32_t abase = areg + (uint32_t)(j * LDR + g * 16);
+    const uint8_t* const tl = reinterpret_cast<const uint8_t*>(r.tiles) + lane * 16;
+    v4i acc[kSsR];
+#pragma unroll
+    for (int gi = 0; gi < kSsR; ++gi) acc[gi] = v4i{0, 0, 0, 0};
+    for (int c = 0; c < nch; ++c) {
+        v4i wb[kSsR], ap[kAP];
+#pragma unroll
+        for (int gi = 0; gi < kSsR; ++gi)  // (groups past the block: its last group again, unused)
+            wb[gi] = ss_ld_tile(tl + ((size_t)min(gi, ng - 1) * nch + c) * kTileBytes);
+#pragma unroll
+        for (int u = 0; u < kAP; ++u) {
+            const int tk = ptok(u);
+            const unsigned go = tk < M ? (unsigned)(tk * ldq + pcol(u) + c * CH) : 0x80000000u;
+            ap[u] = __builtin_amdgcn_raw_buffer_load_b128(qr, go, 0, 0);
+        }
+        // (every load of the step is issued before anything waits for one)
+        __builtin_amdgcn_sched_barrier(0);
+        // (the previous chunk's LDS reads were issued before these writes,
+        // and a wave's LDS accesses complete in order)
+#pragma unroll
+        for (int u = 0; u < kAP; ++u)
+            *reinterpret_cast<__attribute__((address_space(3))) v4i*>(
+                (uintptr_t)(areg + (uint32_t)(ptok(u) * LDR + pcol(u)))) = ap[u];
+        v4i af[STEPS];
+#pragma unroll
+        for (int st = 0; st < STEPS; ++st) af[st] = ss_lds16(abase + st * 64);
+        // (all kSsR groups are multiplied: no branch for the compiler to sink
+        // loads into; products of groups past the block are never stored)
+#pragma unroll
+        for (int gi = 0; gi < kSsR; ++gi) {
+            if constexpr (FMT == XT_PACK5) {
+                int E[4], O[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    E[q] = wb[gi][q] & 0x00ff00ff;
+                    O[q] = ((unsigned)wb[gi][q] >> 8) & 0x00ff00ff;
+                }
+#pragma unroll
+                for (int st = 0; st < STEPS; ++st) {
+                    v4i b;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int pE = E[q] * 3, pO = O[q] * 3;
+                        b[q] = (int)__builtin_amdgcn_perm((unsigned)pO, (unsigned)pE, 0x07030501u);
+                        E[q] = pE & 0x00ff00ff;
+                        O[q] = pO & 0x00ff00ff;
+                    }
+                    acc[gi] = mfma(af[st], b, acc[gi]);
+                }
+            } else {
+#pragma unroll
+                for (int st = 0; st < STEPS; ++st) acc[gi] = mfma(af[st], decode4(wb[gi][st]), acc[gi]);
+            }
+        }
+    }
+    // the row sums and inverse scales of tokens 4g .. 4g + 3 (this lane's
+    // outputs), and the w_scales of row j of each group
+    // (device-scope loads: the M tokens' slots share lines that quantiser
+    // tasks on other XCDs wrote)
+    const __amdgpu_buffer_rsrc_t sr = ss_rsrc(r.q + (size_t)M * ldq, (unsigned)(8 * M));
+    int rs[4];
+    float inv[4];
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        const unsigned tk = (unsigned)min(4 * g + t, M - 1);
+        rs[t] = (int)__builtin_amdgcn_raw_buffer_load_b32(sr, 4u * tk, 0, kSsCoh);
+        inv[t] = __int_as_float((int)__builtin_amdgcn_raw_buffer_load_b32(sr, 4u * (tk + M), 0, kSsCoh));
+    }
+    const int trows = (ng - 1) * 16 + r.nrows;
+    float wsc[kSsR];
+#pragma unroll
+    for (int gi = 0; gi < kSsR; ++gi) wsc[gi] = ((gfloat*)(uintptr_t)r.ws)[min(gi * 16 + j, trows - 1)];
+
+    // acc[gi][t]: token 4g + t, row j of group gi; the MFMAs took codes w + 1,
+    // so the token's sum comes off (layers.rs:340: (dot as f32 * inv) * w_scale)
+    const bool pub = (r.flags & kSsPub) != 0;
+    const __amdgpu_buffer_rsrc_t yr = ss_rsrc(r.y, (unsigned)(((M - 1) * N + trows) * 4));
+#pragma unroll
+    for (int gi = 0; gi < kSsR; ++gi) {
+        if (gi >= ng) break;  // (uniform)
+        const int row = gi * 16 + j;
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            const int tk = 4 * g + t;
+            if (tk < M && row < trows) {
+                const float v = __fmul_rn(__fmul_rn((float)(acc[gi][t] - rs[t]), inv[t]), wsc[gi]);
+                if (pub) ss_st_coh4(yr, (unsigned)((tk * N + row) * 4), __float_as_uint(v));
+                else ((gfloat_w*)(uintptr_t)r.y)[(size_t)tk * N + row] = v;
+            }
+        }
+    }
+    if (pub) {  // another op reads these outputs inside the launch
+        __builtin_amdgcn_s_waitcnt(0);
+        if (lane == 0)
+            __hip_atomic_fetch_add(ss_ctr(a.ctr, kSsDone0 + opi), (unsigned)ng, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
+// MT: the M > 1 group tasks (ss_mblock), else M = 1 (ss_block); one
+// instantiation per form, so each has the registers to itself.
+template <bool MT>
+__global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(MT ? 3 : 4))) void sstack_kernel(const SStackArgs a) {
     __shared__ unsigned known[kSsKnownWords];  // ops this workgroup has seen quantised
     extern __shared__ __align__(16) uint8_t rows[];  // [kSsW][a.row_bytes]: each wave's i8 row
     for (int i = threadIdx.x; i < kSsKnownWords; i += kSsW * 64) known[i] = 0u;
@@ -366,10 +508,12 @@ __global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(4))) 
         if (cur.flags & kSsQuant) {
             if (a.mode == XT_QUANT_AVX512) ss_quant<XT_QUANT_AVX512>(a, cur);
             else ss_quant<XT_QUANT_SCALAR>(a, cur);
-        } else if (cur.flags & kSsPack5) {
-            ss_block<XT_PACK5>(a, cur, areg, known);
+        } else if constexpr (MT) {
+            if (cur.flags & kSsPack5) ss_mblock<XT_PACK5>(a, cur, areg, known);
+            else ss_mblock<XT_PACK4>(a, cur, areg, known);
         } else {
-            ss_block<XT_PACK4>(a, cur, areg, known);
+            if (cur.flags & kSsPack5) ss_block<XT_PACK5>(a, cur, areg, known);
+            else ss_block<XT_PACK4>(a, cur, areg, known);
         }
     }
     // the last wave out resets the counts for the next launch (its own
@@ -392,13 +536,18 @@ __global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(4))) 
 static size_t ss_dyn_lds(int row_bytes) { return (size_t)kSsW * row_bytes; }
 
 hipError_t launch_sstack(const SStackArgs& a, int blocks, hipStream_t s) {
-    hipLaunchKernelGGL(sstack_kernel, dim3(blocks), dim3(kSsW * 64), ss_dyn_lds(a.row_bytes), s, a);
+    if (a.M < 1 || a.M > kSStackMaxM) return hipErrorInvalidValue;
+    if (a.M > 1)
+        hipLaunchKernelGGL(sstack_kernel<true>, dim3(blocks), dim3(kSsW * 64), ss_dyn_lds(a.row_bytes), s, a);
+    else
+        hipLaunchKernelGGL(sstack_kernel<false>, dim3(blocks), dim3(kSsW * 64), ss_dyn_lds(a.row_bytes), s, a);
     return hipGetLastError();
 }
 
-hipError_t sstack_blocks_per_cu(int row_bytes, int* n) {
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(n, reinterpret_cast<const void*>(sstack_kernel),
-                                                        kSsW * 64, ss_dyn_lds(row_bytes));
+hipError_t sstack_blocks_per_cu(int M, int row_bytes, int* n) {
+    const void* k = M > 1 ? reinterpret_cast<const void*>(sstack_kernel<true>)
+                          : reinterpret_cast<const void*>(sstack_kernel<false>);
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(n, k, kSsW * 64, ss_dyn_lds(row_bytes));
 }
 
 int sstack_waves_per_block() { return kSsW; }
