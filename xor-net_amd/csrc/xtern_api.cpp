@@ -1097,7 +1097,9 @@ int create_sstack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stac
     for (const OpInfo& f : info) all_groups += (size_t)f.ngroups;
     // (at most 4: M = 1 a task's rows are one per lane of a wave; M > 1 its
     // groups' tiles of one chunk are loaded together)
-    const int rg = (int)std::max<size_t>(1, std::min<size_t>(4, all_groups / ((size_t)cus0 * 16 * 4)));
+    // M > 1: always 4 (the kernel loads and multiplies four groups' tiles per
+    // step, and shares the chunk's activation pieces among them)
+    const int rg = M > 1 ? 4 : (int)std::max<size_t>(1, std::min<size_t>(4, all_groups / ((size_t)cus0 * 16 * 4)));
     ntasks = (size_t)nops * (size_t)M;
     for (int i = 0; i < nops; ++i)
         for (int p = 0; p < ops[i].n; ++p) ntasks += (size_t)(((ops[i].w[p]->N + 15) / 16 + rg - 1) / rg);
@@ -1181,7 +1183,9 @@ int create_sstack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stac
         std::make_heap(heap.begin(), heap.end(), later);
         for (size_t t = 0; t < tasks.size(); ++t) {
             const xt::SStackTask& k = tasks[t];
-            const double cost = 4096.0 + ((k.flags & 1) ? 8.0 * k.K : 1024.0 * k.nch * (k.flags >> 16));
+            // (M > 1 group tasks also read each chunk's M activation rows)
+            const double cost = 4096.0 + ((k.flags & 1) ? 8.0 * k.K
+                                                         : k.nch * (1024.0 * (k.flags >> 16) + (M > 1 ? 320.0 * M : 0.0)));
             std::pop_heap(heap.begin(), heap.end(), later);
             per[(size_t)heap.back().second].push_back((int)t);
             heap.back().first += cost;
