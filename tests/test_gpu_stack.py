@@ -352,3 +352,22 @@ def test_stack_auto_plan_choice():
     assert st.plan_name == "per_op"
     run_and_compare([([m.w], x2, [y2], None)], [(0, ["p"], [y2], x2, {"p": m})], 17,
                     xtern.XT_QUANT_AVX512, reps=1, plan=None)
+
+
+@pytest.mark.parametrize("M", [1, 6])
+def test_stack_long_rows(M):
+    """in_dim well above the BitNet shapes (Pack4 16000, Pack5 12800 -> 40
+    chunks of 320): the quantiser tasks take the row in several rounds and
+    the group tasks walk 63 / 40 chunks; chained in one launch."""
+    log(f"stack long rows M={M}")
+    rng = np.random.default_rng(zlib.crc32(b"long_rows") & 0xffff + M)
+    a = Mat(rng, 16000, 40)
+    b = Mat(rng, 40, 12800, pack5=False)
+    c = Mat(rng, 12800, 23, pack5=True)
+    x0 = torch.from_numpy(rng.standard_normal((M, 16000)).astype(np.float32)).cuda()
+    ya = torch.full((M, 40), float("nan"), device="cuda")
+    yb = torch.full((M, 12800), float("nan"), device="cuda")
+    yc = torch.full((M, 23), float("nan"), device="cuda")
+    ops = [([a.w], x0, [ya], None), ([b.w], ya, [yb], 0), ([c.w], yb, [yc], 1)]
+    checks = [(0, ["a"], [ya], x0, {"a": a}), (1, ["b"], [yb], ya, {"b": b}), (2, ["c"], [yc], yb, {"c": c})]
+    run_and_compare(ops, checks, M, xtern.XT_QUANT_SCALAR, reps=2)

@@ -1079,27 +1079,21 @@ int create_sstack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stac
         f.fmt = fmt == XT_PACK5 ? XT_PACK5 : XT_PACK4;
         f.K = (int)op.w[0]->K;
         f.nch = (int)op.w[0]->nch;
-        // (M > 1: each token's row fills whole 128-byte lines of its own;
-        // rows written on one XCD are read with ordinary loads on others)
-        f.ldq = M == 1 ? f.nch * ch : (int)align_up((size_t)f.nch * ch, 128);
+        // (each token's row fills whole 128-byte lines of its own: rows
+        // written on one XCD are read with ordinary loads on others)
+        f.ldq = (int)align_up((size_t)f.nch * ch, 128);
         f.qoff = scratch;
         scratch += align_up((size_t)M * f.ldq + 8 * (size_t)M, 256);  // rows, then sums and scales
         ntasks += (size_t)M + (size_t)f.ngroups;
         if (op.dep >= 0) pub[(size_t)op.dep] = 1;
     }
-    // 16-row groups per task: as many as keep about four tasks per wave of
-    // a full grid (a task's start is paid once per task; M > 1 reads a
-    // chunk's activation pieces once per task)
     int dev0 = 0, cus0 = 0;
     XT_HIP(hipGetDevice(&dev0));
     XT_HIP(hipDeviceGetAttribute(&cus0, hipDeviceAttributeMultiprocessorCount, dev0));
-    size_t all_groups = 0;
-    for (const OpInfo& f : info) all_groups += (size_t)f.ngroups;
-    // (at most 4: M = 1 a task's rows are one per lane of a wave; M > 1 its
-    // groups' tiles of one chunk are loaded together)
-    // M > 1: always 4 (the kernel loads and multiplies four groups' tiles per
-    // step, and shares the chunk's activation pieces among them)
-    const int rg = M > 1 ? 4 : (int)std::max<size_t>(1, std::min<size_t>(4, all_groups / ((size_t)cus0 * 16 * 4)));
+    // 16-row groups per task: 4 (the kernel loads and multiplies four
+    // groups' tiles per step and shares the chunk's activation pieces among
+    // them; measured faster than 2 groups per task at M = 1 too)
+    const int rg = 4;
     ntasks = (size_t)nops * (size_t)M;
     for (int i = 0; i < nops; ++i)
         for (int p = 0; p < ops[i].n; ++p) ntasks += (size_t)(((ops[i].w[p]->N + 15) / 16 + rg - 1) / rg);
@@ -1166,9 +1160,8 @@ int create_sstack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stac
     int per_cu = 0;
     int row_bytes = 1024;
     for (const OpInfo& f : info)
-        row_bytes = std::max(row_bytes, M == 1 ? (int)align_up((size_t)f.ldq, 1024)
-                                               : 16 * (xt::chunk_cols(f.fmt) + 16));
-    e = xt::sstack_blocks_per_cu((int)M, row_bytes, &per_cu);
+        row_bytes = std::max(row_bytes, 16 * (xt::chunk_cols(f.fmt) + 16));
+    e = xt::sstack_blocks_per_cu(row_bytes, &per_cu);
     if (e == hipSuccess && per_cu < 1) e = hipErrorInvalidConfiguration;
     const int grid = std::max(1, std::min(cus0 * std::min(per_cu, 4), ((int)tasks.size() + wpb - 1) / wpb));
     const int nw = grid * wpb;
@@ -1185,7 +1178,7 @@ int create_sstack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stac
             const xt::SStackTask& k = tasks[t];
             // (M > 1 group tasks also read each chunk's M activation rows)
             const double cost = 4096.0 + ((k.flags & 1) ? 8.0 * k.K
-                                                         : k.nch * (1024.0 * (k.flags >> 16) + (M > 1 ? 320.0 * M : 0.0)));
+                                                         : k.nch * (1024.0 * (k.flags >> 16) + 320.0 * M));
             std::pop_heap(heap.begin(), heap.end(), later);
             per[(size_t)heap.back().second].push_back((int)t);
             heap.back().first += cost;

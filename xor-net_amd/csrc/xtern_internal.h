@@ -174,7 +174,7 @@ int xs_max_rows();
 hipError_t scratch_region(void** ptr, size_t* bytes);
 // Streaming decode stack, M = 1 (xtern_sstack.hip).
 constexpr int kSStackMaxOps = 8191;          // op index: 13 bits of a task
-constexpr int kSStackMaxRowBytes = 9216;     // i8 row (nch * chunk columns) of one op, at most
+constexpr int kSStackMaxRowBytes = 32768;    // i8 row (nch * chunk columns) of one op, at most
 constexpr int kSStackMaxM = 16;              // tokens of the streaming stack (one MFMA block)
 // One task, 64 bytes: everything a wave needs to start it, loaded one task
 // ahead.  flags bits 0-15: 1 quantiser task, 2 other ops read the outputs
@@ -197,12 +197,11 @@ struct SStackArgs {
     const int* woff;          // [waves + 1]
     unsigned* ctr;            // (4 + 2 * nops) slots of 128 bytes, zero between launches
     int ntasks, nops, mode, spin_limit;
-    int row_bytes;            // LDS per wave: M = 1 the i8 row (the longest ldq, rounded to
-                              // 1 KiB); M > 1 one chunk of 16 token rows
+    int row_bytes;            // LDS per wave: one chunk of 16 token rows, padded
     int M;                    // tokens, 1..kSStackMaxM
 };
 hipError_t launch_sstack(const SStackArgs& a, int blocks, hipStream_t s);
-hipError_t sstack_blocks_per_cu(int M, int row_bytes, int* n);
+hipError_t sstack_blocks_per_cu(int row_bytes, int* n);
 int sstack_waves_per_block();
 // Persistent decode stack (xtern_stack.hip): one launch over a list of ops.
 constexpr int kStackRowGroupsMax = 8;       // 16-row groups per GEMV item (M > 1): stack_gemv_rg

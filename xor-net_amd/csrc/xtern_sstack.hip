@@ -1,5 +1,5 @@
-// Streaming decode stack (M = 1): a whole list of ternary projections in one
-// launch, every wave walking its own sequence of 16-row groups.
+// Streaming decode stack (M = 1 .. 16 tokens): a whole list of ternary
+// projections in one launch, every wave walking its own sequence of tasks.
 //
 // Reference behaviour: the layer loop of the BitNet decode step
 // (src/models/llama/mod.rs:420-470) calls TernaryLinear::forward /
@@ -8,33 +8,34 @@
 // quantisation (quantization.rs:95-195), the exact i32 dot of `dot_row`
 // (:216-231) over pack4 / pack5 / sparse weights, (f32)dot * inv * w_scale.
 //
-// Work list.  The host flattens the ops into tasks: one quantiser task per op
-// (the op's f32 input row -> i8 row, its exact sum and inverse scale) and one
-// task per block of consecutive 16-row groups of one projection.  Every task
-// follows the tasks it waits for: an op's quantiser task comes after the last
-// group of the op its input comes from, its groups after its quantiser task.
-// The host deals the list out to the waves in list order, each task to the
-// wave with the least work so far (weight bytes), and every wave runs its
-// tasks in list order.  The grid is no larger than what is resident at once,
-// so the wave holding the earliest unfinished task is running and has its
-// inputs, and the launch always finishes.  Waits are bounded anyway: one that
-// gives up sets a flag for the host, and all later waits of the launch return
-// at once.
+// Work list.  The host flattens the ops into tasks: one quantiser task per
+// op and token (the token's f32 input row -> i8 row, its exact sum and
+// inverse scale) and one task per block of four consecutive 16-row groups of
+// one projection.  Every task follows the tasks it waits for: an op's
+// quantiser tasks come after the last group of the op its input comes from,
+// its groups after its quantiser tasks.  The host deals the list out to the
+// waves in list order, each task to the wave with the least work so far
+// (weight bytes), and every wave runs its tasks in list order.  The grid is
+// no larger than what is resident at once, so the wave holding the earliest
+// unfinished task is running and has its inputs, and the launch always
+// finishes.  Waits are bounded anyway: one that gives up sets a flag for the
+// host, and all later waits of the launch return at once.
 //
-// A group task streams its nch weight tiles (1 KiB each) D at a time with the
-// row's i8 pieces in the wave's own LDS region (no barrier: a wave's LDS
-// accesses complete in order).  The loads that start a group -- the
-// quantiser-done count, the i8 row, its sum and scale, the w_scales and the
-// first D tiles -- are issued together; if the count shows the row not yet
-// written, the wave waits for it and loads the row again.  This is the
-// streaming GEMV's walk (xtern_gstream.hip) with the dependency checks added:
-// every wave keeps its own loads in flight, no workgroup-wide phases.
+// A group task walks its block chunk by chunk (ss_mblock): one step loads
+// the four groups' tiles of a chunk and the chunk's pieces of the op's M
+// quantised rows, stages the pieces in the wave's own LDS region (no
+// barrier: a wave's LDS accesses complete in order) and runs the four
+// groups' MFMAs on the same A fragments.  Every wave keeps its own loads in
+// flight, with no workgroup-wide phases; twelve waves per CU keep about
+// 48 KB of weights in flight.
 //
-// Coherence across the eight XCDs (each has its own L2): data one task writes
-// for another (quantised rows, outputs other ops read) is written and read
-// with device-scope accesses, and a count is bumped only after the writer's
-// stores have completed.  The last wave out resets the counts, so the next
-// launch starts from zero without a memset.
+// Coherence across the eight XCDs (each has its own L2): quantised rows are
+// written with device-scope stores and counted once the stores have
+// completed; readers load them only after the count shows all M tokens
+// done (see ss_mblock).  Outputs other ops read inside the launch are
+// written with device-scope stores and counted the same way.  The last wave
+// out resets the counts, so the next launch starts from zero without a
+// memset.
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
@@ -48,7 +49,6 @@ namespace xt {
 namespace {
 
 constexpr int kSsW = 4;   // waves per workgroup
-constexpr int kSsD = 2;   // tiles per batch
 constexpr int kSsKnownWords = kSStackMaxOps / 32 + 1;
 
 __device__ __forceinline__ unsigned* ss_ctr(unsigned* c, int slot) { return c + slot * 32; }
@@ -212,144 +212,7 @@ __device__ void ss_quant(const SStackArgs& a, const Rec& r) {
                                __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// A block of r.ngroups consecutive 16-row groups of one projection, each over
-// all of K; areg: this wave's LDS region for the i8 row (loaded once per
-// block).
-template <int FMT>
-__device__ void ss_block(const SStackArgs& a, const Rec& r, uint32_t areg, unsigned* known) {
-    constexpr int STEPS = (FMT == XT_PACK5) ? 5 : 4;
-    constexpr int CH = STEPS * 64;
-    constexpr int kPieces = kSStackMaxRowBytes / 1024;  // 16-byte row pieces per lane, at most
-    const int lane = threadIdx.x & 63;
-    const int g = lane >> 4;
-    const int nch = r.nch, opi = r.opi;
-    const int npieces = r.ldq / 16;
-    const uint8_t* const tl = r.tiles + lane * 16;
-    unsigned* const qdone = ss_ctr(a.ctr, kSsDone0 + a.nops + opi);
-    const bool seen = (known[opi >> 5] >> (opi & 31)) & 1u;
-
-    // the loads that start the block, issued together (the count first).
-    // Values every lane needs (the count, the row's sum and scale) are loaded
-    // by one or two lanes and broadcast: device-scope loads bypass the
-    // per-CU cache, so 64 lanes loading one word would send 64 requests
-    // to one L2 line.
-    const __amdgpu_buffer_rsrc_t qr = ss_rsrc(r.q, (unsigned)(r.ldq + 8));
-    unsigned ready = 1u;
-    if (!seen && lane == 0) ready = ss_ld_coh(qdone);
-    v4i pc[kPieces];
-    unsigned ri = 0;  // lane 0: the row's sum, lane 1: its inverse scale
-    auto load_row = [&]() {
-#pragma unroll
-        for (int u = 0; u < kPieces; ++u) {
-            const int i = lane + 64 * u;
-            if (64 * u < npieces)  // (uniform)
-                pc[u] = ss_ld_coh16(qr, i < npieces ? (unsigned)i * 16u : 0x80000000u);
-        }
-        if (lane < 2) ri = (unsigned)__builtin_amdgcn_raw_buffer_load_b32(qr, (unsigned)(r.ldq + 4 * lane), 0, kSsCoh);
-    };
-    load_row();
-    // lane l holds row l of the task (group l / 16): its w_scale now, its dot
-    // once that group is done; the outputs are stored together at the end
-    const int trows = (r.ngroups - 1) * 16 + r.nrows;
-    const float wsc = ((gfloat*)(uintptr_t)r.ws)[min(lane, trows - 1)];
-    int dot = 0;
-    v4i wb[kSsD];
-#pragma unroll
-    for (int s = 0; s < kSsD; ++s)
-        wb[s] = ss_ld_tile(tl + (size_t)min(s, nch - 1) * kTileBytes);
-    if (!seen) {
-        ready = __builtin_amdgcn_readfirstlane(ready);
-        if (ready < 1u) {  // (uniform) not quantised yet: wait, then load the row again
-            if (lane == 0) ss_wait(qdone, 1u, ss_ctr(a.ctr, kSsError), a.spin_limit);
-            __builtin_amdgcn_wave_barrier();
-            load_row();
-        }
-        if (lane == 0) atomicOr(&known[opi >> 5], 1u << (opi & 31));
-    }
-    const int rsum = __builtin_amdgcn_readlane((int)ri, 0);
-    const float inv = __int_as_float(__builtin_amdgcn_readlane((int)ri, 1));
-    // the row into this wave's LDS region (its own LDS accesses complete in
-    // order: the reads below see these stores, and the previous task's reads
-    // came before them)
-#pragma unroll
-    for (int u = 0; u < kPieces; ++u) {
-        const int i = lane + 64 * u;
-        if (i < npieces)
-            *reinterpret_cast<__attribute__((address_space(3))) v4i*>((uintptr_t)(areg + (uint32_t)i * 16u)) = pc[u];
-    }
-    const uint32_t abase = areg + (uint32_t)(g * 16);
-    const bool pub = (r.flags & kSsPub) != 0;
-
-    for (int gi = 0; gi < r.ngroups; ++gi) {
-        const uint8_t* const tg = tl + (size_t)gi * nch * kTileBytes;
-        if (gi > 0) {  // (the first group's tiles came with the row)
-#pragma unroll
-            for (int s = 0; s < kSsD; ++s)
-                wb[s] = ss_ld_tile(tg + (size_t)min(s, nch - 1) * kTileBytes);
-        }
-        v4i acc[STEPS];
-#pragma unroll
-        for (int st = 0; st < STEPS; ++st) acc[st] = v4i{0, 0, 0, 0};
-        for (int t0 = 0; t0 < nch; t0 += kSsD) {
-            if (t0 > 0) {
-#pragma unroll
-                for (int s = 0; s < kSsD; ++s)
-                    wb[s] = ss_ld_tile(tg + (size_t)min(t0 + s, nch - 1) * kTileBytes);
-            }
-#pragma unroll
-            for (int s = 0; s < kSsD; ++s) {
-                if (t0 + s >= nch) break;  // (uniform)
-                const uint32_t ab = abase + (uint32_t)((t0 + s) * CH);
-                if constexpr (FMT == XT_PACK5) {
-                    int E[4], O[4];
-#pragma unroll
-                    for (int q = 0; q < 4; ++q) {
-                        E[q] = wb[s][q] & 0x00ff00ff;
-                        O[q] = ((unsigned)wb[s][q] >> 8) & 0x00ff00ff;
-                    }
-#pragma unroll
-                    for (int st = 0; st < STEPS; ++st) {
-                        v4i b;
-#pragma unroll
-                        for (int q = 0; q < 4; ++q) {
-                            const int pE = E[q] * 3, pO = O[q] * 3;
-                            b[q] = (int)__builtin_amdgcn_perm((unsigned)pO, (unsigned)pE, 0x07030501u);
-                            E[q] = pE & 0x00ff00ff;
-                            O[q] = pO & 0x00ff00ff;
-                        }
-                        acc[st] = mfma(ss_lds16(ab + st * 64), b, acc[st]);
-                    }
-                } else {
-#pragma unroll
-                    for (int st = 0; st < STEPS; ++st)
-                        acc[st] = mfma(ss_lds16(ab + st * 64), decode4(wb[s][st]), acc[st]);
-                }
-            }
-        }
-        int sum = acc[0][0];
-#pragma unroll
-        for (int st = 1; st < STEPS; ++st) sum += acc[st][0];
-        // token 0 sits in element 0 of lanes 0-15 (row j); lane l takes row
-        // l % 16 of group l / 16
-        const int v = __builtin_amdgcn_ds_bpermute((lane & 15) << 2, sum);
-        if ((lane >> 4) == gi) dot = v;
-    }
-    // the MFMAs took codes w + 1, so the row's sum comes off
-    // (layers.rs:340: (dot as f32 * inv) * w_scale)
-    if (lane < trows) {
-        const float v = __fmul_rn(__fmul_rn((float)(dot - rsum), inv), wsc);
-        if (pub) ss_st_coh4(ss_rsrc(r.y, (unsigned)trows * 4u), (unsigned)lane * 4u, __float_as_uint(v));
-        else ((gfloat_w*)(uintptr_t)r.y)[lane] = v;
-    }
-    if (pub) {  // another op reads these outputs inside the launch
-        __builtin_amdgcn_s_waitcnt(0);
-        if (lane == 0)
-            __hip_atomic_fetch_add(ss_ctr(a.ctr, kSsDone0 + opi), (unsigned)r.ngroups, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
-    }
-}
-
-// M > 1 (up to 16 tokens): a block of r.ngroups (<= kSsR) consecutive
+// A group task (M up to 16 tokens): a block of r.ngroups (<= kSsR) consecutive
 // 16-row groups of one projection, walked chunk by chunk: each step loads
 // the block's tiles of one chunk (one per group) and the chunk's 16-byte
 // pieces of the M quantised rows, puts the pieces in this wave's LDS region
@@ -361,7 +224,7 @@ __device__ void ss_block(const SStackArgs& a, const Rec& r, uint32_t areg, unsig
 // empty of them), every token's row starts on its own 128-byte line (the
 // host pads the row pitch), so its L2 holds no stale copy, and later tasks
 // of the op on the XCD hit in it.
-constexpr int kSsR = 4;  // 16-row groups per task, at most (M > 1)
+constexpr int kSsR = 4;  // 16-row groups per task, at most
 template <int FMT>
 __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsigned* known) {
     constexpr int STEPS = (FMT == XT_PACK5) ? 5 : 4;
@@ -486,10 +349,9 @@ __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsi
     }
 }
 
-// MT: the M > 1 group tasks (ss_mblock), else M = 1 (ss_block); one
-// instantiation per form, so each has the registers to itself.
-template <bool MT>
-__global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(MT ? 3 : 4))) void sstack_kernel(const SStackArgs a) {
+// (three waves per SIMD: 168 registers for a task's tiles, activation
+// pieces, A fragments and the four groups' accumulators)
+__global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(3))) void sstack_kernel(const SStackArgs a) {
     __shared__ unsigned known[kSsKnownWords];  // ops this workgroup has seen quantised
     extern __shared__ __align__(16) uint8_t rows[];  // [kSsW][a.row_bytes]: each wave's i8 row
     for (int i = threadIdx.x; i < kSsKnownWords; i += kSsW * 64) known[i] = 0u;
@@ -508,12 +370,10 @@ __global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(MT ? 
         if (cur.flags & kSsQuant) {
             if (a.mode == XT_QUANT_AVX512) ss_quant<XT_QUANT_AVX512>(a, cur);
             else ss_quant<XT_QUANT_SCALAR>(a, cur);
-        } else if constexpr (MT) {
-            if (cur.flags & kSsPack5) ss_mblock<XT_PACK5>(a, cur, areg, known);
-            else ss_mblock<XT_PACK4>(a, cur, areg, known);
+        } else if (cur.flags & kSsPack5) {
+            ss_mblock<XT_PACK5>(a, cur, areg, known);
         } else {
-            if (cur.flags & kSsPack5) ss_block<XT_PACK5>(a, cur, areg, known);
-            else ss_block<XT_PACK4>(a, cur, areg, known);
+            ss_mblock<XT_PACK4>(a, cur, areg, known);
         }
     }
     // the last wave out resets the counts for the next launch (its own
@@ -531,23 +391,19 @@ __global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(MT ? 
 
 }  // namespace
 
-// LDS beyond the static part: every wave's i8 row region (the stack's
-// longest row, rounded to 1 KiB).
+// LDS beyond the static part: every wave's region for one chunk of 16
+// token rows.
 static size_t ss_dyn_lds(int row_bytes) { return (size_t)kSsW * row_bytes; }
 
 hipError_t launch_sstack(const SStackArgs& a, int blocks, hipStream_t s) {
     if (a.M < 1 || a.M > kSStackMaxM) return hipErrorInvalidValue;
-    if (a.M > 1)
-        hipLaunchKernelGGL(sstack_kernel<true>, dim3(blocks), dim3(kSsW * 64), ss_dyn_lds(a.row_bytes), s, a);
-    else
-        hipLaunchKernelGGL(sstack_kernel<false>, dim3(blocks), dim3(kSsW * 64), ss_dyn_lds(a.row_bytes), s, a);
+    hipLaunchKernelGGL(sstack_kernel, dim3(blocks), dim3(kSsW * 64), ss_dyn_lds(a.row_bytes), s, a);
     return hipGetLastError();
 }
 
-hipError_t sstack_blocks_per_cu(int M, int row_bytes, int* n) {
-    const void* k = M > 1 ? reinterpret_cast<const void*>(sstack_kernel<true>)
-                          : reinterpret_cast<const void*>(sstack_kernel<false>);
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(n, k, kSsW * 64, ss_dyn_lds(row_bytes));
+hipError_t sstack_blocks_per_cu(int row_bytes, int* n) {
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(n, reinterpret_cast<const void*>(sstack_kernel),
+                                                        kSsW * 64, ss_dyn_lds(row_bytes));
 }
 
 int sstack_waves_per_block() { return kSsW; }
