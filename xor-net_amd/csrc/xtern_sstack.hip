@@ -243,6 +243,15 @@ __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsi
         __builtin_amdgcn_wave_barrier();
         if (lane == 0) atomicOr(&known[opi >> 5], 1u << (opi & 31));
     }
+    // Loaded now, used by the epilogue (loaded there, they would stall every
+    // task's end on a memory latency with nothing else in flight): lane l <
+    // 2M slot l of the op's M row sums and M inverse scales (device-scope
+    // loads: those slots share lines that quantiser tasks on other XCDs
+    // wrote); lane l the w_scale of row l of the block.
+    const int trows = (ng - 1) * 16 + r.nrows;
+    const __amdgpu_buffer_rsrc_t sr = ss_rsrc(r.q + (size_t)M * ldq, (unsigned)(8 * M));
+    const int sv = (int)__builtin_amdgcn_raw_buffer_load_b32(sr, lane < 2 * M ? 4u * lane : 0x80000000u, 0, kSsCoh);
+    const int wv = __float_as_int(((gfloat*)(uintptr_t)r.ws)[min(lane, trows - 1)]);
     // the activation pieces of one chunk: piece p = lane + 64 u is token
     // p / PR, bytes (p % PR) * 16; tokens >= M read nothing (outside the
     // resource) and leave rows of the LDS region the outputs never use
@@ -305,23 +314,19 @@ __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsi
             }
         }
     }
-    // the row sums and inverse scales of tokens 4g .. 4g + 3 (this lane's
-    // outputs), and the w_scales of row j of each group
-    // (device-scope loads: the M tokens' slots share lines that quantiser
-    // tasks on other XCDs wrote)
-    const __amdgpu_buffer_rsrc_t sr = ss_rsrc(r.q + (size_t)M * ldq, (unsigned)(8 * M));
+    // this lane's outputs: tokens 4g .. 4g + 3, row j of each group
     int rs[4];
     float inv[4];
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
-        const unsigned tk = (unsigned)min(4 * g + t, M - 1);
-        rs[t] = (int)__builtin_amdgcn_raw_buffer_load_b32(sr, 4u * tk, 0, kSsCoh);
-        inv[t] = __int_as_float((int)__builtin_amdgcn_raw_buffer_load_b32(sr, 4u * (tk + M), 0, kSsCoh));
+        const int tk = min(4 * g + t, M - 1);
+        rs[t] = __builtin_amdgcn_ds_bpermute(4 * tk, sv);
+        inv[t] = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (tk + M), sv));
     }
-    const int trows = (ng - 1) * 16 + r.nrows;
     float wsc[kSsR];
 #pragma unroll
-    for (int gi = 0; gi < kSsR; ++gi) wsc[gi] = ((gfloat*)(uintptr_t)r.ws)[min(gi * 16 + j, trows - 1)];
+    for (int gi = 0; gi < kSsR; ++gi)
+        wsc[gi] = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * min(gi * 16 + j, trows - 1), wv));
 
     // acc[gi][t]: token 4g + t, row j of group gi; the MFMAs took codes w + 1,
     // so the token's sum comes off (layers.rs:340: (dot as f32 * inv) * w_scale)
