@@ -268,7 +268,9 @@ def gemv_sustained(np, torch, xtern, rng, ncopies=121, reps=10):
     y1 = torch.empty((M, N), dtype=torch.float32, device="cuda")
     xtern.linear_q(w1, q, inv, out=y1)
     torch.cuda.synchronize()
-    g = Graph(torch, lambda i: xtern.linear_q(w, q, inv, out=y), 1)
+    # four launches back to back per graph: launch-to-launch time, as for
+    # the per-call lines (a one-launch graph adds the replay's own gap)
+    g = Graph(torch, lambda i: xtern.linear_q(w, q, inv, out=y), 4)
     ms = g.time_ms(reps)
     if not torch.equal(y.view(ncopies, N), y1.expand(ncopies, N)):
         raise SystemExit("sustained GEMV: a copy's output differs from the single-matrix output")
@@ -283,7 +285,7 @@ def gemv_sustained(np, torch, xtern, rng, ncopies=121, reps=10):
     xs = [torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).cuda() for _ in range(ncopies)]
     ys = [torch.empty((M, N), dtype=torch.float32, device="cuda") for _ in range(ncopies)]
     st = xtern.Stack([([w_], x_, [y_], None) for w_, x_, y_ in zip(copies, xs, ys)], M)
-    gs = Graph(torch, lambda _i: st.run(), 1)
+    gs = Graph(torch, lambda _i: st.run(), 4)
     ms_st = gs.time_ms(reps)
     if st.gave_up():
         raise SystemExit("sustained stack: a dependency wait gave up")
@@ -469,8 +471,10 @@ def stack_c4(np, torch, xtern, rng, Ms=(1, 8, 32), layers=30):
                                ("chain_one_launch", ops_chain(), "one_launch")):
             st = xtern.Stack(ops, M, plan=plan)
             row[f"{tag}_plan"] = st.plan_name
-            gs = Graph(torch, lambda _i: st.run(), 1)
-            us_p = gs.time_ms(10) * 1e3
+            # runs back to back in one graph (launch to launch; the runs are
+            # ordered on the graph's stream, as the stack requires)
+            gs = Graph(torch, lambda _i: st.run(), 4)
+            us_p = gs.time_ms(3) * 1e3
             if st.gave_up():
                 raise SystemExit("decode stack: a dependency wait gave up")
             # bit-exact against one call per op, in list order (a chained

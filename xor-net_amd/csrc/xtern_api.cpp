@@ -1160,8 +1160,8 @@ int create_sstack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stac
     int per_cu = 0;
     int row_bytes = 1024;
     for (const OpInfo& f : info)
-        row_bytes = std::max(row_bytes, 16 * (xt::chunk_cols(f.fmt) + 16));
-    e = xt::sstack_blocks_per_cu(row_bytes, &per_cu);
+        row_bytes = std::max(row_bytes, xt::sstack_lds_rows((int)M) * (xt::chunk_cols(f.fmt) + 16));
+    e = xt::sstack_blocks_per_cu((int)M, row_bytes, &per_cu);
     if (e == hipSuccess && per_cu < 1) e = hipErrorInvalidConfiguration;
     const int grid = std::max(1, std::min(cus0 * std::min(per_cu, 4), ((int)tasks.size() + wpb - 1) / wpb));
     const int nw = grid * wpb;

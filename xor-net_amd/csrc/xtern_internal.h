@@ -197,11 +197,12 @@ struct SStackArgs {
     const int* woff;          // [waves + 1]
     unsigned* ctr;            // (4 + 2 * nops) slots of 128 bytes, zero between launches
     int ntasks, nops, mode, spin_limit;
-    int row_bytes;            // LDS per wave: one chunk of 16 token rows, padded
+    int row_bytes;            // LDS per wave: one chunk of the form's token rows, padded
     int M;                    // tokens, 1..kSStackMaxM
 };
 hipError_t launch_sstack(const SStackArgs& a, int blocks, hipStream_t s);
-hipError_t sstack_blocks_per_cu(int row_bytes, int* n);
+hipError_t sstack_blocks_per_cu(int M, int row_bytes, int* n);
+int sstack_lds_rows(int M);  // token rows of a wave's LDS region
 int sstack_waves_per_block();
 // Persistent decode stack (xtern_stack.hip): one launch over a list of ops.
 constexpr int kStackRowGroupsMax = 8;       // 16-row groups per GEMV item (M > 1): stack_gemv_rg

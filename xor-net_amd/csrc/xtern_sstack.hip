@@ -224,14 +224,19 @@ __device__ void ss_quant(const SStackArgs& a, const Rec& r) {
 // empty of them), every token's row starts on its own 128-byte line (the
 // host pads the row pitch), so its L2 holds no stale copy, and later tasks
 // of the op on the XCD hit in it.
+//
+// MT: token rows the LDS region holds (4 for M <= 4, else 16).  PF: the next
+// chunk's activation pieces are loaded during this step (registers allowing:
+// MT = 4), so a step stages its pieces in LDS and reads its A fragments while
+// its tiles are still in flight.
 constexpr int kSsR = 4;  // 16-row groups per task, at most
-template <int FMT>
+template <int FMT, int MT, bool PF>
 __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsigned* known) {
     constexpr int STEPS = (FMT == XT_PACK5) ? 5 : 4;
     constexpr int CH = STEPS * 64;
     constexpr int LDR = CH + 16;       // LDS bytes per token row of a chunk
     constexpr int PR = CH / 16;        // 16-byte pieces per token row of a chunk
-    constexpr int kAP = (16 * PR) / 64;  // pieces per lane for 16 token rows
+    constexpr int kAP = (MT * PR + 63) / 64;  // pieces per lane for MT token rows
     const int lane = threadIdx.x & 63;
     const int g = lane >> 4, j = lane & 15;
     const int M = a.M, nch = r.nch, opi = r.opi, ldq = r.ldq, N = r.K;
@@ -258,30 +263,38 @@ __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsi
     const __amdgpu_buffer_rsrc_t qr = ss_rsrc(r.q, (unsigned)(M * ldq));
     auto ptok = [&](int u) { return (lane + 64 * u) / PR; };
     auto pcol = [&](int u) { return ((lane + 64 * u) % PR) * 16; };
-    const uint32_t abase = areg + (uint32_t)(j * LDR + g * 16);
+    // (rows >= MT of the A fragment: the last row again, never stored)
+    const uint32_t abase = areg + (uint32_t)(min(j, MT - 1) * LDR + g * 16);
     const uint8_t* const tl = reinterpret_cast<const uint8_t*>(r.tiles) + lane * 16;
-    v4i acc[kSsR];
-#pragma unroll
-    for (int gi = 0; gi < kSsR; ++gi) acc[gi] = v4i{0, 0, 0, 0};
-    for (int c = 0; c < nch; ++c) {
-        v4i wb[kSsR], ap[kAP];
-#pragma unroll
-        for (int gi = 0; gi < kSsR; ++gi)  // (groups past the block: its last group again, unused)
-            wb[gi] = ss_ld_tile(tl + ((size_t)min(gi, ng - 1) * nch + c) * kTileBytes);
+    auto load_act = [&](v4i* ap, int c) {  // (chunks past nch read nothing)
 #pragma unroll
         for (int u = 0; u < kAP; ++u) {
             const int tk = ptok(u);
-            const unsigned go = tk < M ? (unsigned)(tk * ldq + pcol(u) + c * CH) : 0x80000000u;
+            const unsigned go = (tk < M && c < nch) ? (unsigned)(tk * ldq + pcol(u) + c * CH) : 0x80000000u;
             ap[u] = __builtin_amdgcn_raw_buffer_load_b128(qr, go, 0, 0);
         }
+    };
+    v4i acc[kSsR];
+#pragma unroll
+    for (int gi = 0; gi < kSsR; ++gi) acc[gi] = v4i{0, 0, 0, 0};
+    v4i ap[kAP];
+    if constexpr (PF) load_act(ap, 0);
+    for (int c = 0; c < nch; ++c) {
+        v4i wb[kSsR], apn[kAP];
+#pragma unroll
+        for (int gi = 0; gi < kSsR; ++gi)  // (groups past the block: its last group again, unused)
+            wb[gi] = ss_ld_tile(tl + ((size_t)min(gi, ng - 1) * nch + c) * kTileBytes);
+        if constexpr (PF) load_act(apn, c + 1);
+        else load_act(ap, c);
         // (every load of the step is issued before anything waits for one)
         __builtin_amdgcn_sched_barrier(0);
         // (the previous chunk's LDS reads were issued before these writes,
         // and a wave's LDS accesses complete in order)
 #pragma unroll
         for (int u = 0; u < kAP; ++u)
-            *reinterpret_cast<__attribute__((address_space(3))) v4i*>(
-                (uintptr_t)(areg + (uint32_t)(ptok(u) * LDR + pcol(u)))) = ap[u];
+            if (64 * (u + 1) <= MT * PR || ptok(u) < MT)  // (the region holds MT rows)
+                *reinterpret_cast<__attribute__((address_space(3))) v4i*>(
+                    (uintptr_t)(areg + (uint32_t)(ptok(u) * LDR + pcol(u)))) = ap[u];
         v4i af[STEPS];
 #pragma unroll
         for (int st = 0; st < STEPS; ++st) af[st] = ss_lds16(abase + st * 64);
@@ -312,6 +325,10 @@ __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsi
 #pragma unroll
                 for (int st = 0; st < STEPS; ++st) acc[gi] = mfma(af[st], decode4(wb[gi][st]), acc[gi]);
             }
+        }
+        if constexpr (PF) {
+#pragma unroll
+            for (int u = 0; u < kAP; ++u) ap[u] = apn[u];
         }
     }
     // this lane's outputs: tokens 4g .. 4g + 3, row j of each group
@@ -354,8 +371,10 @@ __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsi
     }
 }
 
-// (three waves per SIMD: 168 registers for a task's tiles, activation
-// pieces, A fragments and the four groups' accumulators)
+// MT: the token form (see ss_mblock).  Three waves per SIMD: up to 168
+// registers for a task's tiles, activation pieces, A fragments and the four
+// groups' accumulators.
+template <int MT>
 __global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(3))) void sstack_kernel(const SStackArgs a) {
     __shared__ unsigned known[kSsKnownWords];  // ops this workgroup has seen quantised
     extern __shared__ __align__(16) uint8_t rows[];  // [kSsW][a.row_bytes]: each wave's i8 row
@@ -376,9 +395,9 @@ __global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(3))) 
             if (a.mode == XT_QUANT_AVX512) ss_quant<XT_QUANT_AVX512>(a, cur);
             else ss_quant<XT_QUANT_SCALAR>(a, cur);
         } else if (cur.flags & kSsPack5) {
-            ss_mblock<XT_PACK5>(a, cur, areg, known);
+            ss_mblock<XT_PACK5, MT, MT == 4>(a, cur, areg, known);
         } else {
-            ss_mblock<XT_PACK4>(a, cur, areg, known);
+            ss_mblock<XT_PACK4, MT, MT == 4>(a, cur, areg, known);
         }
     }
     // the last wave out resets the counts for the next launch (its own
@@ -396,19 +415,25 @@ __global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(3))) 
 
 }  // namespace
 
-// LDS beyond the static part: every wave's region for one chunk of 16
-// token rows.
+// LDS beyond the static part: every wave's region for one chunk of the
+// form's token rows.
 static size_t ss_dyn_lds(int row_bytes) { return (size_t)kSsW * row_bytes; }
+
+int sstack_lds_rows(int M) { return M <= 4 ? 4 : 16; }
 
 hipError_t launch_sstack(const SStackArgs& a, int blocks, hipStream_t s) {
     if (a.M < 1 || a.M > kSStackMaxM) return hipErrorInvalidValue;
-    hipLaunchKernelGGL(sstack_kernel, dim3(blocks), dim3(kSsW * 64), ss_dyn_lds(a.row_bytes), s, a);
+    if (a.M <= 4)
+        hipLaunchKernelGGL(sstack_kernel<4>, dim3(blocks), dim3(kSsW * 64), ss_dyn_lds(a.row_bytes), s, a);
+    else
+        hipLaunchKernelGGL(sstack_kernel<16>, dim3(blocks), dim3(kSsW * 64), ss_dyn_lds(a.row_bytes), s, a);
     return hipGetLastError();
 }
 
-hipError_t sstack_blocks_per_cu(int row_bytes, int* n) {
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(n, reinterpret_cast<const void*>(sstack_kernel),
-                                                        kSsW * 64, ss_dyn_lds(row_bytes));
+hipError_t sstack_blocks_per_cu(int M, int row_bytes, int* n) {
+    const void* k = M <= 4 ? reinterpret_cast<const void*>(sstack_kernel<4>)
+                           : reinterpret_cast<const void*>(sstack_kernel<16>);
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(n, k, kSsW * 64, ss_dyn_lds(row_bytes));
 }
 
 int sstack_waves_per_block() { return kSsW; }
