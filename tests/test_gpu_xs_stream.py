@@ -101,8 +101,16 @@ def test_stream_refused_where_unsupported():
     t = sparse_tern(rng, N, K)
     blob = np.frombuffer(xtern.encode_sparse_tensor(t, K, N)[0], np.uint8)
     w = xtern.DeviceWeights(xtern.XT_XORSPARSE_STREAM, K, N, blob, np.ones(N, np.float32))
+    x = torch.randn(1, K, device=DEV)
+    y = torch.zeros(1, N, device=DEV)
+    # the one-launch stack kernels take tile formats only; the automatic plan
+    # runs a compact-stream op as its own call
     with pytest.raises(xtern.XternError, match="stack weights"):
-        xtern.Stack([([w], torch.zeros(1, K, device=DEV), [torch.zeros(1, N, device=DEV)], None)], 1)
+        xtern.Stack([([w], x, [y], None)], 1, plan="one_launch")
+    st = xtern.Stack([([w], x, [y], None)], 1)
+    assert st.plan_name == "per_op"
+    st.run()
+    check_bits(y.cpu().numpy(), xtern.linear_f32(w, x).cpu().numpy(), "per-op stack vs call")
     big = sparse_tern(rng, 1, 16384 + 64)
     with pytest.raises(xtern.XternError, match="in_dim up to 16384"):
         xtern.DeviceWeights(xtern.XT_XORSPARSE_STREAM, 16384 + 64, 1,

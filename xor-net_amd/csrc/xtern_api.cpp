@@ -1281,8 +1281,6 @@ namespace {
 // M > 1: the persistent item kernel's work list.
 int create_stack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stack** out) {
     const int rq = xt::stack_rows_per_quant_item();
-    const bool one = xt::stack_pipelined((int)M);  // M = 1: rows quantised once per op
-    int slots = 0;
     std::vector<xt::StackOpDev> dops((size_t)nops);
     size_t scratch = 0;
     std::vector<size_t> qoff((size_t)nops);
@@ -1297,9 +1295,7 @@ int create_stack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stack
             if (!op.w[p] || !op.y[p]) return fail(XT_ERR_INVALID, at + "NULL weights or output");
         xt::StackOpDev& d = dops[(size_t)i];
         memset(&d, 0, sizeof d);
-        // row groups per GEMV item (the M = 1 pipeline takes 8 for short K)
-        int rgi = xt::stack_gemv_rg((int)op.w[0]->nch);
-        if (one) slots = std::max(slots, xt::stack_one_slots((int)op.w[0]->nch, &rgi));
+        const int rgi = xt::stack_gemv_rg((int)op.w[0]->nch);  // row groups per GEMV item
         d.rg = rgi;
         int blocks = 0;
         for (int p = 0; p < op.n; ++p) {
@@ -1335,8 +1331,7 @@ int create_stack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stack
         if (op.dep >= 0) dops[(size_t)op.dep].pub = 1;
         if (d.nq > 0) {
             qoff[(size_t)i] = scratch;
-            scratch += align_up((size_t)M * d.ldq, 256) + align_up((size_t)M * 4, 256) +
-                       (one ? align_up((size_t)M * 128, 256) : 0);
+            scratch += align_up((size_t)M * d.ldq, 256) + align_up((size_t)M * 4, 256);
         }
     }
     // Work list: each op's GEMV items in op order; an op's quantiser items
@@ -1393,7 +1388,7 @@ int create_stack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stack
     int dev = 0, cus = 0, per_cu = 0;
     XT_HIP(hipGetDevice(&dev));
     XT_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    XT_HIP(xt::stack_blocks_per_cu((int)M, slots, &per_cu));
+    XT_HIP(xt::stack_blocks_per_cu(&per_cu));
     if (per_cu < 1) return fail(XT_ERR_UNSUPPORTED, "stack kernel does not fit a CU");
     // Every workgroup resident at once (see xtern_stack.hip): grid = occupancy.
     int grid = std::min(cus * per_cu, (int)items.size());
@@ -1438,7 +1433,6 @@ int create_stack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stack
         const size_t qb = align_up((size_t)M * d.ldq, 256);
         d.q = reinterpret_cast<int8_t*>(sc + qoff[(size_t)i]);
         d.inv = reinterpret_cast<float*>(sc + qoff[(size_t)i] + qb);
-        if (one) d.csum = reinterpret_cast<int32_t*>(sc + qoff[(size_t)i] + qb + align_up((size_t)M * 4, 256));
     }
     e = hipMemcpy(mem, dops.data(), sizeof(xt::StackOpDev) * nops, hipMemcpyHostToDevice);
     if (e == hipSuccess)
@@ -1464,7 +1458,6 @@ int create_stack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stack
     st->args.nops = nops;
     st->args.M = (int)M;
     st->args.mode = mode;
-    st->args.slots = slots;
     // polls (about a microsecond each) before a dependency wait gives up
     st->args.spin_limit = 1 << 20;
     st->blocks = grid;

@@ -204,7 +204,8 @@ hipError_t launch_sstack(const SStackArgs& a, int blocks, hipStream_t s);
 hipError_t sstack_blocks_per_cu(int M, int row_bytes, int* n);
 int sstack_lds_rows(int M);  // token rows of a wave's LDS region
 int sstack_waves_per_block();
-// Persistent decode stack (xtern_stack.hip): one launch over a list of ops.
+// Persistent decode stack for 17 <= M <= 32 (xtern_stack.hip): one launch over
+// a list of ops.
 constexpr int kStackRowGroupsMax = 8;       // 16-row groups per GEMV item (M > 1): stack_gemv_rg
 constexpr int kStackMaxOps = 4095;
 constexpr int kStackMaxWgItems = 1024;      // items one workgroup may be dealt
@@ -214,18 +215,17 @@ struct StackOpDev {
     const float* ws[4];
     float* y[4];              // [M][N[p]] outputs
     const float* x;           // [M][K] f32 input
-    int8_t* q;                // [M][ldq] quantised input (M > 1), launch scratch
+    int8_t* q;                // [M][ldq] quantised input, launch scratch
     float* inv;               // [M]
-    int32_t* csum;            // [M][32] sums of each 256-column chunk of q (M = 1 launch)
     int N[4];
     int gend[4];              // cumulative GEMV items per projection
     int nproj, K, nch, ldq;
     int dep;                  // op whose outputs x reads (wait for all its GEMV items), or -1
     int dep_items;            // that op's GEMV item count
-    int nq;                   // quantiser items (M > 1: ceil(M / rows per item), else 0)
+    int nq;                   // quantiser items: ceil(M / rows per item)
     int ngemv;                // GEMV items
     int pub;                  // another op depends on this one: count its completions
-    int rg;                   // 16-row groups per GEMV item (4, or 8 for short K at M = 1)
+    int rg;                   // 16-row groups per GEMV item (stack_gemv_rg)
 };
 struct StackArgs {
     const StackOpDev* ops;
@@ -234,18 +234,13 @@ struct StackArgs {
     unsigned* ctr;            // (4 + 2 * nops) slots of 128 bytes, zero between launches
     int nitems, nops, M, mode;
     int spin_limit;           // polls before a dependency wait gives up
-    int slots;                // M = 1: chunk slots per wave the ops need
 };
 int stack_threads();
 int stack_max_chunks();  // chunks of K an op may have (4 per wave)
 int stack_gemv_rg(int nch);  // row groups per GEMV item of the M > 1 kernel
 int stack_rows_per_quant_item();
 hipError_t launch_stack(const StackArgs& a, int blocks, hipStream_t s);
-hipError_t stack_blocks_per_cu(int M, int slots, int* n);
-// M = 1 pipelined launch: chunk slots per wave an op of nch chunks needs, and
-// its row groups per item (*rg); whether a launch of M rows takes it.
-int stack_one_slots(int nch, int* rg);
-bool stack_pipelined(int M);
+hipError_t stack_blocks_per_cu(int* n);
 // HF prepacked striped bytes [N/f][K] (device) -> tiles (device).
 hipError_t launch_hf_tiles(int fmt, const uint8_t* stored, int64_t K, int64_t N, uint8_t* tiles,
                            hipStream_t s);

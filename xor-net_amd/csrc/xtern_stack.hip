@@ -1,4 +1,5 @@
-// Persistent decode-stack kernel: one launch runs a whole list of ternary
+// Persistent decode-stack kernel for 17 to 32 tokens (up to 16 take the
+// streaming stack, xtern_sstack.hip): one launch runs a whole list of ternary
 // projections (a decode step's q/k/v, o, gate/up, down of every layer).
 //
 // Reference behaviour: the per-layer sequence of TernaryLinear::forward /
@@ -9,10 +10,9 @@
 // quantisation (quantization.rs:95-195), exact i32 dots, (f32)dot * inv *
 // w_scale.
 //
-// Work list.  The host flattens the ops into items: M > 1 ops have
-// quantiser items (kSW input rows each), every op has one GEMV item per block
-// of 8 (K up to 16 chunks) or 4 16-row groups of one of its projections (all
-// of K).  It then
+// Work list.  The host flattens the ops into items: every op has quantiser
+// items (kSW input rows each) and one GEMV item per block of 8 (K up to 16
+// chunks) or 4 16-row groups of one of its projections (all of K).  It then
 // deals the list out to the workgroups (greedy, by bytes), each workgroup
 // getting its items in list order, and every item after the items it waits
 // for.  With every workgroup of the launch resident at once (the grid is
@@ -114,9 +114,6 @@ struct Shared {
     unsigned desc[kDescLdsWords];          // every op descriptor
     unsigned items[kStackMaxWgItems];      // this workgroup's items, in order
     unsigned known[kKnownWords];           // completions this workgroup has seen
-    unsigned qrow[2][kSNT * 4];            // M = 1: the item's i8 input row (by parity)
-    unsigned csum[2][32];                  //        and its chunk sums
-    float wmax[kSW];
     unsigned last;
 };
 
@@ -170,11 +167,6 @@ __device__ __forceinline__ T* sgpr_ptr(T* p) {
 }
 __device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
-__device__ __forceinline__ bool known(const Shared& sh, int slot) {
-    // (one LDS word for the whole wave: uniform)
-    return (__builtin_amdgcn_readfirstlane(sh.known[slot >> 5]) >> (slot & 31)) & 1u;
-}
-
 // Wait (lane 0 of this wave; no workgroup barrier) until counter `slot`
 // (an op's GEMV completions: slot = op; its quantiser rows: nops + op)
 // reaches target, unless this workgroup has already seen it get there.
@@ -220,8 +212,6 @@ __device__ void quant_item(const StackArgs& a, Shared& sh, const OpRef& d, int o
     const float invs = (rmx > 0.0f) ? __fdiv_rn(rmx, 127.0f) : 1.0f;
     const int kmain = (K / 16) * 16;
     const __amdgpu_buffer_rsrc_t qr = rsrc(d.ptr<int8_t>(OPF(q)) + (size_t)m * ldq, (unsigned)ldq);
-    int32_t* csum = d.ptr<int32_t>(OPF(csum));
-    const __amdgpu_buffer_rsrc_t cr = rsrc(csum ? csum + (size_t)m * 32 : nullptr, csum ? 128u : 0u);
     const bool mine = wave < rows;
     auto body = [&](auto mode_c) {
         for (int f0 = 0; f0 < ldq / 4; f0 += 64) {  // one 256-column chunk per trip
@@ -233,11 +223,6 @@ __device__ void quant_item(const StackArgs& a, Shared& sh, const OpRef& d, int o
                 w |= (unsigned)(quant_one(__int_as_float(r[t]), scale, decltype(mode_c)::value,
                                           4 * f + t < kmain) & 255) << (8 * t);
             if (mine) st_buf(qr, (unsigned)f * 4u, w, true);
-            if (csum) {  // (uniform) the chunk's sum of quantised activations
-                const int cs = wave_reduce_bits(__builtin_amdgcn_sdot4((int)w, 0x01010101, 0, false),
-                                                [](int p_, int q_) { return p_ + q_; });
-                if (mine && lane == 0) st_buf(cr, (unsigned)(f0 / 64) * 4u, (unsigned)cs, true);
-            }
         }
     };
     if (a.mode == XT_QUANT_AVX512) body(std::integral_constant<int, XT_QUANT_AVX512>{});
@@ -252,11 +237,8 @@ __device__ void quant_item(const StackArgs& a, Shared& sh, const OpRef& d, int o
 
 // GEMV item: row groups G0 .. G0 + RG - 1 of projection p over all of K,
 // for every token.  Wave w multiplies chunks w, w + kSW, ... (NCW of them at
-// most).  ONE (M = 1): the item quantises the f32 input row itself in one
-// pass (each wave its own chunks' pieces, the row maximum through LDS), as
-// the decode GEMV does; otherwise it reads the rows the op's quantiser
-// items wrote.
-template <int NCW, bool ONE, int RG>
+// most), reading the rows the op's quantiser items wrote.
+template <int NCW, int RG>
 __device__ void gemv_item(const StackArgs& a, Shared& sh, const OpRef& d, int opi, int blk,
                           int pos) {
     const int lane = threadIdx.x & 63, wave = wave_id();
@@ -267,30 +249,11 @@ __device__ void gemv_item(const StackArgs& a, Shared& sh, const OpRef& d, int op
     const int b0 = p == 0 ? 0 : d.i(OPF(gend) + 4 * (p - 1));
     const int G0 = (blk - b0) * RG;
     const int N = d.i(OPF(N) + 4 * p), NG = (N + 15) >> 4;
-    const int nch = d.i(OPF(nch)), K = d.i(OPF(K)), M = a.M;
-    const int dep = d.i(OPF(dep));
+    const int nch = d.i(OPF(nch)), M = a.M;
     const bool pub = d.i(OPF(pub)) != 0;
     const __amdgpu_buffer_rsrc_t wr =
         rsrc(d.ptr<const uint8_t>(OPF(tiles) + 8 * p), (unsigned)(NG * nch * 1024));
-    const __amdgpu_buffer_rsrc_t xr = rsrc(d.ptr<const float>(OPF(x)), (unsigned)(K * 4));
     const unsigned voff = (unsigned)lane * 16u;
-
-    // ONE without a dependency: the input row is ready, so its pieces are
-    // requested first (they are needed first, for the row maximum); pieces
-    // past K read as zero
-    // (an input written before the launch takes cached loads; one written in
-    // this launch device-scope loads, first when its op is known complete)
-    v4i x0[NCW];
-    const bool x_first = ONE && (dep < 0 || known(sh, dep));
-    if (ONE && dep < 0) {
-#pragma unroll
-        for (int t = 0; t < NCW; ++t)
-            x0[t] = __builtin_amdgcn_raw_buffer_load_b128(xr, voff + (unsigned)(wave + t * kSW) * 1024u, 0, 0);
-    } else if (x_first) {
-#pragma unroll
-        for (int t = 0; t < NCW; ++t) x0[t] = ld_coh16(xr, voff, (unsigned)(wave + t * kSW) * 1024u);
-    }
-    __builtin_amdgcn_sched_barrier(0);
     v4i wv[NCW][RG];
 #pragma unroll
     for (int t = 0; t < NCW; ++t) {
@@ -303,59 +266,17 @@ __device__ void gemv_item(const StackArgs& a, Shared& sh, const OpRef& d, int op
     const int o = (G0 + min(wave, RG - 1)) * 16 + j;
     const float wscale = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(
         rsrc(d.ptr<const float>(OPF(ws) + 8 * p), (unsigned)(N * 4)), (unsigned)min(o, N - 1) * 4u, 0, 0));
-    if (ONE) {
-        if (!x_first) {  // written in this launch: device-scope loads after the wait
-            wave_wait(a, sh, dep, (unsigned)d.i(OPF(dep_items)));
-#pragma unroll
-            for (int t = 0; t < NCW; ++t) x0[t] = ld_coh16(xr, voff, (unsigned)(wave + t * kSW) * 1024u);
-        }
-    } else {
-        wave_wait(a, sh, a.nops + opi, (unsigned)M);
-    }
+    wave_wait(a, sh, a.nops + opi, (unsigned)M);
 
-    const int ntb = ONE ? 1 : (M + 15) >> 4;
+    const int ntb = (M + 15) >> 4;
     for (int tb = 0; tb < ntb; ++tb) {
         // the previous block's sums are read (its reduction stage doubles as
         // this block's activation slice)
         if (tb > 0) __syncthreads();
-        const int mt = ONE ? 1 : min(16, M - 16 * tb);  // tokens of this block
+        const int mt = min(16, M - 16 * tb);  // tokens of this block
         float invr[4];
-        unsigned w4[NCW];
-        v4i aq[ONE ? 1 : NCW][4];
-        if constexpr (ONE) {
-            float mx = 0.0f;
-#pragma unroll
-            for (int t = 0; t < NCW; ++t)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) mx = fmaxf(mx, fabsf(__int_as_float(x0[t][e])));
-            const int wm = wave_reduce_bits(__float_as_int(mx), [](int p_, int q_) {
-                return __float_as_int(fmaxf(__int_as_float(p_), __int_as_float(q_)));
-            });
-            if (lane == 0) sh.wmax[wave] = __int_as_float(wm);
-            __syncthreads();
-            float rmx = sh.wmax[0];
-#pragma unroll
-            for (int w = 1; w < kSW; ++w) rmx = fmaxf(rmx, sh.wmax[w]);
-            const float scale = (rmx > 0.0f) ? __fdiv_rn(127.0f, rmx) : 1.0f;
-            const float iv = (rmx > 0.0f) ? __fdiv_rn(rmx, 127.0f) : 1.0f;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) invr[r] = iv;
-            const int kmain = (K / 16) * 16;
-            auto pack = [&](auto mode_c) {
-#pragma unroll
-                for (int t = 0; t < NCW; ++t) {
-                    const int f = (wave + t * kSW) * 64 + lane;
-                    unsigned r = 0;
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)  // (zeros past K quantise to 0)
-                        r |= (unsigned)(quant_one(__int_as_float(x0[t][e]), scale, decltype(mode_c)::value,
-                                                  4 * f + e < kmain) & 255) << (8 * e);
-                    w4[t] = r;
-                }
-            };
-            if (a.mode == XT_QUANT_AVX512) pack(std::integral_constant<int, XT_QUANT_AVX512>{});
-            else pack(std::integral_constant<int, XT_QUANT_SCALAR>{});
-        } else {
+        v4i aq[NCW][4];
+        {
             const int ldq = d.i(OPF(ldq));
             const __amdgpu_buffer_rsrc_t qr = rsrc(d.ptr<const int8_t>(OPF(q)), (unsigned)(M * ldq));
             const __amdgpu_buffer_rsrc_t ir = rsrc(d.ptr<const float>(OPF(inv)), (unsigned)(M * 4));
@@ -401,21 +322,12 @@ __device__ void gemv_item(const StackArgs& a, Shared& sh, const OpRef& d, int op
         for (int r = 0; r < RG; ++r) acc[r] = v4i{0, 0, 0, 0};
 #pragma unroll
         for (int t = 0; t < NCW; ++t) {
-            // chunks past K: ONE's activations are zero there; the quantised
-            // rows of the other path are not, so those waves skip the chunk
-            const bool live = ONE || wave + t * kSW < nch;
+            // (chunks past K: the loads above clamp to the last chunk, so
+            // those waves skip it)
+            const bool live = wave + t * kSW < nch;
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
-                v4i av;
-                if constexpr (ONE) {
-                    // lane (g, j) of k-step s takes the chunk's packed pieces 16 s + 4 g + d
-#pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        av[e] = __builtin_amdgcn_ds_bpermute((16 * s + 4 * g + e) << 2, (int)w4[t]);
-                } else {
-                    av = aq[t][s];
-                }
-                const v4i x = (live && j < mt) ? av : v4i{0, 0, 0, 0};
+                const v4i x = (live && j < mt) ? aq[t][s] : v4i{0, 0, 0, 0};
 #pragma unroll
                 for (int r = 0; r < RG; ++r) {
                     v4i b = decode4(wv[t][r][s]);
@@ -453,260 +365,8 @@ __device__ void gemv_item(const StackArgs& a, Shared& sh, const OpRef& d, int op
     }
 }
 
-// ---------------------------------------------------------------------------
-// M = 1: software-pipelined items over rows quantised once per op.
-//
-// The op's quantiser item writes its input row as i8 plus the sum of each
-// 256-column chunk.  A GEMV item covers rg row groups (8 when K has at most
-// 16 chunks, else 4): wave w multiplies row group w % rg and the chunks c
-// with c % (8 / rg) == w / rg, so every wave holds one accumulator and at
-// most NS weight tiles, and all waves carry the same load.  Weights enter the
-// MFMA as codes (w + 1) and each wave subtracts the chunk sums of the chunks
-// it multiplied: the decode is 3 shifts and 4 ANDs per 16 weights.  The i8
-// row goes through LDS (double-buffered by item parity); the A fragment of a
-// k-step is one ds_read_b128 that the 16 token lanes share.
-//
-// While item k computes, item k + 1's weights and row are in flight: each
-// item issues the same number of loads (slots it does not need at an
-// out-of-range offset: zeros, no memory access), so the compiler's wait
-// counts stay exact and a wait for item k never waits for item k + 1.
-// ---------------------------------------------------------------------------
-template <int NS>
-struct OneBuf {
-    v4i w[NS];   // weight tiles of this wave's chunk slots
-    v4i q;       // 16 bytes of the i8 input row (thread t: bytes 16 t ..)
-    v4i cs;      // threads 0..7: chunk sums 4 t .. 4 t + 3
-    float inv;   // the row's inverse scale
-    float wsc;   // w_scale of this lane's output row (loaded with the tiles:
-                 // a load issued after the next item's would wait for them)
-};
-
-struct OneGeo {
-    int opi, p, G0, N, NG, nch, rg, dep_ready, pub;
-    int quant;  // a quantiser item (runs in the compute stage; its loads are empty)
-    // resources as base + size (built where used: resources kept in the
-    // struct would be copied through scratch memory)
-    const void* wp;
-    const void* qp;
-    const void* cp;
-    const void* ip;
-    unsigned wn, qn, cn, in_;
-    __device__ __forceinline__ __amdgpu_buffer_rsrc_t wr() const { return rsrc(wp, wn); }
-    __device__ __forceinline__ __amdgpu_buffer_rsrc_t qr() const { return rsrc(qp, qn); }
-    __device__ __forceinline__ __amdgpu_buffer_rsrc_t cr() const { return rsrc(cp, cn); }
-    __device__ __forceinline__ __amdgpu_buffer_rsrc_t ir() const { return rsrc(ip, in_); }
-};
-
-// k >= n gives an empty item (no chunks, empty resources).
-__device__ __forceinline__ OneGeo one_geo(const Shared& sh, int k, int n, int nops) {
-    OneGeo g;
-    if (k >= n) {
-        g.opi = g.p = g.G0 = 0;
-        g.N = g.NG = 1;
-        g.nch = 0;
-        g.rg = 8;
-        g.dep_ready = 1;
-        g.pub = 0;
-        g.quant = 0;
-        g.wp = g.qp = g.cp = g.ip = nullptr;
-        g.wn = g.qn = g.cn = g.in_ = 0u;
-        return g;
-    }
-    const unsigned it = __builtin_amdgcn_readfirstlane(sh.items[k]);
-    g.opi = (int)(it >> 20);
-    const OpRef d = load_op(sh, g.opi);
-    const int blk = (int)(it & 0xfffff) - d.i(OPF(nq));
-    if (blk < 0) {  // quantiser item
-        g.p = g.G0 = 0;
-        g.N = g.NG = 1;
-        g.nch = 0;
-        g.rg = 8;
-        g.dep_ready = 1;
-        g.pub = 0;
-        g.quant = 1;
-        g.wp = g.qp = g.cp = g.ip = nullptr;
-        g.wn = g.qn = g.cn = g.in_ = 0u;
-        return g;
-    }
-    g.quant = 0;
-    const int np = d.i(OPF(nproj));
-    const int ge0 = d.i(OPF(gend)), ge1 = d.i(OPF(gend) + 4), ge2 = d.i(OPF(gend) + 8);
-    g.p = (np > 1 && blk >= ge0) + (np > 2 && blk >= ge1) + (np > 3 && blk >= ge2);
-    const int b0 = g.p == 0 ? 0 : d.i(OPF(gend) + 4 * (g.p - 1));
-    g.rg = d.i(OPF(rg));
-    g.G0 = (blk - b0) * g.rg;
-    g.N = d.i(OPF(N) + 4 * g.p);
-    g.NG = (g.N + 15) >> 4;
-    g.nch = d.i(OPF(nch));
-    g.pub = d.i(OPF(pub));
-    g.dep_ready = known(sh, nops + g.opi);  // the op's row has been seen quantised
-    g.wp = d.ptr<const uint8_t>(OPF(tiles) + 8 * g.p);
-    g.wn = (unsigned)(g.NG * g.nch * 1024);
-    g.qp = d.ptr<const int8_t>(OPF(q));
-    g.qn = (unsigned)d.i(OPF(ldq));
-    g.cp = d.ptr<const int32_t>(OPF(csum));
-    g.cn = 128u;
-    g.ip = d.ptr<const float>(OPF(inv));
-    g.in_ = 4u;
-    return g;
-}
-
-// chunk of slot i for this wave, or -1
-__device__ __forceinline__ int one_chunk(const OneGeo& g, int wave, int i) {
-    const int per = kSW / g.rg;  // waves per row group: 1 or 2
-    const int c = (wave / g.rg) + per * i;
-    return c < g.nch ? c : -1;
-}
-
-template <int NS>
-__device__ __forceinline__ void one_issue_w(const Shared& sh, const OneGeo& g, OneBuf<NS>& B) {
-    const int wave = wave_id();
-    const unsigned voff = (unsigned)(threadIdx.x & 63) * 16u;
-    const int r = wave % g.rg;
-#pragma unroll
-    for (int i = 0; i < NS; ++i) {
-        const int c = one_chunk(g, wave, i);
-        B.w[i] = ld_w16(g.wr(), voff, c >= 0 ? (unsigned)(((g.G0 + r) * g.nch + c) * 1024) : kOutOfRange);
-    }
-    const int o = (g.G0 + r) * 16 + (int)(threadIdx.x & 15);
-    // (the scale pointer from the descriptor, read with every lane active;
-    // empty and quantiser items read nothing: a 0-byte resource)
-    const float* sp = load_op(sh, g.opi).ptr<const float>(OPF(ws) + 8 * g.p);
-    const unsigned sn = g.nch > 0 ? (unsigned)(g.N * 4) : 0u;
-    B.wsc = __int_as_float(
-        __builtin_amdgcn_raw_buffer_load_b32(rsrc(sp, sn), (unsigned)min(o, g.N - 1) * 4u, 0u, 0));
-}
-// The i8 row, chunk sums and scale (device scope: written in this launch);
-// out of range (zeros) when `now` is false, to be loaded again later.
-template <int NS>
-__device__ __forceinline__ void one_issue_q(const OneGeo& g, OneBuf<NS>& B, bool now) {
-    const unsigned t = threadIdx.x;
-    const unsigned so = now ? 0u : kOutOfRange;
-    B.q = ld_coh16(g.qr(), t * 16u, so);
-    B.cs = ld_coh16(g.cr(), (t & 7u) * 16u, so);
-    B.inv = __int_as_float(__builtin_amdgcn_raw_buffer_load_b32(g.ir(), so, 0, kAuxCoh));
-}
-
-template <int NS>
-__device__ __forceinline__ void one_pre(const StackArgs& a, Shared& sh, const OneGeo& g, OneBuf<NS>& B,
-                                        int pos) {
-    const bool now = g.dep_ready != 0;  // (quantiser and empty items: ready)
-    if (!now) wave_wait(a, sh, a.nops + g.opi, 1u);
-    OneBuf<NS> L;
-    one_issue_q<NS>(g, L, !now);
-    B.q = now ? B.q : L.q;
-    B.cs = now ? B.cs : L.cs;
-    B.inv = now ? B.inv : L.inv;
-}
-
-template <int NS>
-__device__ __forceinline__ void one_compute(const StackArgs& a, Shared& sh, const OneGeo& g,
-                                            OneBuf<NS>& B, int parity, int pos) {
-    if (g.quant) {  // (uniform)
-        quant_item(a, sh, load_op(sh, g.opi), g.opi, 0, 1u);
-        return;
-    }
-    const int lane = threadIdx.x & 63, wave = wave_id();
-    const int gq = lane >> 4, j = lane & 15;
-    unsigned* qb = sh.qrow[parity];
-    *reinterpret_cast<v4i*>(qb + threadIdx.x * 4) = B.q;
-    if (threadIdx.x < 8) *reinterpret_cast<v4i*>(sh.csum[parity] + threadIdx.x * 4) = B.cs;
-    const int r = wave % g.rg;
-    const int o = (g.G0 + r) * 16 + j;
-    // (read here, with every lane active: see load_op)
-    float* const yp = load_op(sh, g.opi).ptr<float>(OPF(y) + 8 * g.p);
-    __syncthreads();
-    v4i acc = v4i{0, 0, 0, 0};
-    int xsum = 0;
-#pragma unroll
-    for (int i = 0; i < NS; ++i) {
-        const int c = one_chunk(g, wave, i);
-        if (c >= 0) {  // (uniform)
-            xsum += (int)sh.csum[parity][c];
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-                const v4i av = *reinterpret_cast<const v4i*>(qb + (c * 256 + s * 64 + gq * 16) / 4);
-                acc = mfma(av, decode4(B.w[i][s]), acc);
-            }
-        }
-    }
-    acc[0] -= xsum;  // codes are w + 1 (token 0: element 0 of the lanes with gq == 0)
-    const bool split = g.rg == 4;  // two waves per row group: add through LDS
-    if (split) {
-        sh.red[wave][0][lane] = acc;
-        __syncthreads();
-    }
-    if (wave < g.rg && gq == 0 && g.G0 + r < g.NG && o < g.N) {
-        const int sum = split ? sh.red[wave][0][lane][0] + sh.red[wave + 4][0][lane][0] : acc[0];
-        // layers.rs:294 -- (dot as f32 * inv_scale) * w_scale; device-scope
-        // stores only where another op of the launch reads the output
-        const float v = __fmul_rn(__fmul_rn((float)sum, B.inv), B.wsc);
-        const __amdgpu_buffer_rsrc_t yr = rsrc(yp, (unsigned)(g.N * 4));
-        st_buf(yr, (unsigned)o * 4u, __float_as_uint(v), g.pub != 0);
-    }
-    if (g.pub) {  // another op reads these outputs inside the launch
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
-        if (threadIdx.x == 0)
-            __hip_atomic_fetch_add(done_ctr(a, g.opi), 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    } else if (split) {
-        __syncthreads();  // the reduction stage is read before the next item writes it
-    }
-}
-
-// (A quantiser item -- one per op, listed early -- runs in its compute slot.)
-template <int NS>
-__global__ __launch_bounds__(kSNT, 2) void stack_one_kernel(const StackArgs a) {
-    __shared__ Shared sh;
-    const int i0 = a.sched_off[blockIdx.x], n = a.sched_off[blockIdx.x + 1] - i0;
-    for (int i = threadIdx.x; i < n; i += kSNT) sh.items[i] = a.sched[i0 + i];
-    for (int i = threadIdx.x; i < a.nops * kDescWords; i += kSNT)
-        sh.desc[i] = reinterpret_cast<const unsigned*>(a.ops)[i];
-    for (int i = threadIdx.x; i < kKnownWords; i += kSNT) sh.known[i] = 0u;
-    __syncthreads();
-    const int k0 = 0, m = n;
-    OneBuf<NS> A, B;
-    OneGeo ga, gb;
-    auto item = [&](int k) { return k0 + k; };
-    ga = one_geo(sh, item(0), n, a.nops);
-    one_issue_q<NS>(ga, A, ga.dep_ready != 0);
-    one_issue_w<NS>(sh, ga, A);
-    // two items per trip: A holds item k, B item k + 1 (the next item's loads
-    // are issued on every trip, empty past the end)
-    for (int k = 0; k < m; k += 2) {
-        one_pre<NS>(a, sh, ga, A, i0 + item(k));
-        gb = one_geo(sh, item(k + 1), n, a.nops);
-        one_issue_q<NS>(gb, B, gb.dep_ready != 0);
-        one_issue_w<NS>(sh, gb, B);
-        one_compute<NS>(a, sh, ga, A, 0, i0 + item(k));
-        if (k + 1 >= m) break;
-        one_pre<NS>(a, sh, gb, B, i0 + item(k + 1));
-        ga = one_geo(sh, item(k + 2), n, a.nops);
-        one_issue_q<NS>(ga, A, ga.dep_ready != 0);
-        one_issue_w<NS>(sh, ga, A);
-        one_compute<NS>(a, sh, gb, B, 1, i0 + item(k + 1));
-    }
-    if (threadIdx.x == 0) {
-        __builtin_amdgcn_s_waitcnt(0);
-        const unsigned old = __hip_atomic_fetch_add(ctr_at(a.ctr, kCtrExit), 1u, __ATOMIC_RELAXED,
-                                                    __HIP_MEMORY_SCOPE_AGENT);
-        sh.last = old == gridDim.x - 1;
-    }
-    __syncthreads();
-    if (sh.last) {
-        for (int i = threadIdx.x; i < a.nops; i += kSNT) {
-            st_coh(done_ctr(a, i), 0u);
-            st_coh(qdone_ctr(a, i), 0u);
-        }
-        if (threadIdx.x == 0) st_coh(ctr_at(a.ctr, kCtrExit), 0u);
-    }
-}
-
-
-// ONE: the M = 1 launch (every GEMV item quantises its row).  WPE: waves per
-// SIMD the register budget allows (4: two workgroups per CU).
-template <bool ONE, int WPE>
-__global__ __launch_bounds__(kSNT, WPE) void stack_kernel(const StackArgs a) {
+// (two waves per SIMD: two workgroups per CU)
+__global__ __launch_bounds__(kSNT, 2) void stack_kernel(const StackArgs a) {
     __shared__ Shared sh;
     // this workgroup's items and (when they fit) every op descriptor into LDS
     const int i0 = a.sched_off[blockIdx.x], n = a.sched_off[blockIdx.x + 1] - i0;
@@ -720,13 +380,13 @@ __global__ __launch_bounds__(kSNT, WPE) void stack_kernel(const StackArgs a) {
         const int opi = (int)(it >> 20), local = (int)(it & 0xfffff);
         const OpRef op = load_op(sh, opi);
         const int nq = op.i(OPF(nq));
-        if (!ONE && local < nq) {
+        if (local < nq) {
             quant_item(a, sh, op, opi, local * kSW, 1u);
         } else {
             const int blk = local - nq;
             // (row groups per item as the host dealt them: stack_gemv_rg)
-            if ((op.i(OPF(nch)) + kSW - 1) / kSW <= 2) gemv_item<2, ONE, 8>(a, sh, op, opi, blk, i0 + k);
-            else gemv_item<4, ONE, 4>(a, sh, op, opi, blk, i0 + k);
+            if ((op.i(OPF(nch)) + kSW - 1) / kSW <= 2) gemv_item<2, 8>(a, sh, op, opi, blk, i0 + k);
+            else gemv_item<4, 4>(a, sh, op, opi, blk, i0 + k);
         }
     }
     // the last workgroup out resets the counters for the next launch (its
@@ -754,29 +414,13 @@ int stack_max_chunks() { return 4 * kSW; }
 int stack_rows_per_quant_item() { return kSW; }
 int stack_gemv_rg(int nch) { return (nch + kSW - 1) / kSW <= 2 ? 8 : 4; }
 
-// M = 1 launches take the pipelined kernel whose chunk slots per wave (NS)
-// cover every op of the stack; M > 1 the general one (which reads rows its
-// quantiser items wrote: the host lists those items for every op).
-static const void* stack_fn(int M, int ns) {
-    if (M != 1) return reinterpret_cast<const void*>(stack_kernel<false, 2>);
-    if (ns <= 8) return reinterpret_cast<const void*>(stack_one_kernel<8>);
-    if (ns <= 10) return reinterpret_cast<const void*>(stack_one_kernel<10>);
-    if (ns <= 14) return reinterpret_cast<const void*>(stack_one_kernel<14>);
-    return reinterpret_cast<const void*>(stack_one_kernel<16>);
-}
-int stack_one_slots(int nch, int* rg) {
-    *rg = nch <= 16 ? 8 : 4;
-    return *rg == 8 ? nch : (nch + 1) / 2;
-}
-bool stack_pipelined(int M) { return M == 1; }
-
 hipError_t launch_stack(const StackArgs& a, int blocks, hipStream_t s) {
-    void* args[] = {const_cast<StackArgs*>(&a)};
-    return hipLaunchKernel(stack_fn(a.M, a.slots), dim3(blocks), dim3(kSNT), args, 0, s);
+    hipLaunchKernelGGL(stack_kernel, dim3(blocks), dim3(kSNT), 0, s, a);
+    return hipGetLastError();
 }
 
-hipError_t stack_blocks_per_cu(int M, int slots, int* n) {
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(n, stack_fn(M, slots), kSNT, 0);
+hipError_t stack_blocks_per_cu(int* n) {
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(n, reinterpret_cast<const void*>(stack_kernel), kSNT, 0);
 }
 
 }  // namespace xt
