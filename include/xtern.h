@@ -363,10 +363,10 @@ int xt_ternary_mlp_f32(const xt_weights* gate, const xt_weights* up, const xt_we
  * between them may run concurrently: no op may write a buffer that another
  * op reads or writes unless a dep chain orders them.  M is 1..32 for the
  * whole stack.  The one-launch plan takes Pack4, Pack5 and XorSparse tile
- * weights at M = 1 (in_dim a multiple of 4, a padded row of at most 9216
- * bytes) and Pack4 / XorSparse at M > 1 (in_dim at most 8192); the per-op
- * plan takes every format, and is what XT_STACK_AUTO picks for a list the
- * one-launch kernels do not take.  The stack keeps the pointers (x, y,
+ * weights (in_dim a multiple of 4, a padded row of at most 32768 bytes; the
+ * projections of one op in one tile format); the per-op plan takes every
+ * format, and is what XT_STACK_AUTO picks for a list the one-launch kernel
+ * does not take (the compact XorSparse stream).  The stack keeps the pointers (x, y,
  * weights): they must stay valid while it is used; change the data in place
  * between runs.  No reference counterpart as an API: the reference has no
  * device launches. */

@@ -185,10 +185,10 @@ def test_stack_rejects_bad_ops():
         xtern.Stack([([m.w], x, [y], None)], 33)      # M above 32
     p5 = xtern.DeviceWeights(xtern.XT_PACK5, 256, 32,
                              np.concatenate([xtern.pack_ternary5(r) for r in m.t]), m.ws)
-    x17 = torch.zeros((17, 256), device="cuda")
-    y17 = torch.zeros((17, 32), device="cuda")
+    xs = xtern.DeviceWeights(xtern.XT_XORSPARSE_STREAM, 256, 32,
+                             np.frombuffer(xtern.encode_sparse_tensor(m.t, 256, 32)[0], np.uint8), m.ws)
     with pytest.raises(xtern.XternError):
-        xtern.Stack([([p5], x17, [y17], None)], 17, plan="one_launch")  # Pack5: M <= 16 launch only
+        xtern.Stack([([xs], x, [y], None)], 1, plan="one_launch")  # compact stream: per op only
     with pytest.raises(xtern.XternError):
         xtern.Stack([([m.w], x, [y], None)], 1, plan="fastest")      # unknown plan
     with pytest.raises(xtern.XternError):
@@ -314,7 +314,7 @@ def test_stack_ragged_mixed_formats(M):
 def test_stack_auto_plan_choice():
     """XT_STACK_AUTO: the strict 8-layer chain (32 dependency levels) runs
     per op; the residual-only list (two levels, 32 ops) in one launch; a
-    Pack5 list at M = 17 (not taken by the M > 16 launch) per op.  Each is
+    compact-stream XorSparse op (not taken by the one-launch kernels) per op.  Each is
     checked against the oracle in the plan it got."""
     log("stack auto plan choice")
     rng = np.random.default_rng(zlib.crc32(b"auto_plan") & 0xffff)
@@ -345,12 +345,15 @@ def test_stack_auto_plan_choice():
     assert st.plan_name == "one_launch"
     run_and_compare(ops, checks, 1, xtern.XT_QUANT_SCALAR, reps=1, plan=None)
 
-    m = Mat(rng, 320, 48, pack5=True)
-    x2 = torch.from_numpy(rng.standard_normal((17, 320)).astype(np.float32)).cuda()
-    y2 = torch.full((17, 48), float("nan"), device="cuda")
-    st = xtern.Stack([([m.w], x2, [y2], None)], 17)
+    m = Mat(rng, 320, 48)
+    xs = xtern.DeviceWeights(xtern.XT_XORSPARSE_STREAM, 320, 48,
+                             np.frombuffer(xtern.encode_sparse_tensor(m.t, 320, 48)[0], np.uint8), m.ws)
+    m.w = xs  # (the oracle reference stays the Pack4 bytes of the same matrix)
+    x2 = torch.from_numpy(rng.standard_normal((5, 320)).astype(np.float32)).cuda()
+    y2 = torch.full((5, 48), float("nan"), device="cuda")
+    st = xtern.Stack([([m.w], x2, [y2], None)], 5)
     assert st.plan_name == "per_op"
-    run_and_compare([([m.w], x2, [y2], None)], [(0, ["p"], [y2], x2, {"p": m})], 17,
+    run_and_compare([([m.w], x2, [y2], None)], [(0, ["p"], [y2], x2, {"p": m})], 5,
                     xtern.XT_QUANT_AVX512, reps=1, plan=None)
 
 

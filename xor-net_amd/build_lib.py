@@ -11,7 +11,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 OUT = os.path.join(HERE, "xtern", "libxtern.so")
 
-SOURCES = ["xtern_kernels.hip", "xtern_stack.hip", "xtern_sstack.hip", "xtern_gstream.hip", "xtern_xs.hip",
+SOURCES = ["xtern_kernels.hip", "xtern_sstack.hip", "xtern_gstream.hip", "xtern_xs.hip",
            "xtern_api.cpp", "xtern_layout.cpp", "xtern_container.cpp"]
 
 HIPCC_FLAGS = [

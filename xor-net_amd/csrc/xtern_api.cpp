@@ -951,9 +951,7 @@ int xt_workspace_release(void) {
 }
 
 struct xt_stack {
-    xt::StackArgs args;    // M > 1: the persistent item kernel (xtern_stack.hip)
-    xt::SStackArgs sargs;  // M = 1: the streaming kernel (xtern_sstack.hip)
-    bool stream;
+    xt::SStackArgs sargs;  // the one-launch plan: the streaming kernel (xtern_sstack.hip)
     int blocks;
     int device;
     void* dev_mem;  // ops, items, counters, scratch (one allocation)
@@ -989,23 +987,23 @@ std::vector<int> stack_order(const xt_stack_op* ops, int nops, const std::vector
 
 // Which plan runs a list faster, from measured figures (BitNet-2B
 // projection shapes, weights streamed from HBM, MI355X):
-//  * one call per op: about 4.6 us per op at M = 1, 6.5 at M <= 8 and 9.2 up
+//  * one call per op: about 4.7 us per op at M = 1, 6.5 at M <= 8 and 9.4 up
 //    to M = 32 (launch to launch in a HIP graph), or the op's weight bytes at
 //    2.7 TB/s where that is longer;
-//  * one launch: the weights at 3.6 TB/s (M = 1), 2.0 (M <= 8) or 1.2 TB/s,
-//    plus about 20 us per dependency level after the first: a level's ops
-//    start only once the level before has published its outputs (device-
-//    scope stores, a count, polls, the quantiser task and its count), and
-//    each of its waves then walks its share of the op's tiles two at a time
-//    (one memory latency per pair), where a one-op launch loads all of a
-//    workgroup's tiles at once.
+//  * one launch: the weights at 4.3 TB/s (M = 1), 3.4 (M <= 8) or 1.7 TB/s,
+//    plus about 20 / 24 / 30 us per dependency level after the first: a
+//    level's ops start only once the level before has published its outputs
+//    (device-scope stores, a count, polls, the quantiser tasks and their
+//    count), and each of its waves then walks its share of the op's tiles one
+//    chunk at a time, where a one-op launch loads all of a workgroup's tiles
+//    at once.
 // The 30-layer projection stack with the residual dependency (2 levels) runs
-// in one launch in 143 us against 556 us per op; the strict chain (120
-// levels) took 2440 us in one launch against 556 us per op.
+// in one launch in 121 us against 560 us per op at M = 1; the strict chain
+// (120 levels) took 2450 us in one launch against 598 us per op.
 bool stack_prefers_per_op(const xt_stack_op* ops, int nops, int64_t M) {
-    const double call_us = M == 1 ? 4.6 : (M <= 8 ? 6.5 : 9.2);
-    const double call_bpus = 2.7e6, launch_bpus = M == 1 ? 3.6e6 : (M <= 8 ? 2.0e6 : 1.2e6);
-    const double level_us = 20.0;
+    const double call_us = M == 1 ? 4.7 : (M <= 8 ? 6.5 : 9.4);
+    const double call_bpus = 2.7e6, launch_bpus = M == 1 ? 4.3e6 : (M <= 8 ? 3.4e6 : 1.7e6);
+    const double level_us = M == 1 ? 20.0 : (M <= 8 ? 24.0 : 30.0);
     std::vector<int> lvl((size_t)nops, 0);
     int depth = 0;
     double bytes = 0, per_op_us = 0;
@@ -1042,14 +1040,13 @@ int create_per_op(const xt_stack_op* ops, int nops, int64_t M, int qmode, xt_sta
     return XT_OK;
 }
 
-int create_stack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stack** out);
-
-// M = 1: the streaming stack.  Tasks in list order: the quantiser tasks of
-// ops without a dependency, then per op (in stack_order) its 16-row groups
-// followed by the quantiser tasks of the ops that read its outputs.
+// The one-launch plan (xtern_sstack.hip, M = 1 .. 32).  Tasks in list order:
+// the quantiser tasks (one per token) of ops without a dependency, then per
+// op (in stack_order) its blocks of 16-row groups followed by the quantiser
+// tasks of the ops that read its outputs.
 int create_sstack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stack** out) {
     if (nops > xt::kSStackMaxOps)
-        return fail(XT_ERR_UNSUPPORTED, "at most " + std::to_string(xt::kSStackMaxOps) + " ops per M = 1 stack");
+        return fail(XT_ERR_UNSUPPORTED, "at most " + std::to_string(xt::kSStackMaxOps) + " ops per stack");
     struct OpInfo {
         int fmt, nch, ldq, K, ngroups;
         size_t qoff;
@@ -1205,14 +1202,12 @@ int create_sstack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stac
         (void)hipFree(mem);
         return fail(XT_ERR_NOMEM, "stack handle");
     }
-    st->stream = true;
     st->sargs.tasks = reinterpret_cast<const xt::SStackTask*>(mem);
     st->sargs.ctr = reinterpret_cast<unsigned*>(mem + tasks_b);
     st->sargs.ntasks = (int)tasks.size();
     st->sargs.nops = nops;
     st->sargs.mode = mode;
     st->sargs.spin_limit = 1 << 20;  // polls (about a microsecond each) before a wait gives up
-    st->args.ctr = st->sargs.ctr;    // (the error slot, read by xt_stack_check)
     st->sargs.woff = reinterpret_cast<const int*>(mem + tasks_b + ctr_b + scratch);
     st->sargs.row_bytes = row_bytes;
     st->sargs.M = (int)M;
@@ -1231,7 +1226,7 @@ int xt_stack_create(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_st
     if (!out) return fail(XT_ERR_INVALID, "out is NULL");
     *out = nullptr;
     if (!ops || nops < 1) return fail(XT_ERR_INVALID, "need at least one op");
-    const int max_ops = std::min<int>(xt::kStackMaxOps, xt::kStackDescLdsBytes / sizeof(xt::StackOpDev));
+    const int max_ops = xt::kSStackMaxOps;
     if (nops > max_ops)
         return fail(XT_ERR_UNSUPPORTED, "at most " + std::to_string(max_ops) +
                                             " ops per stack (split longer lists into several stacks)");
@@ -1261,8 +1256,7 @@ int xt_stack_create(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_st
     }
     if (plan == XT_STACK_PER_OP || (plan == XT_STACK_AUTO && stack_prefers_per_op(ops, nops, M)))
         return create_per_op(ops, nops, M, mode, out);
-    const int rc = M <= xt::kSStackMaxM ? create_sstack(ops, nops, M, mode, out)
-                                        : create_stack(ops, nops, M, mode, out);
+    const int rc = create_sstack(ops, nops, M, mode, out);
     // (a list the one-launch kernels do not take runs per op unless the
     // caller asked for one launch)
     if (rc == XT_ERR_UNSUPPORTED && plan == XT_STACK_AUTO) return create_per_op(ops, nops, M, mode, out);
@@ -1276,199 +1270,6 @@ int xt_stack_plan(const xt_stack* st) {
 
 }  // extern "C"
 
-namespace {
-
-// M > 1: the persistent item kernel's work list.
-int create_stack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stack** out) {
-    const int rq = xt::stack_rows_per_quant_item();
-    std::vector<xt::StackOpDev> dops((size_t)nops);
-    size_t scratch = 0;
-    std::vector<size_t> qoff((size_t)nops);
-    for (int i = 0; i < nops; ++i) {
-        const xt_stack_op& op = ops[i];
-        const std::string at = "op " + std::to_string(i) + ": ";
-        if (op.n < 1 || op.n > 4) return fail(XT_ERR_INVALID, at + "n must be 1..4");
-        if (!op.x) return fail(XT_ERR_INVALID, at + "x is NULL");
-        if (op.dep < -1 || op.dep >= i)
-            return fail(XT_ERR_INVALID, at + "dep must be -1 or an earlier op");
-        for (int p = 0; p < op.n; ++p)
-            if (!op.w[p] || !op.y[p]) return fail(XT_ERR_INVALID, at + "NULL weights or output");
-        xt::StackOpDev& d = dops[(size_t)i];
-        memset(&d, 0, sizeof d);
-        const int rgi = xt::stack_gemv_rg((int)op.w[0]->nch);  // row groups per GEMV item
-        d.rg = rgi;
-        int blocks = 0;
-        for (int p = 0; p < op.n; ++p) {
-            const xt_weights* w = op.w[p];
-            if (!w || !op.y[p]) return fail(XT_ERR_INVALID, at + "NULL weights or output");
-            if (w->fmt != XT_PACK4 && w->fmt != XT_XORSPARSE)
-                return fail(XT_ERR_UNSUPPORTED, at + "stack weights must be Pack4 or XorSparse");
-            if (w->K != op.w[0]->K) return fail(XT_ERR_INVALID, at + "projections must share in_dim");
-            if (w->K % 4 != 0 || w->nch > xt::stack_max_chunks())
-                return fail(XT_ERR_UNSUPPORTED, at + "in_dim must be a multiple of 4 and at most " +
-                                                    std::to_string(xt::stack_max_chunks() * 256));
-            if (w->tile_bytes >= ((size_t)1 << 31))
-                return fail(XT_ERR_UNSUPPORTED, at + "weights above 2 GiB per projection");
-            d.tiles[p] = w->tiles;
-            d.ws[p] = w->ws;
-            d.y[p] = op.y[p];
-            d.N[p] = (int)w->N;
-            blocks += (int)(((w->N + 15) / 16 + rgi - 1) / rgi);
-            d.gend[p] = blocks;
-        }
-        d.nproj = op.n;
-        d.K = (int)op.w[0]->K;
-        d.nch = (int)op.w[0]->nch;
-        d.ldq = d.nch * 256;
-        d.x = op.x;
-        d.dep = op.dep;
-        d.dep_items = op.dep >= 0 ? dops[(size_t)op.dep].ngemv : 0;
-        // quantiser items for every op: both kernels read the rows they write
-        // (a GEMV item of the general kernel dereferences d.q / d.inv)
-        d.nq = (int)((M + rq - 1) / rq);
-        d.ngemv = blocks;
-        if (d.nq + blocks >= (1 << 20)) return fail(XT_ERR_UNSUPPORTED, at + "too many rows");
-        if (op.dep >= 0) dops[(size_t)op.dep].pub = 1;
-        if (d.nq > 0) {
-            qoff[(size_t)i] = scratch;
-            scratch += align_up((size_t)M * d.ldq, 256) + align_up((size_t)M * 4, 256);
-        }
-    }
-    // Work list: each op's GEMV items in op order; an op's quantiser items
-    // (M > 1) go right after the GEMV items of the op it depends on (at the
-    // front when it has none), so they are done long before its GEMV items
-    // are taken.  Every item follows everything it waits for.
-    std::vector<uint32_t> items;
-    std::vector<double> cost;
-    auto push_quant = [&](int i) {
-        const xt::StackOpDev& d = dops[(size_t)i];
-        for (int t = 0; t < d.nq; ++t) {
-            items.push_back(((uint32_t)i << 20) | (uint32_t)t);
-            cost.push_back(16384.0 + 8.0 * rq * d.K);  // two reads of the rows
-        }
-    };
-    // Op order: ops that others wait for go as early as their own inputs
-    // allow, the rest keep the caller's order.  (Ops with no dependency path
-    // between them may run in any order: they share no buffers, per the
-    // contract in xtern.h.)  Every op still follows the op it depends on.
-    std::vector<int> order;
-    {
-        std::vector<char> placed((size_t)nops, 0);
-        std::vector<int> pend;
-        for (int i = 0; i < nops; ++i) pend.push_back(i);
-        while ((int)order.size() < nops) {
-            int pick = -1;
-            for (int i : pend)
-                if (!placed[(size_t)i] && (ops[i].dep < 0 || placed[(size_t)ops[i].dep]) &&
-                    dops[(size_t)i].pub) {
-                    pick = i;
-                    break;
-                }
-            if (pick < 0)
-                for (int i : pend)
-                    if (!placed[(size_t)i] && (ops[i].dep < 0 || placed[(size_t)ops[i].dep])) {
-                        pick = i;
-                        break;
-                    }
-            placed[(size_t)pick] = 1;
-            order.push_back(pick);
-        }
-    }
-    for (int i = 0; i < nops; ++i)
-        if (ops[i].dep < 0) push_quant(i);
-    for (int i : order) {
-        const xt::StackOpDev& d = dops[(size_t)i];
-        for (int t = 0; t < d.ngemv; ++t) {
-            items.push_back(((uint32_t)i << 20) | (uint32_t)(d.nq + t));
-            cost.push_back(16384.0 + 1024.0 * d.rg * d.nch + (double)M * d.K);  // + weights
-        }
-        for (int k = i + 1; k < nops; ++k)
-            if (ops[k].dep == i) push_quant(k);
-    }
-    int dev = 0, cus = 0, per_cu = 0;
-    XT_HIP(hipGetDevice(&dev));
-    XT_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    XT_HIP(xt::stack_blocks_per_cu(&per_cu));
-    if (per_cu < 1) return fail(XT_ERR_UNSUPPORTED, "stack kernel does not fit a CU");
-    // Every workgroup resident at once (see xtern_stack.hip): grid = occupancy.
-    int grid = std::min(cus * per_cu, (int)items.size());
-    // Deal the list out: each item, in list order, to the workgroup that is
-    // predicted to finish its earlier items first (bytes as the cost).
-    std::vector<std::vector<uint32_t>> per((size_t)grid);
-    {
-        typedef std::pair<double, int> Slot;
-        std::vector<Slot> heap;
-        for (int b = 0; b < grid; ++b) heap.push_back(Slot(0.0, b));
-        auto later = [](const Slot& x, const Slot& y) { return x > y; };
-        std::make_heap(heap.begin(), heap.end(), later);
-        for (size_t t = 0; t < items.size(); ++t) {
-            std::pop_heap(heap.begin(), heap.end(), later);
-            Slot& s0 = heap.back();
-            per[(size_t)s0.second].push_back(items[t]);
-            s0.first += cost[t];
-            std::push_heap(heap.begin(), heap.end(), later);
-        }
-    }
-    std::vector<int> sched_off((size_t)grid + 1, 0);
-    std::vector<uint32_t> sched;
-    sched.reserve(items.size());
-    for (int b = 0; b < grid; ++b) {
-        if (per[(size_t)b].size() > (size_t)xt::kStackMaxWgItems)
-            return fail(XT_ERR_UNSUPPORTED, "stack too long for one launch (" +
-                                                std::to_string(items.size()) + " items)");
-        sched.insert(sched.end(), per[(size_t)b].begin(), per[(size_t)b].end());
-        sched_off[(size_t)b + 1] = (int)sched.size();
-    }
-    const size_t ops_b = align_up(sizeof(xt::StackOpDev) * nops, 256);
-    const size_t off_b = align_up(sched_off.size() * 4, 256);
-    const size_t items_b = align_up(sched.size() * 4, 256);
-    const size_t ctr_b = (size_t)(4 + 2 * nops) * 128;
-    char* mem = nullptr;
-    hipError_t e = hipMalloc(reinterpret_cast<void**>(&mem), ops_b + off_b + items_b + ctr_b + scratch);
-    if (e != hipSuccess) return fail(XT_ERR_NOMEM, std::string("stack allocation: ") + hipGetErrorString(e));
-    char* sc = mem + ops_b + off_b + items_b + ctr_b;
-    for (int i = 0; i < nops; ++i) {
-        xt::StackOpDev& d = dops[(size_t)i];
-        if (d.nq == 0) continue;  // (not reached: every op has quantiser items)
-        const size_t qb = align_up((size_t)M * d.ldq, 256);
-        d.q = reinterpret_cast<int8_t*>(sc + qoff[(size_t)i]);
-        d.inv = reinterpret_cast<float*>(sc + qoff[(size_t)i] + qb);
-    }
-    e = hipMemcpy(mem, dops.data(), sizeof(xt::StackOpDev) * nops, hipMemcpyHostToDevice);
-    if (e == hipSuccess)
-        e = hipMemcpy(mem + ops_b, sched_off.data(), sched_off.size() * 4, hipMemcpyHostToDevice);
-    if (e == hipSuccess)
-        e = hipMemcpy(mem + ops_b + off_b, sched.data(), sched.size() * 4, hipMemcpyHostToDevice);
-    if (e == hipSuccess) e = hipMemset(mem + ops_b + off_b + items_b, 0, ctr_b);
-    if (e == hipSuccess) e = hipDeviceSynchronize();
-    if (e != hipSuccess) {
-        (void)hipFree(mem);
-        return hip_fail(e, "stack upload");
-    }
-    xt_stack* st = new (std::nothrow) xt_stack();
-    if (!st) {
-        (void)hipFree(mem);
-        return fail(XT_ERR_NOMEM, "stack handle");
-    }
-    st->args.ops = reinterpret_cast<const xt::StackOpDev*>(mem);
-    st->args.sched_off = reinterpret_cast<const int*>(mem + ops_b);
-    st->args.sched = reinterpret_cast<const uint32_t*>(mem + ops_b + off_b);
-    st->args.ctr = reinterpret_cast<unsigned*>(mem + ops_b + off_b + items_b);
-    st->args.nitems = (int)items.size();
-    st->args.nops = nops;
-    st->args.M = (int)M;
-    st->args.mode = mode;
-    // polls (about a microsecond each) before a dependency wait gives up
-    st->args.spin_limit = 1 << 20;
-    st->blocks = grid;
-    st->device = dev;
-    st->dev_mem = mem;
-    *out = st;
-    return XT_OK;
-}
-
-}  // namespace
-
 extern "C" {
 
 int xt_stack_run(const xt_stack* st, void* stream) {
@@ -1481,8 +1282,7 @@ int xt_stack_run(const xt_stack* st, void* stream) {
         }
         return XT_OK;
     }
-    hipError_t e = st->stream ? xt::launch_sstack(st->sargs, st->blocks, static_cast<hipStream_t>(stream))
-                              : xt::launch_stack(st->args, st->blocks, static_cast<hipStream_t>(stream));
+    hipError_t e = xt::launch_sstack(st->sargs, st->blocks, static_cast<hipStream_t>(stream));
     if (e != hipSuccess) return hip_fail(e, "stack launch");
     return XT_OK;
 }
@@ -1495,7 +1295,7 @@ int xt_stack_check(xt_stack* st, int* gave_up) {
         return XT_OK;
     }
     unsigned flag = 0;
-    unsigned* slot = st->args.ctr + 2 * 32;  // the error slot (xtern_stack.hip kCtrError)
+    unsigned* slot = st->sargs.ctr + 2 * 32;  // the error slot (xtern_sstack.hip kSsError)
     XT_HIP(hipMemcpy(&flag, slot, sizeof flag, hipMemcpyDeviceToHost));
     if (flag) XT_HIP(hipMemset(slot, 0, sizeof flag));
     *gave_up = flag ? 1 : 0;

@@ -1,5 +1,5 @@
 // Device helpers shared by the xtern kernels (xtern_kernels.hip,
-// xtern_stack.hip): the quantiser's per-element rounding, DPP wave reductions,
+// xtern_sstack.hip, xtern_gstream.hip, xtern_xs.hip): the quantiser's per-element rounding, DPP wave reductions,
 // load flavours, the Pack4 decode and the i8 MFMA.
 #pragma once
 #include <hip/hip_runtime.h>

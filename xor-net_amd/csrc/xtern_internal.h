@@ -175,7 +175,7 @@ hipError_t scratch_region(void** ptr, size_t* bytes);
 // Streaming decode stack, M = 1 (xtern_sstack.hip).
 constexpr int kSStackMaxOps = 8191;          // op index: 13 bits of a task
 constexpr int kSStackMaxRowBytes = 32768;    // i8 row (nch * chunk columns) of one op, at most
-constexpr int kSStackMaxM = 16;              // tokens of the streaming stack (one MFMA block)
+constexpr int kSStackMaxM = 32;              // tokens of the streaming stack (two MFMA blocks)
 // One task, 64 bytes: everything a wave needs to start it, loaded one task
 // ahead.  flags bits 0-15: 1 quantiser task, 2 other ops read the outputs
 // (count the groups' completion), 4 Pack5 tiles; bits 16-31: the task's
@@ -204,43 +204,6 @@ hipError_t launch_sstack(const SStackArgs& a, int blocks, hipStream_t s);
 hipError_t sstack_blocks_per_cu(int M, int row_bytes, int* n);
 int sstack_lds_rows(int M);  // token rows of a wave's LDS region
 int sstack_waves_per_block();
-// Persistent decode stack for 17 <= M <= 32 (xtern_stack.hip): one launch over
-// a list of ops.
-constexpr int kStackRowGroupsMax = 8;       // 16-row groups per GEMV item (M > 1): stack_gemv_rg
-constexpr int kStackMaxOps = 4095;
-constexpr int kStackMaxWgItems = 1024;      // items one workgroup may be dealt
-constexpr int kStackDescLdsBytes = 40 * 1024;  // every op descriptor is copied to LDS
-struct StackOpDev {
-    const uint8_t* tiles[4];  // Pack4 tiles of each projection
-    const float* ws[4];
-    float* y[4];              // [M][N[p]] outputs
-    const float* x;           // [M][K] f32 input
-    int8_t* q;                // [M][ldq] quantised input, launch scratch
-    float* inv;               // [M]
-    int N[4];
-    int gend[4];              // cumulative GEMV items per projection
-    int nproj, K, nch, ldq;
-    int dep;                  // op whose outputs x reads (wait for all its GEMV items), or -1
-    int dep_items;            // that op's GEMV item count
-    int nq;                   // quantiser items: ceil(M / rows per item)
-    int ngemv;                // GEMV items
-    int pub;                  // another op depends on this one: count its completions
-    int rg;                   // 16-row groups per GEMV item (stack_gemv_rg)
-};
-struct StackArgs {
-    const StackOpDev* ops;
-    const int* sched_off;     // [grid + 1]: workgroup b takes sched[sched_off[b] .. sched_off[b+1])
-    const uint32_t* sched;    // items (op << 20 | item index within the op), per workgroup in list order
-    unsigned* ctr;            // (4 + 2 * nops) slots of 128 bytes, zero between launches
-    int nitems, nops, M, mode;
-    int spin_limit;           // polls before a dependency wait gives up
-};
-int stack_threads();
-int stack_max_chunks();  // chunks of K an op may have (4 per wave)
-int stack_gemv_rg(int nch);  // row groups per GEMV item of the M > 1 kernel
-int stack_rows_per_quant_item();
-hipError_t launch_stack(const StackArgs& a, int blocks, hipStream_t s);
-hipError_t stack_blocks_per_cu(int* n);
 // HF prepacked striped bytes [N/f][K] (device) -> tiles (device).
 hipError_t launch_hf_tiles(int fmt, const uint8_t* stored, int64_t K, int64_t N, uint8_t* tiles,
                            hipStream_t s);

@@ -225,10 +225,11 @@ __device__ void ss_quant(const SStackArgs& a, const Rec& r) {
 // host pads the row pitch), so its L2 holds no stale copy, and later tasks
 // of the op on the XCD hit in it.
 //
-// MT: token rows the LDS region holds (4 for M <= 4, else 16).  PF: the next
-// chunk's activation pieces are loaded during this step (registers allowing:
-// MT = 4), so a step stages its pieces in LDS and reads its A fragments while
-// its tiles are still in flight.
+// MT: token rows the LDS region holds (4 for M <= 4, 16, or 32: two blocks
+// of 16 tokens, each weight tile decoded once per k-step for both blocks'
+// MFMAs).  PF: the next chunk's activation pieces are loaded during this
+// step (registers allowing: MT = 4), so a step stages its pieces in LDS and
+// reads its A fragments while its tiles are still in flight.
 constexpr int kSsR = 4;  // 16-row groups per task, at most
 template <int FMT, int MT, bool PF>
 __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsigned* known) {
@@ -237,6 +238,7 @@ __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsi
     constexpr int LDR = CH + 16;       // LDS bytes per token row of a chunk
     constexpr int PR = CH / 16;        // 16-byte pieces per token row of a chunk
     constexpr int kAP = (MT * PR + 63) / 64;  // pieces per lane for MT token rows
+    constexpr int TB = (MT + 15) / 16;        // 16-token MFMA blocks
     const int lane = threadIdx.x & 63;
     const int g = lane >> 4, j = lane & 15;
     const int M = a.M, nch = r.nch, opi = r.opi, ldq = r.ldq, N = r.K;
@@ -263,8 +265,9 @@ __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsi
     const __amdgpu_buffer_rsrc_t qr = ss_rsrc(r.q, (unsigned)(M * ldq));
     auto ptok = [&](int u) { return (lane + 64 * u) / PR; };
     auto pcol = [&](int u) { return ((lane + 64 * u) % PR) * 16; };
-    // (rows >= MT of the A fragment: the last row again, never stored)
-    const uint32_t abase = areg + (uint32_t)(min(j, MT - 1) * LDR + g * 16);
+    // block tb's A fragment: token row 16 tb + j (rows >= MT: the last row
+    // again, never stored)
+    auto abase = [&](int tb) { return areg + (uint32_t)(min(16 * tb + j, MT - 1) * LDR + g * 16); };
     const uint8_t* const tl = reinterpret_cast<const uint8_t*>(r.tiles) + lane * 16;
     auto load_act = [&](v4i* ap, int c) {  // (chunks past nch read nothing)
 #pragma unroll
@@ -274,9 +277,11 @@ __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsi
             ap[u] = __builtin_amdgcn_raw_buffer_load_b128(qr, go, 0, 0);
         }
     };
-    v4i acc[kSsR];
+    v4i acc[TB][kSsR];
 #pragma unroll
-    for (int gi = 0; gi < kSsR; ++gi) acc[gi] = v4i{0, 0, 0, 0};
+    for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+        for (int gi = 0; gi < kSsR; ++gi) acc[tb][gi] = v4i{0, 0, 0, 0};
     v4i ap[kAP];
     if constexpr (PF) load_act(ap, 0);
     for (int c = 0; c < nch; ++c) {
@@ -295,9 +300,11 @@ __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsi
             if (64 * (u + 1) <= MT * PR || ptok(u) < MT)  // (the region holds MT rows)
                 *reinterpret_cast<__attribute__((address_space(3))) v4i*>(
                     (uintptr_t)(areg + (uint32_t)(ptok(u) * LDR + pcol(u)))) = ap[u];
-        v4i af[STEPS];
+        v4i af[TB][STEPS];
 #pragma unroll
-        for (int st = 0; st < STEPS; ++st) af[st] = ss_lds16(abase + st * 64);
+        for (int tb = 0; tb < TB; ++tb)
+#pragma unroll
+            for (int st = 0; st < STEPS; ++st) af[tb][st] = ss_lds16(abase(tb) + st * 64);
         // (all kSsR groups are multiplied: no branch for the compiler to sink
         // loads into; products of groups past the block are never stored)
 #pragma unroll
@@ -319,11 +326,16 @@ __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsi
                         E[q] = pE & 0x00ff00ff;
                         O[q] = pO & 0x00ff00ff;
                     }
-                    acc[gi] = mfma(af[st], b, acc[gi]);
+#pragma unroll
+                    for (int tb = 0; tb < TB; ++tb) acc[tb][gi] = mfma(af[tb][st], b, acc[tb][gi]);
                 }
             } else {
 #pragma unroll
-                for (int st = 0; st < STEPS; ++st) acc[gi] = mfma(af[st], decode4(wb[gi][st]), acc[gi]);
+                for (int st = 0; st < STEPS; ++st) {
+                    const v4i b = decode4(wb[gi][st]);
+#pragma unroll
+                    for (int tb = 0; tb < TB; ++tb) acc[tb][gi] = mfma(af[tb][st], b, acc[tb][gi]);
+                }
             }
         }
         if constexpr (PF) {
@@ -331,35 +343,39 @@ __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsi
             for (int u = 0; u < kAP; ++u) ap[u] = apn[u];
         }
     }
-    // this lane's outputs: tokens 4g .. 4g + 3, row j of each group
-    int rs[4];
-    float inv[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-        const int tk = min(4 * g + t, M - 1);
-        rs[t] = __builtin_amdgcn_ds_bpermute(4 * tk, sv);
-        inv[t] = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (tk + M), sv));
-    }
+    // this lane's outputs: tokens 16 tb + 4g .. + 3, row j of each group
     float wsc[kSsR];
 #pragma unroll
     for (int gi = 0; gi < kSsR; ++gi)
         wsc[gi] = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * min(gi * 16 + j, trows - 1), wv));
 
-    // acc[gi][t]: token 4g + t, row j of group gi; the MFMAs took codes w + 1,
-    // so the token's sum comes off (layers.rs:340: (dot as f32 * inv) * w_scale)
+    // acc[tb][gi][t]: token 16 tb + 4g + t, row j of group gi; the MFMAs took
+    // codes w + 1, so the token's sum comes off (layers.rs:340: (dot as f32 *
+    // inv) * w_scale)
     const bool pub = (r.flags & kSsPub) != 0;
     const __amdgpu_buffer_rsrc_t yr = ss_rsrc(r.y, (unsigned)(((M - 1) * N + trows) * 4));
 #pragma unroll
-    for (int gi = 0; gi < kSsR; ++gi) {
-        if (gi >= ng) break;  // (uniform)
-        const int row = gi * 16 + j;
+    for (int tb = 0; tb < TB; ++tb) {
+        int rs[4];
+        float inv[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
-            const int tk = 4 * g + t;
-            if (tk < M && row < trows) {
-                const float v = __fmul_rn(__fmul_rn((float)(acc[gi][t] - rs[t]), inv[t]), wsc[gi]);
-                if (pub) ss_st_coh4(yr, (unsigned)((tk * N + row) * 4), __float_as_uint(v));
-                else ((gfloat_w*)(uintptr_t)r.y)[(size_t)tk * N + row] = v;
+            const int tk = min(16 * tb + 4 * g + t, M - 1);
+            rs[t] = __builtin_amdgcn_ds_bpermute(4 * tk, sv);
+            inv[t] = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (tk + M), sv));
+        }
+#pragma unroll
+        for (int gi = 0; gi < kSsR; ++gi) {
+            if (gi >= ng) break;  // (uniform)
+            const int row = gi * 16 + j;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) {
+                const int tk = 16 * tb + 4 * g + t;
+                if (tk < M && row < trows) {
+                    const float v = __fmul_rn(__fmul_rn((float)(acc[tb][gi][t] - rs[t]), inv[t]), wsc[gi]);
+                    if (pub) ss_st_coh4(yr, (unsigned)((tk * N + row) * 4), __float_as_uint(v));
+                    else ((gfloat_w*)(uintptr_t)r.y)[(size_t)tk * N + row] = v;
+                }
             }
         }
     }
@@ -375,7 +391,7 @@ __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsi
 // registers for a task's tiles, activation pieces, A fragments and the four
 // groups' accumulators.
 template <int MT>
-__global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(3))) void sstack_kernel(const SStackArgs a) {
+__global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(MT == 32 ? 2 : 3))) void sstack_kernel(const SStackArgs a) {
     __shared__ unsigned known[kSsKnownWords];  // ops this workgroup has seen quantised
     extern __shared__ __align__(16) uint8_t rows[];  // [kSsW][a.row_bytes]: each wave's i8 row
     for (int i = threadIdx.x; i < kSsKnownWords; i += kSsW * 64) known[i] = 0u;
@@ -419,21 +435,22 @@ __global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(3))) 
 // form's token rows.
 static size_t ss_dyn_lds(int row_bytes) { return (size_t)kSsW * row_bytes; }
 
-int sstack_lds_rows(int M) { return M <= 4 ? 4 : 16; }
+int sstack_lds_rows(int M) { return M <= 4 ? 4 : (M <= 16 ? 16 : 32); }
+
+static const void* ss_fn(int M) {
+    if (M <= 4) return reinterpret_cast<const void*>(sstack_kernel<4>);
+    if (M <= 16) return reinterpret_cast<const void*>(sstack_kernel<16>);
+    return reinterpret_cast<const void*>(sstack_kernel<32>);
+}
 
 hipError_t launch_sstack(const SStackArgs& a, int blocks, hipStream_t s) {
     if (a.M < 1 || a.M > kSStackMaxM) return hipErrorInvalidValue;
-    if (a.M <= 4)
-        hipLaunchKernelGGL(sstack_kernel<4>, dim3(blocks), dim3(kSsW * 64), ss_dyn_lds(a.row_bytes), s, a);
-    else
-        hipLaunchKernelGGL(sstack_kernel<16>, dim3(blocks), dim3(kSsW * 64), ss_dyn_lds(a.row_bytes), s, a);
-    return hipGetLastError();
+    void* args[] = {const_cast<SStackArgs*>(&a)};
+    return hipLaunchKernel(ss_fn(a.M), dim3(blocks), dim3(kSsW * 64), args, ss_dyn_lds(a.row_bytes), s);
 }
 
 hipError_t sstack_blocks_per_cu(int M, int row_bytes, int* n) {
-    const void* k = M <= 4 ? reinterpret_cast<const void*>(sstack_kernel<4>)
-                           : reinterpret_cast<const void*>(sstack_kernel<16>);
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(n, k, kSsW * 64, ss_dyn_lds(row_bytes));
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(n, ss_fn(M), kSsW * 64, ss_dyn_lds(row_bytes));
 }
 
 int sstack_waves_per_block() { return kSsW; }
