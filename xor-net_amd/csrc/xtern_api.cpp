@@ -1090,7 +1090,7 @@ int create_sstack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stac
     // 16-row groups per task: 4 (the kernel loads and multiplies four
     // groups' tiles per step and shares the chunk's activation pieces among
     // them; measured faster than 2 groups per task at M = 1 too)
-    const int rg = 4;
+    const int rg = xt::sstack_groups_per_task((int)M);
     ntasks = (size_t)nops * (size_t)M;
     for (int i = 0; i < nops; ++i)
         for (int p = 0; p < ops[i].n; ++p) ntasks += (size_t)(((ops[i].w[p]->N + 15) / 16 + rg - 1) / rg);

@@ -212,7 +212,7 @@ __device__ void ss_quant(const SStackArgs& a, const Rec& r) {
                                __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// A group task (M up to 16 tokens): a block of r.ngroups (<= kSsR) consecutive
+// A group task (M up to 32 tokens): a block of r.ngroups (<= R) consecutive
 // 16-row groups of one projection, walked chunk by chunk: each step loads
 // the block's tiles of one chunk (one per group) and the chunk's 16-byte
 // pieces of the M quantised rows, puts the pieces in this wave's LDS region
@@ -230,8 +230,8 @@ __device__ void ss_quant(const SStackArgs& a, const Rec& r) {
 // MFMAs).  PF: the next chunk's activation pieces are loaded during this
 // step (registers allowing: MT = 4), so a step stages its pieces in LDS and
 // reads its A fragments while its tiles are still in flight.
-constexpr int kSsR = 4;  // 16-row groups per task, at most
-template <int FMT, int MT, bool PF>
+// R: 16-row groups per task, at most (the host deals blocks of R).
+template <int FMT, int MT, bool PF, int R>
 __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsigned* known) {
     constexpr int STEPS = (FMT == XT_PACK5) ? 5 : 4;
     constexpr int CH = STEPS * 64;
@@ -277,17 +277,17 @@ __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsi
             ap[u] = __builtin_amdgcn_raw_buffer_load_b128(qr, go, 0, 0);
         }
     };
-    v4i acc[TB][kSsR];
+    v4i acc[TB][R];
 #pragma unroll
     for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
-        for (int gi = 0; gi < kSsR; ++gi) acc[tb][gi] = v4i{0, 0, 0, 0};
+        for (int gi = 0; gi < R; ++gi) acc[tb][gi] = v4i{0, 0, 0, 0};
     v4i ap[kAP];
     if constexpr (PF) load_act(ap, 0);
     for (int c = 0; c < nch; ++c) {
-        v4i wb[kSsR], apn[kAP];
+        v4i wb[R], apn[kAP];
 #pragma unroll
-        for (int gi = 0; gi < kSsR; ++gi)  // (groups past the block: its last group again, unused)
+        for (int gi = 0; gi < R; ++gi)  // (groups past the block: its last group again, unused)
             wb[gi] = ss_ld_tile(tl + ((size_t)min(gi, ng - 1) * nch + c) * kTileBytes);
         if constexpr (PF) load_act(apn, c + 1);
         else load_act(ap, c);
@@ -305,10 +305,13 @@ __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsi
         for (int tb = 0; tb < TB; ++tb)
 #pragma unroll
             for (int st = 0; st < STEPS; ++st) af[tb][st] = ss_lds16(abase(tb) + st * 64);
-        // (all kSsR groups are multiplied: no branch for the compiler to sink
+        // (the LDS stage goes ahead of the weight decode: its wait for the
+        // first tile would otherwise come first and hold the stage back)
+        __builtin_amdgcn_sched_barrier(0);
+        // (all R groups are multiplied: no branch for the compiler to sink
         // loads into; products of groups past the block are never stored)
 #pragma unroll
-        for (int gi = 0; gi < kSsR; ++gi) {
+        for (int gi = 0; gi < R; ++gi) {
             if constexpr (FMT == XT_PACK5) {
                 int E[4], O[4];
 #pragma unroll
@@ -344,9 +347,9 @@ __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsi
         }
     }
     // this lane's outputs: tokens 16 tb + 4g .. + 3, row j of each group
-    float wsc[kSsR];
+    float wsc[R];
 #pragma unroll
-    for (int gi = 0; gi < kSsR; ++gi)
+    for (int gi = 0; gi < R; ++gi)
         wsc[gi] = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * min(gi * 16 + j, trows - 1), wv));
 
     // acc[tb][gi][t]: token 16 tb + 4g + t, row j of group gi; the MFMAs took
@@ -365,7 +368,7 @@ __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsi
             inv[t] = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (tk + M), sv));
         }
 #pragma unroll
-        for (int gi = 0; gi < kSsR; ++gi) {
+        for (int gi = 0; gi < R; ++gi) {
             if (gi >= ng) break;  // (uniform)
             const int row = gi * 16 + j;
 #pragma unroll
@@ -390,8 +393,8 @@ __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsi
 // MT: the token form (see ss_mblock).  Three waves per SIMD: up to 168
 // registers for a task's tiles, activation pieces, A fragments and the four
 // groups' accumulators.
-template <int MT>
-__global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(MT == 32 ? 2 : 3))) void sstack_kernel(const SStackArgs a) {
+template <int MT, int R, int WPE>
+__global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(WPE))) void sstack_kernel(const SStackArgs a) {
     __shared__ unsigned known[kSsKnownWords];  // ops this workgroup has seen quantised
     extern __shared__ __align__(16) uint8_t rows[];  // [kSsW][a.row_bytes]: each wave's i8 row
     for (int i = threadIdx.x; i < kSsKnownWords; i += kSsW * 64) known[i] = 0u;
@@ -411,9 +414,9 @@ __global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(MT ==
             if (a.mode == XT_QUANT_AVX512) ss_quant<XT_QUANT_AVX512>(a, cur);
             else ss_quant<XT_QUANT_SCALAR>(a, cur);
         } else if (cur.flags & kSsPack5) {
-            ss_mblock<XT_PACK5, MT, MT == 4>(a, cur, areg, known);
+            ss_mblock<XT_PACK5, MT, MT == 4, R>(a, cur, areg, known);
         } else {
-            ss_mblock<XT_PACK4, MT, MT == 4>(a, cur, areg, known);
+            ss_mblock<XT_PACK4, MT, MT == 4, R>(a, cur, areg, known);
         }
     }
     // the last wave out resets the counts for the next launch (its own
@@ -435,12 +438,15 @@ __global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(MT ==
 // form's token rows.
 static size_t ss_dyn_lds(int row_bytes) { return (size_t)kSsW * row_bytes; }
 
+// Token forms: rows of the LDS region, groups per task, waves per SIMD.
+constexpr int kSsF4R = 4, kSsF4W = 3;
 int sstack_lds_rows(int M) { return M <= 4 ? 4 : (M <= 16 ? 16 : 32); }
+int sstack_groups_per_task(int M) { return M <= 4 ? kSsF4R : 4; }
 
 static const void* ss_fn(int M) {
-    if (M <= 4) return reinterpret_cast<const void*>(sstack_kernel<4>);
-    if (M <= 16) return reinterpret_cast<const void*>(sstack_kernel<16>);
-    return reinterpret_cast<const void*>(sstack_kernel<32>);
+    if (M <= 4) return reinterpret_cast<const void*>(sstack_kernel<4, kSsF4R, kSsF4W>);
+    if (M <= 16) return reinterpret_cast<const void*>(sstack_kernel<16, 4, 3>);
+    return reinterpret_cast<const void*>(sstack_kernel<32, 4, 2>);
 }
 
 hipError_t launch_sstack(const SStackArgs& a, int blocks, hipStream_t s) {
