@@ -990,20 +990,20 @@ std::vector<int> stack_order(const xt_stack_op* ops, int nops, const std::vector
 //  * one call per op: about 4.7 us per op at M = 1, 6.5 at M <= 8 and 9.4 up
 //    to M = 32 (launch to launch in a HIP graph), or the op's weight bytes at
 //    2.7 TB/s where that is longer;
-//  * one launch: the weights at 4.3 TB/s (M = 1), 3.4 (M <= 8) or 1.7 TB/s,
-//    plus about 20 / 24 / 30 us per dependency level after the first: a
+//  * one launch: the weights at 4.5 TB/s (M = 1), 3.4 (M <= 8) or 1.7 TB/s,
+//    plus about 16 / 24 / 30 us per dependency level after the first: a
 //    level's ops start only once the level before has published its outputs
-//    (device-scope stores, a count, polls, the quantiser tasks and their
-//    count), and each of its waves then walks its share of the op's tiles one
-//    chunk at a time, where a one-op launch loads all of a workgroup's tiles
-//    at once.
+//    (device-scope stores and a count; at M > 1 also the quantiser tasks and
+//    their count), and each of its waves then walks its share of the op's
+//    tiles one chunk at a time, where a one-op launch loads all of a
+//    workgroup's tiles at once.
 // The 30-layer projection stack with the residual dependency (2 levels) runs
-// in one launch in 121 us against 560 us per op at M = 1; the strict chain
-// (120 levels) took 2450 us in one launch against 598 us per op.
+// in one launch in 114 us against 560 us per op at M = 1; the strict chain
+// (120 levels) took 2027 us in one launch against 601 us per op.
 bool stack_prefers_per_op(const xt_stack_op* ops, int nops, int64_t M) {
     const double call_us = M == 1 ? 4.7 : (M <= 8 ? 6.5 : 9.4);
-    const double call_bpus = 2.7e6, launch_bpus = M == 1 ? 4.3e6 : (M <= 8 ? 3.4e6 : 1.7e6);
-    const double level_us = M == 1 ? 20.0 : (M <= 8 ? 24.0 : 30.0);
+    const double call_bpus = 2.7e6, launch_bpus = M == 1 ? 4.5e6 : (M <= 8 ? 3.4e6 : 1.7e6);
+    const double level_us = M == 1 ? 16.0 : (M <= 8 ? 24.0 : 30.0);
     std::vector<int> lvl((size_t)nops, 0);
     int depth = 0;
     double bytes = 0, per_op_us = 0;
@@ -1091,7 +1091,10 @@ int create_sstack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stac
     // groups' tiles per step and shares the chunk's activation pieces among
     // them; measured faster than 2 groups per task at M = 1 too)
     const int rg = xt::sstack_groups_per_task((int)M);
-    ntasks = (size_t)nops * (size_t)M;
+    // (M = 1: no quantiser tasks; each group task quantises the op's row)
+    const bool qtasks = xt::sstack_quant_tasks((int)M);
+    if (!qtasks) scratch = 0;
+    ntasks = qtasks ? (size_t)nops * (size_t)M : 0;
     for (int i = 0; i < nops; ++i)
         for (int p = 0; p < ops[i].n; ++p) ntasks += (size_t)(((ops[i].w[p]->N + 15) / 16 + rg - 1) / rg);
     if (ntasks > (size_t)1 << 30) return fail(XT_ERR_UNSUPPORTED, "stack too large");
@@ -1120,7 +1123,7 @@ int create_sstack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stac
     };
     auto quant_task = [&](int i) {  // one per token
         const OpInfo& f = info[(size_t)i];
-        for (int64_t m = 0; m < M; ++m) {
+        for (int64_t m = 0; m < M && qtasks; ++m) {
             xt::SStackTask t = base(i);
             t.tiles = ops[i].x + m * f.K;
             t.q = reinterpret_cast<int8_t*>(sc + f.qoff + (size_t)m * f.ldq);
@@ -1142,7 +1145,12 @@ int create_sstack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stac
                 t.tiles = w->tiles + (size_t)G * w->nch * xt::kTileBytes;
                 t.ws = w->ws + G * 16;
                 t.y = op.y[p] + G * 16;
-                t.K = (int)w->N;  // (a group task's output row stride)
+                if (qtasks) {
+                    t.K = (int)w->N;  // (a group task's output row stride)
+                } else {
+                    t.q = reinterpret_cast<int8_t*>(const_cast<float*>(op.x));  // the f32 row it quantises
+                    t.K = info[(size_t)i].K;                                   // (its length)
+                }
                 t.flags = (pub[(size_t)i] ? 2 : 0) | (info[(size_t)i].fmt == XT_PACK5 ? 4 : 0) | (n_g << 16);
                 t.nrows = (int)std::min<int64_t>(16, w->N - (G + n_g - 1) * 16);
                 tasks.push_back(t);

@@ -204,6 +204,7 @@ hipError_t launch_sstack(const SStackArgs& a, int blocks, hipStream_t s);
 hipError_t sstack_blocks_per_cu(int M, int row_bytes, int* n);
 int sstack_lds_rows(int M);         // token rows of a wave's LDS region
 int sstack_groups_per_task(int M);  // 16-row groups per group task
+bool sstack_quant_tasks(int M);     // quantiser tasks (else each group task quantises its row: M = 1)
 int sstack_waves_per_block();
 // HF prepacked striped bytes [N/f][K] (device) -> tiles (device).
 hipError_t launch_hf_tiles(int fmt, const uint8_t* stored, int64_t K, int64_t N, uint8_t* tiles,

@@ -8,12 +8,13 @@
 // quantisation (quantization.rs:95-195), the exact i32 dot of `dot_row`
 // (:216-231) over pack4 / pack5 / sparse weights, (f32)dot * inv * w_scale.
 //
-// Work list.  The host flattens the ops into tasks: one quantiser task per
+// Work list.  The host flattens the ops into tasks: (M > 1) one quantiser task per
 // op and token (the token's f32 input row -> i8 row, its exact sum and
-// inverse scale) and one task per block of four consecutive 16-row groups of
-// one projection.  Every task follows the tasks it waits for: an op's
-// quantiser tasks come after the last group of the op its input comes from,
-// its groups after its quantiser tasks.  The host deals the list out to the
+// inverse scale) and one task per block of consecutive 16-row groups of one
+// projection (at M = 1 the group tasks quantise the row themselves:
+// ss_mblock_q1).  Every task follows the tasks it waits for: an op's
+// quantiser tasks (or, at M = 1, its group tasks) come after the last group
+// of the op its input comes from, its groups after its quantiser tasks.  The host deals the list out to the
 // waves in list order, each task to the wave with the least work so far
 // (weight bytes), and every wave runs its tasks in list order.  The grid is
 // no larger than what is resident at once, so the wave holding the earliest
@@ -390,6 +391,157 @@ __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsi
     }
 }
 
+// M = 1: a group task that quantises its op's row itself (no quantiser
+// tasks, no quantised-row buffer).  It waits only for the op its input comes
+// from (if any), takes the row's absmax in one pass over the f32 row (rounds
+// of kQ1 pieces per lane in flight), then quantises each chunk's pieces as
+// it walks the chunks (the next chunk's f32 pieces load during the current
+// step), stages the chunk's i8 bytes in its LDS row and runs the R groups'
+// MFMAs on them; the row's exact sum is summed on the way.  Each task reads
+// the op's row from L2 twice (25-50 % above its weight bytes), against three
+// device-scope hops per dependency when quantiser tasks publish the rows.
+// (x is read with ordinary loads: written before the launch, or by the op it
+// depends on, whose count this task has seen complete; each 128-byte line of
+// that op's output is written by one task only.)
+template <int FMT, int MODE, int R>
+__device__ void ss_mblock_q1(const SStackArgs& a, const Rec& r, uint32_t areg, unsigned* known) {
+    constexpr int STEPS = (FMT == XT_PACK5) ? 5 : 4;
+    constexpr int CH = STEPS * 64;
+    constexpr int XP = (CH / 4 + 63) / 64;  // f32 pieces (float4) per lane per chunk: 1, or 2 for Pack5
+    constexpr int kQ1 = 14;                 // absmax pass: pieces per lane per round
+    const int lane = threadIdx.x & 63;
+    const int g = lane >> 4, j = lane & 15;
+    const int nch = r.nch, K = r.K, ng = r.ngroups, dep = r.dep;
+    (void)j;
+    if (dep >= 0 && !((known[dep >> 5] >> (dep & 31)) & 1u)) {
+        if (lane == 0)
+            ss_wait(ss_ctr(a.ctr, kSsDone0 + dep), (unsigned)r.dep_groups, ss_ctr(a.ctr, kSsError), a.spin_limit);
+        __builtin_amdgcn_wave_barrier();
+        if (lane == 0) atomicOr(&known[dep >> 5], 1u << (dep & 31));
+    }
+    const int trows = (ng - 1) * 16 + r.nrows;
+    const int wv = __float_as_int(((gfloat*)(uintptr_t)r.ws)[min(lane, trows - 1)]);
+    const uint8_t* const tl = reinterpret_cast<const uint8_t*>(r.tiles) + lane * 16;
+    auto load_tiles = [&](v4i* wb, int c) {
+#pragma unroll
+        for (int gi = 0; gi < R; ++gi)  // (groups past the block: its last group again, unused)
+            wb[gi] = ss_ld_tile(tl + ((size_t)min(gi, ng - 1) * nch + c) * kTileBytes);
+    };
+    // the first chunk's tiles go out with the absmax pass
+    v4i wb[R];
+    load_tiles(wb, 0);
+    const __amdgpu_buffer_rsrc_t xr = ss_rsrc(r.q, (unsigned)(K * 4));  // (pieces past K: zeros)
+    const int n4 = (K + 3) >> 2;
+    float mx = 0.0f;
+    for (int f0 = 0; f0 < n4; f0 += 64 * kQ1) {
+        v4i v[kQ1];
+#pragma unroll
+        for (int u = 0; u < kQ1; ++u) v[u] = __builtin_amdgcn_raw_buffer_load_b128(xr, (unsigned)(f0 + u * 64 + lane) * 16u, 0, 0);
+#pragma unroll
+        for (int u = 0; u < kQ1; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) mx = fmaxf(mx, fabsf(__int_as_float(v[u][e])));
+    }
+    const float rmx = __int_as_float(wave_reduce_bits(__float_as_int(mx), [](int p, int q) {
+        return __float_as_int(fmaxf(__int_as_float(p), __int_as_float(q)));
+    }));
+    const float scale = (rmx > 0.0f) ? __fdiv_rn(127.0f, rmx) : 1.0f;
+    const float invs = (rmx > 0.0f) ? __fdiv_rn(rmx, 127.0f) : 1.0f;
+    const int kmain = (K / 16) * 16;
+    // chunk c's f32 pieces of this lane: piece lane + 64 u (16 bytes of i8
+    // columns 4 (lane + 64 u) .. + 3 of the chunk)
+    auto load_x = [&](v4i* xp, int c) {
+#pragma unroll
+        for (int u = 0; u < XP; ++u) {
+            const int pc = lane + 64 * u;
+            const bool in = pc < CH / 4 && c < nch;
+            xp[u] = __builtin_amdgcn_raw_buffer_load_b128(xr, in ? (unsigned)(c * CH + 4 * pc) * 4u : 0x80000000u, 0, 0);
+        }
+    };
+    v4i xc[XP];
+    load_x(xc, 0);
+    int rs = 0;
+    v4i acc[R];
+#pragma unroll
+    for (int gi = 0; gi < R; ++gi) acc[gi] = v4i{0, 0, 0, 0};
+    for (int c = 0; c < nch; ++c) {
+        v4i xn[XP];
+        if (c > 0) load_tiles(wb, c);  // (uniform)
+        load_x(xn, c + 1);
+        __builtin_amdgcn_sched_barrier(0);
+        // this chunk's i8 bytes into the LDS row (layers.rs quantisation:
+        // quantization.rs:95-195), then the A fragments of row 0
+#pragma unroll
+        for (int u = 0; u < XP; ++u) {
+            const int pc = lane + 64 * u;
+            if (64 * (u + 1) <= CH / 4 || pc < CH / 4) {
+                unsigned w = 0;
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const int col = c * CH + 4 * pc + t;
+                    w |= (unsigned)(quant_one(__int_as_float(xc[u][t]), scale, MODE, col < kmain) & 255) << (8 * t);
+                }
+                rs = __builtin_amdgcn_sdot4((int)w, 0x01010101, rs, false);
+                *reinterpret_cast<__attribute__((address_space(3))) unsigned*>((uintptr_t)(areg + 4u * pc)) = w;
+            }
+        }
+        v4i af[STEPS];
+#pragma unroll
+        for (int st = 0; st < STEPS; ++st) af[st] = ss_lds16(areg + (uint32_t)(g * 16 + st * 64));
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int gi = 0; gi < R; ++gi) {
+            if constexpr (FMT == XT_PACK5) {
+                int E[4], O[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    E[q] = wb[gi][q] & 0x00ff00ff;
+                    O[q] = ((unsigned)wb[gi][q] >> 8) & 0x00ff00ff;
+                }
+#pragma unroll
+                for (int st = 0; st < STEPS; ++st) {
+                    v4i b;
+#pragma unroll
+                    for (int q = 0; q < 4; ++q) {
+                        const int pE = E[q] * 3, pO = O[q] * 3;
+                        b[q] = (int)__builtin_amdgcn_perm((unsigned)pO, (unsigned)pE, 0x07030501u);
+                        E[q] = pE & 0x00ff00ff;
+                        O[q] = pO & 0x00ff00ff;
+                    }
+                    acc[gi] = mfma(af[st], b, acc[gi]);
+                }
+            } else {
+#pragma unroll
+                for (int st = 0; st < STEPS; ++st) acc[gi] = mfma(af[st], decode4(wb[gi][st]), acc[gi]);
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < XP; ++u) xc[u] = xn[u];
+    }
+    rs = wave_reduce_bits(rs, [](int p, int q) { return p + q; });
+    // acc[gi][0] of lanes 0-15: the token, row j of group gi; the MFMAs took
+    // codes w + 1, so the row's sum comes off (layers.rs:340)
+    const bool pub = (r.flags & kSsPub) != 0;
+    const __amdgpu_buffer_rsrc_t yr = ss_rsrc(r.y, (unsigned)(trows * 4));
+#pragma unroll
+    for (int gi = 0; gi < R; ++gi) {
+        if (gi >= ng) break;  // (uniform)
+        const int row = gi * 16 + (lane & 15);
+        const float wsc = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * min(row, trows - 1), wv));
+        if (lane < 16 && row < trows) {
+            const float v = __fmul_rn(__fmul_rn((float)(acc[gi][0] - rs), invs), wsc);
+            if (pub) ss_st_coh4(yr, (unsigned)(row * 4), __float_as_uint(v));
+            else ((gfloat_w*)(uintptr_t)r.y)[row] = v;
+        }
+    }
+    if (pub) {  // another op reads these outputs inside the launch
+        __builtin_amdgcn_s_waitcnt(0);
+        if (lane == 0)
+            __hip_atomic_fetch_add(ss_ctr(a.ctr, kSsDone0 + r.opi), (unsigned)ng, __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
+    }
+}
+
 // MT: the token form (see ss_mblock).  Three waves per SIMD: up to 168
 // registers for a task's tiles, activation pieces, A fragments and the four
 // groups' accumulators.
@@ -413,6 +565,14 @@ __global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(WPE))
         if (cur.flags & kSsQuant) {
             if (a.mode == XT_QUANT_AVX512) ss_quant<XT_QUANT_AVX512>(a, cur);
             else ss_quant<XT_QUANT_SCALAR>(a, cur);
+        } else if constexpr (MT == 1) {
+            if (cur.flags & kSsPack5) {
+                if (a.mode == XT_QUANT_AVX512) ss_mblock_q1<XT_PACK5, XT_QUANT_AVX512, R>(a, cur, areg, known);
+                else ss_mblock_q1<XT_PACK5, XT_QUANT_SCALAR, R>(a, cur, areg, known);
+            } else {
+                if (a.mode == XT_QUANT_AVX512) ss_mblock_q1<XT_PACK4, XT_QUANT_AVX512, R>(a, cur, areg, known);
+                else ss_mblock_q1<XT_PACK4, XT_QUANT_SCALAR, R>(a, cur, areg, known);
+            }
         } else if (cur.flags & kSsPack5) {
             ss_mblock<XT_PACK5, MT, MT == 4, R>(a, cur, areg, known);
         } else {
@@ -440,10 +600,12 @@ static size_t ss_dyn_lds(int row_bytes) { return (size_t)kSsW * row_bytes; }
 
 // Token forms: rows of the LDS region, groups per task, waves per SIMD.
 constexpr int kSsF4R = 4, kSsF4W = 3;
-int sstack_lds_rows(int M) { return M <= 4 ? 4 : (M <= 16 ? 16 : 32); }
+int sstack_lds_rows(int M) { return M == 1 ? 1 : (M <= 4 ? 4 : (M <= 16 ? 16 : 32)); }
 int sstack_groups_per_task(int M) { return M <= 4 ? kSsF4R : 4; }
+bool sstack_quant_tasks(int M) { return M > 1; }
 
 static const void* ss_fn(int M) {
+    if (M == 1) return reinterpret_cast<const void*>(sstack_kernel<1, 4, 3>);
     if (M <= 4) return reinterpret_cast<const void*>(sstack_kernel<4, kSsF4R, kSsF4W>);
     if (M <= 16) return reinterpret_cast<const void*>(sstack_kernel<16, 4, 3>);
     return reinterpret_cast<const void*>(sstack_kernel<32, 4, 2>);
