@@ -990,20 +990,20 @@ std::vector<int> stack_order(const xt_stack_op* ops, int nops, const std::vector
 //  * one call per op: about 4.7 us per op at M = 1, 6.5 at M <= 8 and 9.4 up
 //    to M = 32 (launch to launch in a HIP graph), or the op's weight bytes at
 //    2.7 TB/s where that is longer;
-//  * one launch: the weights at 4.5 TB/s (M = 1), 3.4 (M <= 8) or 1.7 TB/s,
-//    plus about 16 / 24 / 30 us per dependency level after the first: a
+//  * one launch: the weights at 4.8 TB/s (M = 1), 3.4 (M <= 8) or 1.7 TB/s,
+//    plus about 18 / 24 / 30 us per dependency level after the first: a
 //    level's ops start only once the level before has published its outputs
 //    (device-scope stores and a count; at M > 1 also the quantiser tasks and
 //    their count), and each of its waves then walks its share of the op's
 //    tiles one chunk at a time, where a one-op launch loads all of a
 //    workgroup's tiles at once.
 // The 30-layer projection stack with the residual dependency (2 levels) runs
-// in one launch in 114 us against 560 us per op at M = 1; the strict chain
-// (120 levels) took 2027 us in one launch against 601 us per op.
+// in one launch in 108.5 us against 562 us per op at M = 1; the strict chain
+// (120 levels) took 2307 us in one launch against 602 us per op.
 bool stack_prefers_per_op(const xt_stack_op* ops, int nops, int64_t M) {
     const double call_us = M == 1 ? 4.7 : (M <= 8 ? 6.5 : 9.4);
-    const double call_bpus = 2.7e6, launch_bpus = M == 1 ? 4.5e6 : (M <= 8 ? 3.4e6 : 1.7e6);
-    const double level_us = M == 1 ? 16.0 : (M <= 8 ? 24.0 : 30.0);
+    const double call_bpus = 2.7e6, launch_bpus = M == 1 ? 4.8e6 : (M <= 8 ? 3.4e6 : 1.7e6);
+    const double level_us = M == 1 ? 18.0 : (M <= 8 ? 24.0 : 30.0);
     std::vector<int> lvl((size_t)nops, 0);
     int depth = 0;
     double bytes = 0, per_op_us = 0;

@@ -420,7 +420,10 @@ __device__ void ss_mblock_q1(const SStackArgs& a, const Rec& r, uint32_t areg, u
         if (lane == 0) atomicOr(&known[dep >> 5], 1u << (dep & 31));
     }
     const int trows = (ng - 1) * 16 + r.nrows;
-    const int wv = __float_as_int(((gfloat*)(uintptr_t)r.ws)[min(lane, trows - 1)]);
+    constexpr int WH = (R * 16 + 63) / 64;  // registers for the block's w_scales: lane l, row l + 64 h
+    int wv[WH];
+#pragma unroll
+    for (int h = 0; h < WH; ++h) wv[h] = __float_as_int(((gfloat*)(uintptr_t)r.ws)[min(lane + 64 * h, trows - 1)]);
     const uint8_t* const tl = reinterpret_cast<const uint8_t*>(r.tiles) + lane * 16;
     auto load_tiles = [&](v4i* wb, int c) {
 #pragma unroll
@@ -527,7 +530,8 @@ __device__ void ss_mblock_q1(const SStackArgs& a, const Rec& r, uint32_t areg, u
     for (int gi = 0; gi < R; ++gi) {
         if (gi >= ng) break;  // (uniform)
         const int row = gi * 16 + (lane & 15);
-        const float wsc = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * min(row, trows - 1), wv));
+        const int rw = min(row, trows - 1);  // (gi * 16 / 64 is uniform: the register is known)
+        const float wsc = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (rw & 63), wv[(gi * 16) >> 6]));
         if (lane < 16 && row < trows) {
             const float v = __fmul_rn(__fmul_rn((float)(acc[gi][0] - rs), invs), wsc);
             if (pub) ss_st_coh4(yr, (unsigned)(row * 4), __float_as_uint(v));
@@ -599,13 +603,17 @@ __global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(WPE))
 static size_t ss_dyn_lds(int row_bytes) { return (size_t)kSsW * row_bytes; }
 
 // Token forms: rows of the LDS region, groups per task, waves per SIMD.
+// M = 1: eight groups per task at two waves per SIMD (183 registers) ran the
+// C4 list in 108.5 us against 114 us with four at three (and six at three:
+// 117 us); more bytes per step per wave beat more waves here.
 constexpr int kSsF4R = 4, kSsF4W = 3;
+constexpr int kSsF1R = 8, kSsF1W = 2;
 int sstack_lds_rows(int M) { return M == 1 ? 1 : (M <= 4 ? 4 : (M <= 16 ? 16 : 32)); }
-int sstack_groups_per_task(int M) { return M <= 4 ? kSsF4R : 4; }
+int sstack_groups_per_task(int M) { return M == 1 ? kSsF1R : (M <= 4 ? kSsF4R : 4); }
 bool sstack_quant_tasks(int M) { return M > 1; }
 
 static const void* ss_fn(int M) {
-    if (M == 1) return reinterpret_cast<const void*>(sstack_kernel<1, 4, 3>);
+    if (M == 1) return reinterpret_cast<const void*>(sstack_kernel<1, kSsF1R, kSsF1W>);
     if (M <= 4) return reinterpret_cast<const void*>(sstack_kernel<4, kSsF4R, kSsF4W>);
     if (M <= 16) return reinterpret_cast<const void*>(sstack_kernel<16, 4, 3>);
     return reinterpret_cast<const void*>(sstack_kernel<32, 4, 2>);
