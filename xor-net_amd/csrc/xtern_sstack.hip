@@ -255,11 +255,14 @@ __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsi
     // task's end on a memory latency with nothing else in flight): lane l <
     // 2M slot l of the op's M row sums and M inverse scales (device-scope
     // loads: those slots share lines that quantiser tasks on other XCDs
-    // wrote); lane l the w_scale of row l of the block.
+    // wrote); lane l the w_scales of rows l and l + 64 of the block.
     const int trows = (ng - 1) * 16 + r.nrows;
     const __amdgpu_buffer_rsrc_t sr = ss_rsrc(r.q + (size_t)M * ldq, (unsigned)(8 * M));
     const int sv = (int)__builtin_amdgcn_raw_buffer_load_b32(sr, lane < 2 * M ? 4u * lane : 0x80000000u, 0, kSsCoh);
-    const int wv = __float_as_int(((gfloat*)(uintptr_t)r.ws)[min(lane, trows - 1)]);
+    constexpr int WH = (R * 16 + 63) / 64;  // registers for the block's w_scales: lane l, row l + 64 h
+    int wv[WH];
+#pragma unroll
+    for (int h = 0; h < WH; ++h) wv[h] = __float_as_int(((gfloat*)(uintptr_t)r.ws)[min(lane + 64 * h, trows - 1)]);
     // the activation pieces of one chunk: piece p = lane + 64 u is token
     // p / PR, bytes (p % PR) * 16; tokens >= M read nothing (outside the
     // resource) and leave rows of the LDS region the outputs never use
@@ -350,8 +353,8 @@ __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsi
     // this lane's outputs: tokens 16 tb + 4g .. + 3, row j of each group
     float wsc[R];
 #pragma unroll
-    for (int gi = 0; gi < R; ++gi)
-        wsc[gi] = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * min(gi * 16 + j, trows - 1), wv));
+    for (int gi = 0; gi < R; ++gi)  // (rows past trows are never stored)
+        wsc[gi] = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (min(gi * 16 + j, trows - 1) & 63), wv[(gi * 16) >> 6]));
 
     // acc[tb][gi][t]: token 16 tb + 4g + t, row j of group gi; the MFMAs took
     // codes w + 1, so the token's sum comes off (layers.rs:340: (dot as f32 *
@@ -605,17 +608,21 @@ static size_t ss_dyn_lds(int row_bytes) { return (size_t)kSsW * row_bytes; }
 // Token forms: rows of the LDS region, groups per task, waves per SIMD.
 // M = 1: eight groups per task at two waves per SIMD (183 registers) ran the
 // C4 list in 108.5 us against 114 us with four at three (and six at three:
-// 117 us); more bytes per step per wave beat more waves here.
-constexpr int kSsF4R = 4, kSsF4W = 3;
+// 117 us); more bytes per step per wave beat more waves here.  M = 2 .. 4
+// likewise (121 independent C0 ops at M = 4: 120 against 125.6 us); the
+// 16-token form gained 1.5 % on those ops and nothing on the C4 list with
+// eight groups, so it keeps four at three waves per SIMD.
+constexpr int kSsF4R = 8, kSsF4W = 2;
 constexpr int kSsF1R = 8, kSsF1W = 2;
+constexpr int kSsF16R = 4, kSsF16W = 3;
 int sstack_lds_rows(int M) { return M == 1 ? 1 : (M <= 4 ? 4 : (M <= 16 ? 16 : 32)); }
-int sstack_groups_per_task(int M) { return M == 1 ? kSsF1R : (M <= 4 ? kSsF4R : 4); }
+int sstack_groups_per_task(int M) { return M == 1 ? kSsF1R : (M <= 4 ? kSsF4R : (M <= 16 ? kSsF16R : 4)); }
 bool sstack_quant_tasks(int M) { return M > 1; }
 
 static const void* ss_fn(int M) {
     if (M == 1) return reinterpret_cast<const void*>(sstack_kernel<1, kSsF1R, kSsF1W>);
     if (M <= 4) return reinterpret_cast<const void*>(sstack_kernel<4, kSsF4R, kSsF4W>);
-    if (M <= 16) return reinterpret_cast<const void*>(sstack_kernel<16, 4, 3>);
+    if (M <= 16) return reinterpret_cast<const void*>(sstack_kernel<16, kSsF16R, kSsF16W>);
     return reinterpret_cast<const void*>(sstack_kernel<32, 4, 2>);
 }
 
