@@ -114,6 +114,25 @@ class Graph:
                 fn(i)
         self.n = n
 
+    def time_ms_median(self, replays):
+        """Median, min and max ms per captured call over `replays` replays,
+        each replay timed on its own (HIP events on the replay stream); one
+        untimed replay first."""
+        torch = self.torch
+        per = []
+        with torch.cuda.stream(self.stream):
+            self.g.replay()
+            for _ in range(replays):
+                a = torch.cuda.Event(enable_timing=True)
+                b = torch.cuda.Event(enable_timing=True)
+                a.record()
+                self.g.replay()
+                b.record()
+                b.synchronize()
+                per.append(a.elapsed_time(b) / self.n)
+        per.sort()
+        return per[len(per) // 2], per[0], per[-1]
+
     def time_ms(self, replays):
         """Average ms per captured call over `replays` replays (HIP events on
         the replay stream)."""
@@ -268,10 +287,11 @@ def gemv_sustained(np, torch, xtern, rng, ncopies=121, reps=10):
     y1 = torch.empty((M, N), dtype=torch.float32, device="cuda")
     xtern.linear_q(w1, q, inv, out=y1)
     torch.cuda.synchronize()
-    # four launches back to back per graph: launch-to-launch time, as for
-    # the per-call lines (a one-launch graph adds the replay's own gap)
-    g = Graph(torch, lambda i: xtern.linear_q(w, q, inv, out=y), 4)
-    ms = g.time_ms(reps)
+    # eight launches back to back per graph: launch-to-launch time, as for
+    # the per-call lines (a graph of one launch adds the replay's own gap:
+    # 87-94 us there against 84-85 us with 8 or 16 per graph)
+    g = Graph(torch, lambda i: xtern.linear_q(w, q, inv, out=y), 8)
+    ms, ms_lo, ms_hi = g.time_ms_median(9)
     if not torch.equal(y.view(ncopies, N), y1.expand(ncopies, N)):
         raise SystemExit("sustained GEMV: a copy's output differs from the single-matrix output")
     alg = NT * (K // 4) + M * K + 4 * M + 4 * NT + 4 * M * NT
@@ -285,8 +305,8 @@ def gemv_sustained(np, torch, xtern, rng, ncopies=121, reps=10):
     xs = [torch.from_numpy(rng.standard_normal((M, K)).astype(np.float32)).cuda() for _ in range(ncopies)]
     ys = [torch.empty((M, N), dtype=torch.float32, device="cuda") for _ in range(ncopies)]
     st = xtern.Stack([([w_], x_, [y_], None) for w_, x_, y_ in zip(copies, xs, ys)], M)
-    gs = Graph(torch, lambda _i: st.run(), 4)
-    ms_st = gs.time_ms(reps)
+    gs = Graph(torch, lambda _i: st.run(), 8)
+    ms_st, st_lo, st_hi = gs.time_ms_median(9)
     if st.gave_up():
         raise SystemExit("sustained stack: a dependency wait gave up")
     for w_, x_, y_ in zip(copies[:4], xs[:4], ys[:4]):
@@ -297,11 +317,15 @@ def gemv_sustained(np, torch, xtern, rng, ncopies=121, reps=10):
     del gs, st, copies, w1
     torch.cuda.empty_cache()
     return {"workload": "c0_sustained", "K": K, "N_per_copy": N, "copies": ncopies, "M": M,
-            "us_per_launch": round(ms * 1e3, 2), "alg_bytes_per_launch": alg,
+            "us_per_launch": round(ms * 1e3, 2),
+            "us_per_launch_min_max": [round(ms_lo * 1e3, 2), round(ms_hi * 1e3, 2)],
+            "timing": "median of 9 graph replays of 8 back-to-back launches, each replay timed",
+            "alg_bytes_per_launch": alg,
             "roofline": {"bound": "hbm", "achieved": round(gbs, 1), "peak": HBM_PEAK_GBS,
                          "unit": "GB/s", "frac": round(gbs / HBM_PEAK_GBS, 4)},
             "checked": "every copy's 6912 outputs bit-equal to the single C0 product",
             "stack_us_per_launch": round(ms_st * 1e3, 2),
+            "stack_us_min_max": [round(st_lo * 1e3, 2), round(st_hi * 1e3, 2)],
             "stack_GBs": round(gbs_st, 1), "stack_hbm_frac": round(gbs_st / HBM_PEAK_GBS, 4),
             "stack_form": f"{ncopies} independent C0 ops (f32 in, quantised in the launch) in one "
                           f"xt_stack launch; checked against per-call outputs"}
@@ -471,10 +495,10 @@ def stack_c4(np, torch, xtern, rng, Ms=(1, 8, 32), layers=30):
                                ("chain_one_launch", ops_chain(), "one_launch")):
             st = xtern.Stack(ops, M, plan=plan)
             row[f"{tag}_plan"] = st.plan_name
-            # runs back to back in one graph (launch to launch; the runs are
-            # ordered on the graph's stream, as the stack requires)
-            gs = Graph(torch, lambda _i: st.run(), 4)
-            us_p = gs.time_ms(3) * 1e3
+            # eight runs back to back in one graph (launch to launch; the runs
+            # are ordered on the graph's stream, as the stack requires)
+            gs = Graph(torch, lambda _i: st.run(), 8)
+            us_p = gs.time_ms_median(5)[0] * 1e3  # (median of 5 replays of 8 runs)
             if st.gave_up():
                 raise SystemExit("decode stack: a dependency wait gave up")
             # bit-exact against one call per op, in list order (a chained
