@@ -226,11 +226,11 @@ __device__ void ss_quant(const SStackArgs& a, const Rec& r) {
 // host pads the row pitch), so its L2 holds no stale copy, and later tasks
 // of the op on the XCD hit in it.
 //
-// MT: token rows the LDS region holds (4 for M <= 4, 16, or 32: two blocks
-// of 16 tokens, each weight tile decoded once per k-step for both blocks'
-// MFMAs).  PF: the next chunk's activation pieces are loaded during this
-// step (registers allowing: MT = 4), so a step stages its pieces in LDS and
-// reads its A fragments while its tiles are still in flight.
+// MT: token rows the LDS region holds (4 for M <= 4, 8, 16, or 32: two
+// blocks of 16 tokens, each weight tile decoded once per k-step for both
+// blocks' MFMAs).  PF: the next chunk's activation pieces are loaded during
+// this step (registers allowing: MT <= 8), so a step stages its pieces in
+// LDS and reads its A fragments while its tiles are still in flight.
 // R: 16-row groups per task, at most (the host deals blocks of R).
 template <int FMT, int MT, bool PF, int R>
 __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsigned* known) {
@@ -581,9 +581,9 @@ __global__ __launch_bounds__(kSsW * 64) __attribute__((amdgpu_waves_per_eu(WPE))
                 else ss_mblock_q1<XT_PACK4, XT_QUANT_SCALAR, R>(a, cur, areg, known);
             }
         } else if (cur.flags & kSsPack5) {
-            ss_mblock<XT_PACK5, MT, MT == 4, R>(a, cur, areg, known);
+            ss_mblock<XT_PACK5, MT, MT <= 8, R>(a, cur, areg, known);
         } else {
-            ss_mblock<XT_PACK4, MT, MT == 4, R>(a, cur, areg, known);
+            ss_mblock<XT_PACK4, MT, MT <= 8, R>(a, cur, areg, known);
         }
     }
     // the last wave out resets the counts for the next launch (its own
@@ -611,17 +611,23 @@ static size_t ss_dyn_lds(int row_bytes) { return (size_t)kSsW * row_bytes; }
 // 117 us); more bytes per step per wave beat more waves here.  M = 2 .. 4
 // likewise (121 independent C0 ops at M = 4: 120 against 125.6 us); the
 // 16-token form gained 1.5 % on those ops and nothing on the C4 list with
-// eight groups, so it keeps four at three waves per SIMD.
+// eight groups, so it keeps four at three waves per SIMD; an 8-token form
+// with eight groups and the next chunk's pieces in flight took the M = 8
+// C4 list from 152 to 146 us.
 constexpr int kSsF4R = 8, kSsF4W = 2;
 constexpr int kSsF1R = 8, kSsF1W = 2;
+constexpr int kSsF8R = 8, kSsF8W = 2;
 constexpr int kSsF16R = 4, kSsF16W = 3;
-int sstack_lds_rows(int M) { return M == 1 ? 1 : (M <= 4 ? 4 : (M <= 16 ? 16 : 32)); }
-int sstack_groups_per_task(int M) { return M == 1 ? kSsF1R : (M <= 4 ? kSsF4R : (M <= 16 ? kSsF16R : 4)); }
+int sstack_lds_rows(int M) { return M == 1 ? 1 : (M <= 4 ? 4 : (M <= 8 ? 8 : (M <= 16 ? 16 : 32))); }
+int sstack_groups_per_task(int M) {
+    return M == 1 ? kSsF1R : (M <= 4 ? kSsF4R : (M <= 8 ? kSsF8R : (M <= 16 ? kSsF16R : 4)));
+}
 bool sstack_quant_tasks(int M) { return M > 1; }
 
 static const void* ss_fn(int M) {
     if (M == 1) return reinterpret_cast<const void*>(sstack_kernel<1, kSsF1R, kSsF1W>);
     if (M <= 4) return reinterpret_cast<const void*>(sstack_kernel<4, kSsF4R, kSsF4W>);
+    if (M <= 8) return reinterpret_cast<const void*>(sstack_kernel<8, kSsF8R, kSsF8W>);
     if (M <= 16) return reinterpret_cast<const void*>(sstack_kernel<16, kSsF16R, kSsF16W>);
     return reinterpret_cast<const void*>(sstack_kernel<32, 4, 2>);
 }
