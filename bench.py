@@ -22,7 +22,7 @@ Also reported, from the same process:
                VNNI dot, min(nproc, 8) threads, per-token tasks) on a bounded
                sample of the same workload
 
-    python bench.py [--steps K] [--warmup W] [--workload c1|c0|c3|c4]
+    python bench.py [--steps K] [--warmup W] [--workload c1|c0|c0s|c2s|c3|c4]
                     [--no-cpu] [--copy-calibration]
 """
 import argparse
@@ -551,6 +551,77 @@ def lm_head(np, torch, xtern, rng, Ms=(1, 16)):
     return res
 
 
+def stack_c2_pack5(np, torch, xtern, rng, Ms=(1, 8), layers=26):
+    """The Pack5 weights of BASELINE config 2 (BitNet-3B shapes, P(0) = 0.4)
+    as a decode stack: 26 layers x {q, k, v, o, gate, up, down} (548 MB of
+    distinct device weights, > 2x the MALL), residual dependency only (as
+    stack_c4's residual_only), one launch, against one library call per op;
+    every output checked bit-exact against the per-call one.  Not a BASELINE
+    metric: it shows the Pack5 format streaming through the one-launch plan."""
+    shapes = {"q": (3200, 3200), "k": (3200, 320), "v": (3200, 320), "o": (3200, 3200),
+              "gate": (3200, 8640), "up": (3200, 8640), "down": (8640, 3200)}
+    proto = {n: tern_bytes(np, rng, N, K, xtern.XT_PACK5, p0=0.4)[0] for n, (K, N) in shapes.items()}
+    W = [{n: xtern.DeviceWeights(xtern.XT_PACK5, K, N, proto[n],
+                                 np.full(N, 1.0 / np.sqrt(0.6 * K), np.float32))
+          for n, (K, N) in shapes.items()} for _ in range(layers)]
+    wbytes = sum(w.device_bytes() for L in W for w in L.values())
+    res = []
+    for M in Ms:
+        f32 = torch.float32
+        xa = torch.from_numpy(rng.standard_normal((M, 3200)).astype(np.float32)).cuda()
+        xo = [torch.from_numpy(rng.standard_normal((M, 3200)).astype(np.float32)).cuda() for _ in range(layers)]
+        xd = [torch.from_numpy(rng.standard_normal((M, 8640)).astype(np.float32)).cuda() for _ in range(layers)]
+        outs = [{n: torch.empty((M, N), dtype=f32, device="cuda") for n, (K, N) in shapes.items()}
+                for _ in range(layers)]
+        ops = []
+        h, dep = xa, None
+        for L in range(layers):
+            w, o = W[L], outs[L]
+            ops.append(([w["down"]], xd[L], [o["down"]], None))
+            dn = len(ops) - 1
+            ops.append(([w["q"], w["k"], w["v"]], h, [o["q"], o["k"], o["v"]], dep))
+            ops.append(([w["o"]], xo[L], [o["o"]], None))
+            ops.append(([w["gate"], w["up"]], h, [o["gate"], o["up"]], dep))
+            h, dep = o["down"], dn
+
+        def per_call(_i):
+            for ws_, x_, ys_, _d in ops:
+                if len(ws_) == 1:
+                    xtern.linear_f32(ws_[0], x_, out=ys_[0])
+                else:
+                    xtern.linear_multi_f32(ws_, x_, outs=ys_)
+        g = Graph(torch, per_call, 1)
+        us_call = g.time_ms(5) * 1e3
+        del g
+        st = xtern.Stack(ops, M)
+        gs = Graph(torch, lambda _i: st.run(), 8)
+        us = gs.time_ms_median(5)[0] * 1e3
+        if st.gave_up():
+            raise SystemExit("pack5 stack: a dependency wait gave up")
+        for ws_, x_, ys_, _d in ops:
+            ref = [torch.empty_like(y) for y in ys_]
+            if len(ws_) == 1:
+                xtern.linear_f32(ws_[0], x_, out=ref[0])
+            else:
+                xtern.linear_multi_f32(ws_, x_, outs=ref)
+            for a_, b_ in zip(ys_, ref):
+                if not torch.isfinite(a_).all() or not torch.equal(a_, b_):
+                    raise SystemExit("pack5 stack output differs from the per-call output")
+        res.append({"workload": "c2_pack5_projection_stack_bitnet3b", "M": M, "layers": layers,
+                    "weight_bytes": wbytes, "plan": st.plan_name,
+                    "us_per_stack_per_call": round(us_call, 1),
+                    "us_per_stack": round(us, 1),
+                    "weight_GBs": round(wbytes / (us * 1e-6) / 1e9, 1),
+                    "hbm_frac": round(wbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                    "checked": "bit-exact vs per-call outputs",
+                    "timing": "median of 5 graph replays of 8 back-to-back runs"})
+        del gs, st, outs, xo, xd
+        torch.cuda.empty_cache()
+    del W
+    torch.cuda.empty_cache()
+    return res
+
+
 def mlp_block_c4(np, torch, xtern, rng, Ms=(1, 8), layers=30):
     """The BitNet-2B MLP block of the decode step as the reference's
     fused_mlp_all runs it (layers.rs:497-645): gate+up on one quantised input,
@@ -823,11 +894,15 @@ def main():
     if args.workload == "c4":
         print(json.dumps({"c4": stack_c4(np, torch, xtern, rng)}))
         return
+    if args.workload == "c2s":
+        print(json.dumps({"c2_stack": stack_c2_pack5(np, torch, xtern, rng)}))
+        return
     if args.workload == "c3":
         print(json.dumps({"c3": gemv_configs(np, torch, xtern, rng, only="c3")}))
         return
     if args.workload != "c1":
-        raise SystemExit("workloads: c1 (the headline step), c0 (the M=1 GEMV alone), "
+        raise SystemExit("workloads: c1 (the headline step), c0 (the M=1 GEMV alone), c0s (the "
+                         "C0 GEMV sustained over 121 matrices), c2s (the Pack5 BitNet-3B stack), "
                          "c3 (XorSparse: tiles and compact stream), c4 (stack)")
     log("setting up c1 weights (rotating copies) ...")
     wl = workload_c1(np, torch, xtern, rng)
@@ -869,6 +944,8 @@ def main():
         out["configs"] = gemv_configs(np, torch, xtern, rng)
         log("c4 stack ...")
         out["configs"] += stack_c4(np, torch, xtern, rng)
+        log("c2 pack5 stack ...")
+        out["configs"] += stack_c2_pack5(np, torch, xtern, rng)
         log("c4 mlp block ...")
         out["configs"] += mlp_block_c4(np, torch, xtern, rng)
         log("lm head ...")
