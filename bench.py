@@ -551,7 +551,7 @@ def lm_head(np, torch, xtern, rng, Ms=(1, 16)):
     return res
 
 
-def stack_c2_pack5(np, torch, xtern, rng, Ms=(1, 8), layers=26):
+def stack_c2_pack5(np, torch, xtern, rng, Ms=(1, 4, 8), layers=26):
     """The Pack5 weights of BASELINE config 2 (BitNet-3B shapes, P(0) = 0.4)
     as a decode stack: 26 layers x {q, k, v, o, gate, up, down} (548 MB of
     distinct device weights, > 2x the MALL), residual dependency only (as

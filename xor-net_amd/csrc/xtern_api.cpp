@@ -1087,10 +1087,19 @@ int create_sstack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stac
     int dev0 = 0, cus0 = 0;
     XT_HIP(hipGetDevice(&dev0));
     XT_HIP(hipDeviceGetAttribute(&cus0, hipDeviceAttributeMultiprocessorCount, dev0));
-    // 16-row groups per task: 4 (the kernel loads and multiplies four
-    // groups' tiles per step and shares the chunk's activation pieces among
-    // them; measured faster than 2 groups per task at M = 1 too)
-    const int rg = xt::sstack_groups_per_task((int)M);
+    // the token form: Pack5 forms when Pack5 tiles are most of the bytes
+    double p5_bytes = 0.0, all_bytes = 0.0;
+    for (int i = 0; i < nops; ++i)
+        for (int p = 0; p < ops[i].n; ++p) {
+            const double b = (double)((ops[i].w[p]->N + 15) / 16) * (double)ops[i].w[p]->nch;
+            all_bytes += b;
+            if (info[(size_t)i].fmt == XT_PACK5) p5_bytes += b;
+        }
+    const bool p5 = 2.0 * p5_bytes > all_bytes;
+    // 16-row groups per task (the kernel loads and multiplies all of a
+    // task's groups' tiles per step and shares the chunk's activation pieces
+    // among them)
+    const int rg = xt::sstack_groups_per_task((int)M, p5);
     // (M = 1: no quantiser tasks; each group task quantises the op's row)
     const bool qtasks = xt::sstack_quant_tasks((int)M);
     if (!qtasks) scratch = 0;
@@ -1166,7 +1175,7 @@ int create_sstack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stac
     int row_bytes = 1024;
     for (const OpInfo& f : info)
         row_bytes = std::max(row_bytes, xt::sstack_lds_rows((int)M) * (xt::chunk_cols(f.fmt) + 16));
-    e = xt::sstack_blocks_per_cu((int)M, row_bytes, &per_cu);
+    e = xt::sstack_blocks_per_cu((int)M, p5, row_bytes, &per_cu);
     if (e == hipSuccess && per_cu < 1) e = hipErrorInvalidConfiguration;
     const int grid = std::max(1, std::min(cus0 * std::min(per_cu, 4), ((int)tasks.size() + wpb - 1) / wpb));
     const int nw = grid * wpb;
@@ -1219,6 +1228,7 @@ int create_sstack(const xt_stack_op* ops, int nops, int64_t M, int mode, xt_stac
     st->sargs.woff = reinterpret_cast<const int*>(mem + tasks_b + ctr_b + scratch);
     st->sargs.row_bytes = row_bytes;
     st->sargs.M = (int)M;
+    st->sargs.pack5 = p5 ? 1 : 0;
     st->blocks = grid;
     st->device = dev0;
     st->dev_mem = mem;

@@ -199,11 +199,12 @@ struct SStackArgs {
     int ntasks, nops, mode, spin_limit;
     int row_bytes;            // LDS per wave: one chunk of the form's token rows, padded
     int M;                    // tokens, 1..kSStackMaxM
+    int pack5;                // 1: the base-3 token forms (Pack5 tiles are most of the bytes)
 };
 hipError_t launch_sstack(const SStackArgs& a, int blocks, hipStream_t s);
-hipError_t sstack_blocks_per_cu(int M, int row_bytes, int* n);
+hipError_t sstack_blocks_per_cu(int M, bool p5, int row_bytes, int* n);
 int sstack_lds_rows(int M);         // token rows of a wave's LDS region
-int sstack_groups_per_task(int M);  // 16-row groups per group task
+int sstack_groups_per_task(int M, bool p5);  // 16-row groups per group task
 bool sstack_quant_tasks(int M);     // quantiser tasks (else each group task quantises its row: M = 1)
 int sstack_waves_per_block();
 // HF prepacked striped bytes [N/f][K] (device) -> tiles (device).

@@ -618,13 +618,26 @@ constexpr int kSsF4R = 8, kSsF4W = 2;
 constexpr int kSsF1R = 8, kSsF1W = 2;
 constexpr int kSsF8R = 8, kSsF8W = 2;
 constexpr int kSsF16R = 4, kSsF16W = 3;
+// Base-3 forms (Pack5 tiles are most of the stack's bytes), M <= 8.  A Pack5
+// tile's decode is five multiply-mask-permute rounds per dword and k-step
+// against Pack4's one permute, so the VALU work per tile is several times
+// Pack4's and more waves hide it better than more groups per wave: four
+// groups at three waves per SIMD ran the 26-layer BitNet-3B Pack5 stack in
+// 194 / 194 / 199 us at M = 1 / 4 / 8 against 247 / 230 / 254 us with the
+// Pack4 forms (two groups at four waves: 218 / 225 / 226 us; three groups at
+// four waves for M = 1 and three at three above: 203 / 211 / 216 us).
+constexpr int kSsP5R = 4, kSsP5W = 3;
 int sstack_lds_rows(int M) { return M == 1 ? 1 : (M <= 4 ? 4 : (M <= 8 ? 8 : (M <= 16 ? 16 : 32))); }
-int sstack_groups_per_task(int M) {
+int sstack_groups_per_task(int M, bool p5) {
+    if (p5 && M <= 8) return kSsP5R;
     return M == 1 ? kSsF1R : (M <= 4 ? kSsF4R : (M <= 8 ? kSsF8R : (M <= 16 ? kSsF16R : 4)));
 }
 bool sstack_quant_tasks(int M) { return M > 1; }
 
-static const void* ss_fn(int M) {
+static const void* ss_fn(int M, bool p5) {
+    if (p5 && M == 1) return reinterpret_cast<const void*>(sstack_kernel<1, kSsP5R, kSsP5W>);
+    if (p5 && M <= 4) return reinterpret_cast<const void*>(sstack_kernel<4, kSsP5R, kSsP5W>);
+    if (p5 && M <= 8) return reinterpret_cast<const void*>(sstack_kernel<8, kSsP5R, kSsP5W>);
     if (M == 1) return reinterpret_cast<const void*>(sstack_kernel<1, kSsF1R, kSsF1W>);
     if (M <= 4) return reinterpret_cast<const void*>(sstack_kernel<4, kSsF4R, kSsF4W>);
     if (M <= 8) return reinterpret_cast<const void*>(sstack_kernel<8, kSsF8R, kSsF8W>);
@@ -635,11 +648,11 @@ static const void* ss_fn(int M) {
 hipError_t launch_sstack(const SStackArgs& a, int blocks, hipStream_t s) {
     if (a.M < 1 || a.M > kSStackMaxM) return hipErrorInvalidValue;
     void* args[] = {const_cast<SStackArgs*>(&a)};
-    return hipLaunchKernel(ss_fn(a.M), dim3(blocks), dim3(kSsW * 64), args, ss_dyn_lds(a.row_bytes), s);
+    return hipLaunchKernel(ss_fn(a.M, a.pack5 != 0), dim3(blocks), dim3(kSsW * 64), args, ss_dyn_lds(a.row_bytes), s);
 }
 
-hipError_t sstack_blocks_per_cu(int M, int row_bytes, int* n) {
-    return hipOccupancyMaxActiveBlocksPerMultiprocessor(n, ss_fn(M), kSsW * 64, ss_dyn_lds(row_bytes));
+hipError_t sstack_blocks_per_cu(int M, bool p5, int row_bytes, int* n) {
+    return hipOccupancyMaxActiveBlocksPerMultiprocessor(n, ss_fn(M, p5), kSsW * 64, ss_dyn_lds(row_bytes));
 }
 
 int sstack_waves_per_block() { return kSsW; }
