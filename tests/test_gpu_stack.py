@@ -311,6 +311,33 @@ def test_stack_ragged_mixed_formats(M):
     run_and_compare(ops, checks, M, xtern.XT_QUANT_AVX512, reps=3)
 
 
+@pytest.mark.parametrize("M", [1, 3, 8])
+def test_stack_pack5_heavy_mixed_formats(M):
+    """A list whose bytes are mostly Pack5 (the one-launch plan then runs its
+    base-3 token forms for M <= 8) with a Pack4 and an XorSparse projection
+    running in those forms too, ragged shapes, dependencies inside the
+    launch."""
+    log(f"stack pack5-heavy mixed formats M={M}")
+    rng = np.random.default_rng(zlib.crc32(b"pack5_heavy") & 0xffff + M)
+    a = Mat(rng, 1000, 720, pack5=True)
+    b = Mat(rng, 1000, 61)
+    c = Mat(rng, 720, 1000, pack5=True)
+    d = Mat(rng, 1000, 83, sparse=True)
+    tiles = lambda K, N, cols: -(-N // 16) * -(-K // cols)
+    p5 = tiles(1000, 720, 320) + tiles(720, 1000, 320)
+    assert 2 * p5 > p5 + tiles(1000, 61, 256) + tiles(1000, 83, 256)
+    x0 = torch.from_numpy(rng.standard_normal((M, 1000)).astype(np.float32)).cuda()
+    ya = torch.full((M, 720), float("nan"), device="cuda")
+    yb = torch.full((M, 61), float("nan"), device="cuda")
+    yc = torch.full((M, 1000), float("nan"), device="cuda")
+    yd = torch.full((M, 83), float("nan"), device="cuda")
+    # (the projections of one op share a tile format)
+    ops = [([a.w], x0, [ya], None), ([b.w], x0, [yb], None), ([c.w], ya, [yc], 0), ([d.w], yc, [yd], 2)]
+    checks = [(0, ["a"], [ya], x0, {"a": a}), (1, ["b"], [yb], x0, {"b": b}), (2, ["c"], [yc], ya, {"c": c}),
+              (3, ["d"], [yd], yc, {"d": d})]
+    run_and_compare(ops, checks, M, xtern.XT_QUANT_SCALAR, reps=3)
+
+
 def test_stack_auto_plan_choice():
     """XT_STACK_AUTO: the strict 8-layer chain (32 dependency levels) runs
     per op; the residual-only list (two levels, 32 ops) in one launch; a
