@@ -1,4 +1,4 @@
-// Streaming decode stack (M = 1 .. 16 tokens): a whole list of ternary
+// Streaming decode stack (M = 1 .. 32 tokens): a whole list of ternary
 // projections in one launch, every wave walking its own sequence of tasks.
 //
 // Reference behaviour: the layer loop of the BitNet decode step
@@ -22,13 +22,14 @@
 // finishes.  Waits are bounded anyway: one that gives up sets a flag for the
 // host, and all later waits of the launch return at once.
 //
-// A group task walks its block chunk by chunk (ss_mblock): one step loads
-// the four groups' tiles of a chunk and the chunk's pieces of the op's M
-// quantised rows, stages the pieces in the wave's own LDS region (no
-// barrier: a wave's LDS accesses complete in order) and runs the four
-// groups' MFMAs on the same A fragments.  Every wave keeps its own loads in
-// flight, with no workgroup-wide phases; twelve waves per CU keep about
-// 48 KB of weights in flight.
+// A group task walks its block of R row groups chunk by chunk (ss_mblock;
+// ss_mblock_q1 at M = 1): one step loads the R groups' tiles of a chunk and
+// the chunk's pieces of the op's M quantised rows, stages the pieces in the
+// wave's own LDS region (no barrier: a wave's LDS accesses complete in
+// order) and runs the R groups' MFMAs on the same A fragments.  Every wave
+// keeps its own loads in flight, with no workgroup-wide phases: R = 8 at two
+// waves per SIMD keeps 64 KB of weights in flight per CU (the token forms
+// and their measurements are listed with the instantiations below).
 //
 // Coherence across the eight XCDs (each has its own L2): quantised rows are
 // written with device-scope stores and counted once the stores have
