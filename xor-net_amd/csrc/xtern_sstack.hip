@@ -626,7 +626,8 @@ constexpr int kSsF16R = 4, kSsF16W = 3;
 // groups at three waves per SIMD ran the 26-layer BitNet-3B Pack5 stack in
 // 194 / 194 / 199 us at M = 1 / 4 / 8 against 247 / 230 / 254 us with the
 // Pack4 forms (two groups at four waves: 218 / 225 / 226 us; three groups at
-// four waves for M = 1 and three at three above: 203 / 211 / 216 us).
+// four waves for M = 1 and three at three above: 203 / 211 / 216 us; five
+// at three: 192 / 203 / 228 us; six at three: 249 / 227 / 230 us).
 constexpr int kSsP5R = 4, kSsP5W = 3;
 int sstack_lds_rows(int M) { return M == 1 ? 1 : (M <= 4 ? 4 : (M <= 8 ? 8 : (M <= 16 ? 16 : 32))); }
 int sstack_groups_per_task(int M, bool p5) {
