@@ -610,29 +610,36 @@ static size_t ss_dyn_lds(int row_bytes) { return (size_t)kSsW * row_bytes; }
 // M = 1: eight groups per task at two waves per SIMD (183 registers) ran the
 // C4 list in 108.5 us against 114 us with four at three (and six at three:
 // 117 us); more bytes per step per wave beat more waves here.  M = 2 .. 4
-// likewise (121 independent C0 ops at M = 4: 120 against 125.6 us); the
-// 16-token form gained 1.5 % on those ops and nothing on the C4 list with
-// eight groups, so it keeps four at three waves per SIMD; an 8-token form
-// with eight groups and the next chunk's pieces in flight took the M = 8
-// C4 list from 152 to 146 us.
+// likewise (121 independent C0 ops at M = 4: 120 against 125.6 us); an
+// 8-token form with eight groups and the next chunk's pieces in flight took
+// the M = 8 C4 list from 152 to 146 us.  The 16-token form: eight groups at
+// two waves per SIMD 171.7 us on the C4 list at M = 16 against 175.5 with
+// four at three (six at two: 197.8; eight with the next chunk's pieces in
+// flight: 174.2).  The 32-token form (two 16-token MFMA blocks per tile):
+// six groups 255 us on the C4 list against 293 with four and 275 with seven
+// (eight spill registers).
 constexpr int kSsF4R = 8, kSsF4W = 2;
 constexpr int kSsF1R = 8, kSsF1W = 2;
 constexpr int kSsF8R = 8, kSsF8W = 2;
-constexpr int kSsF16R = 4, kSsF16W = 3;
-// Base-3 forms (Pack5 tiles are most of the stack's bytes), M <= 8.  A Pack5
-// tile's decode is five multiply-mask-permute rounds per dword and k-step
-// against Pack4's one permute, so the VALU work per tile is several times
-// Pack4's and more waves hide it better than more groups per wave: four
-// groups at three waves per SIMD ran the 26-layer BitNet-3B Pack5 stack in
-// 194 / 194 / 199 us at M = 1 / 4 / 8 against 247 / 230 / 254 us with the
+constexpr int kSsF16R = 8, kSsF16W = 2;
+constexpr int kSsF32R = 6, kSsF32W = 2;
+// Base-3 forms (Pack5 tiles are most of the stack's bytes), M <= 16.  A
+// Pack5 tile's decode is five multiply-mask-permute rounds per dword and
+// k-step against Pack4's one permute, so the VALU work per tile is several
+// times Pack4's and more waves hide it better than more groups per wave:
+// four groups at three waves per SIMD ran the 26-layer BitNet-3B Pack5 stack
+// in 194 / 194 / 199 us at M = 1 / 4 / 8 against 247 / 230 / 254 us with the
 // Pack4 forms (two groups at four waves: 218 / 225 / 226 us; three groups at
 // four waves for M = 1 and three at three above: 203 / 211 / 216 us; five
 // at three: 192 / 203 / 228 us; six at three: 249 / 227 / 230 us).
 constexpr int kSsP5R = 4, kSsP5W = 3;
+// (Pack5 at M = 32 keeps four groups: 408 us on that stack against 478 with
+// six)
+constexpr int kSsP32R = 4;
 int sstack_lds_rows(int M) { return M == 1 ? 1 : (M <= 4 ? 4 : (M <= 8 ? 8 : (M <= 16 ? 16 : 32))); }
 int sstack_groups_per_task(int M, bool p5) {
-    if (p5 && M <= 8) return kSsP5R;
-    return M == 1 ? kSsF1R : (M <= 4 ? kSsF4R : (M <= 8 ? kSsF8R : (M <= 16 ? kSsF16R : 4)));
+    if (p5) return M <= 16 ? kSsP5R : kSsP32R;
+    return M == 1 ? kSsF1R : (M <= 4 ? kSsF4R : (M <= 8 ? kSsF8R : (M <= 16 ? kSsF16R : kSsF32R)));
 }
 bool sstack_quant_tasks(int M) { return M > 1; }
 
@@ -640,11 +647,13 @@ static const void* ss_fn(int M, bool p5) {
     if (p5 && M == 1) return reinterpret_cast<const void*>(sstack_kernel<1, kSsP5R, kSsP5W>);
     if (p5 && M <= 4) return reinterpret_cast<const void*>(sstack_kernel<4, kSsP5R, kSsP5W>);
     if (p5 && M <= 8) return reinterpret_cast<const void*>(sstack_kernel<8, kSsP5R, kSsP5W>);
+    if (p5 && M <= 16) return reinterpret_cast<const void*>(sstack_kernel<16, kSsP5R, kSsP5W>);
+    if (p5) return reinterpret_cast<const void*>(sstack_kernel<32, kSsP32R, kSsF32W>);
     if (M == 1) return reinterpret_cast<const void*>(sstack_kernel<1, kSsF1R, kSsF1W>);
     if (M <= 4) return reinterpret_cast<const void*>(sstack_kernel<4, kSsF4R, kSsF4W>);
     if (M <= 8) return reinterpret_cast<const void*>(sstack_kernel<8, kSsF8R, kSsF8W>);
     if (M <= 16) return reinterpret_cast<const void*>(sstack_kernel<16, kSsF16R, kSsF16W>);
-    return reinterpret_cast<const void*>(sstack_kernel<32, 4, 2>);
+    return reinterpret_cast<const void*>(sstack_kernel<32, kSsF32R, kSsF32W>);
 }
 
 hipError_t launch_sstack(const SStackArgs& a, int blocks, hipStream_t s) {
