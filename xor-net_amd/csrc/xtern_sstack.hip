@@ -373,13 +373,12 @@ __device__ void ss_mblock(const SStackArgs& a, const Rec& r, uint32_t areg, unsi
             inv[t] = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (tk + M), sv));
         }
 #pragma unroll
-        for (int gi = 0; gi < R; ++gi) {
-            if (gi >= ng) break;  // (uniform)
+        for (int gi = 0; gi < R; ++gi) {  // (gi >= ng: groups past the block, predicated)
             const int row = gi * 16 + j;
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
                 const int tk = 16 * tb + 4 * g + t;
-                if (tk < M && row < trows) {
+                if (gi < ng && tk < M && row < trows) {
                     const float v = __fmul_rn(__fmul_rn((float)(acc[tb][gi][t] - rs[t]), inv[t]), wsc[gi]);
                     if (pub) ss_st_coh4(yr, (unsigned)((tk * N + row) * 4), __float_as_uint(v));
                     else ((gfloat_w*)(uintptr_t)r.y)[(size_t)tk * N + row] = v;
@@ -532,11 +531,12 @@ __device__ void ss_mblock_q1(const SStackArgs& a, const Rec& r, uint32_t areg, u
     const __amdgpu_buffer_rsrc_t yr = ss_rsrc(r.y, (unsigned)(trows * 4));
 #pragma unroll
     for (int gi = 0; gi < R; ++gi) {
-        if (gi >= ng) break;  // (uniform)
+        // (groups past the block: gi >= ng, uniform; a predicate, not a
+        // break, so that the loop unrolls and acc stays in registers)
         const int row = gi * 16 + (lane & 15);
         const int rw = min(row, trows - 1);  // (gi * 16 / 64 is uniform: the register is known)
         const float wsc = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (rw & 63), wv[(gi * 16) >> 6]));
-        if (lane < 16 && row < trows) {
+        if (gi < ng && lane < 16 && row < trows) {
             const float v = __fmul_rn(__fmul_rn((float)(acc[gi][0] - rs), invs), wsc);
             if (pub) ss_st_coh4(yr, (unsigned)(row * 4), __float_as_uint(v));
             else ((gfloat_w*)(uintptr_t)r.y)[row] = v;
@@ -617,7 +617,9 @@ static size_t ss_dyn_lds(int row_bytes) { return (size_t)kSsW * row_bytes; }
 // four at three (six at two: 197.8; eight with the next chunk's pieces in
 // flight: 174.2).  The 32-token form (two 16-token MFMA blocks per tile):
 // six groups 255 us on the C4 list against 293 with four and 275 with seven
-// (eight spill registers).
+// (eight spill registers).  Ten or twelve groups at two waves per SIMD
+// (204-253 registers): M = 1 / 8 C4 lists 127 / 168 and 136 / 159 us
+// against 112-114 / 145 with eight.
 constexpr int kSsF4R = 8, kSsF4W = 2;
 constexpr int kSsF1R = 8, kSsF1W = 2;
 constexpr int kSsF8R = 8, kSsF8W = 2;
