@@ -273,7 +273,8 @@ PACK5_3B = {"q": (3200, 3200), "k": (3200, 320), "v": (3200, 320), "o": (3200, 3
 
 
 @pytest.mark.parametrize("M,mode", [(1, xtern.XT_QUANT_AVX512), (1, xtern.XT_QUANT_SCALAR),
-                                    (8, xtern.XT_QUANT_AVX512), (16, xtern.XT_QUANT_SCALAR)])
+                                    (8, xtern.XT_QUANT_AVX512), (16, xtern.XT_QUANT_SCALAR),
+                                    (24, xtern.XT_QUANT_AVX512)])
 def test_stack_pack5_chain(M, mode):
     """Pack5 weights (BitNet-3B shapes) in one launch,
     strict chain, two layers."""
@@ -311,10 +312,10 @@ def test_stack_ragged_mixed_formats(M):
     run_and_compare(ops, checks, M, xtern.XT_QUANT_AVX512, reps=3)
 
 
-@pytest.mark.parametrize("M", [1, 3, 8])
+@pytest.mark.parametrize("M", [1, 3, 8, 13, 20, 32])
 def test_stack_pack5_heavy_mixed_formats(M):
     """A list whose bytes are mostly Pack5 (the one-launch plan then runs its
-    base-3 token forms for M <= 8) with a Pack4 and an XorSparse projection
+    base-3 token forms) with a Pack4 and an XorSparse projection
     running in those forms too, ragged shapes, dependencies inside the
     launch."""
     log(f"stack pack5-heavy mixed formats M={M}")
